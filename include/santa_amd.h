@@ -1,0 +1,139 @@
+/*
+ * santa_amd.h -- C ABI of the MI355X (gfx950) S^2ANTA sampled-attention
+ * decode library (libsanta_amd.so).
+ *
+ * Plain pointers, sizes and a hipStream_t; no torch types.  All device
+ * pointers are device memory on the current HIP device; every launch is
+ * asynchronous on `stream` and nothing here synchronizes the device or reads
+ * device memory on the host.  Inputs are never written.
+ *
+ * Reference interfaces replaced (upstream paths, with
+ *   flash/ = flash_style_fused_santa_fixed_tile_budgets/,
+ *   prop/  = santa_fused_proportional_tile_budgets/):
+ *   santa_flash_plan          <- flash/santa_cuda.cpp:36-44,188-210 (block_n, T_c, S_per_tile)
+ *   santa_flash_fused_tiles   <- launch_fused_tiles_vec_gqa_gh4_d128_bn{32,64,256}_{bf16,f16}
+ *                                flash/santa_cuda.cpp:56-96, flash/santa_cuda_kernel.cu:514-626
+ *   santa_flash_finalize      <- launch_finalize_weighted_{bf16,f16} + launch_reduce_vrows
+ *                                flash/santa_cuda.cpp:98-120, flash/santa_cuda_kernel.cu:628-681
+ *   santa_flash_decode        <- the launch sequence of decode_systematic_scalar,
+ *                                flash/santa_cuda.cpp:174-343 (minus the torch allocations)
+ *   santa_prop_plan           <- prop/santa_cuda.cpp:39-77,188-229 (block_n, T_c, pass-1 path)
+ *   santa_prop_pass1          <- launch_pass1_tiles_{vec,wmma}_gqa_{bf16,f16}
+ *                                prop/santa_cuda.cpp:81-101, prop/santa_cuda_kernel.cu:445-519
+ *   santa_prop_tile_budgets   <- launch_tile_budgets, prop/santa_cuda.cpp:108-112,
+ *                                prop/santa_cuda_kernel.cu:904-915
+ *   santa_prop_pass2          <- launch_pass2_grouped_fused_atomic_{bf16,f16} +
+ *                                launch_cast_scale_out_{bf16,f16} + launch_reduce_vrows,
+ *                                prop/santa_cuda.cpp:114-138, prop/santa_cuda_kernel.cu:917-1005
+ *   santa_prop_decode         <- the launch sequence of decode_systematic_scalar,
+ *                                prop/santa_cuda.cpp:270-352
+ *
+ * Layouts (row-major, contiguous):
+ *   q   [B, H, D]            (B = 1 for the single-request form [H, D])
+ *   K,V [B, L_storage, KVH, D]  (NHD cache; prop: [L, KVH, D])
+ *   out [B, H, D] in the input dtype, m_star [B, H] f32, vrows [B, KVH] i32.
+ */
+#ifndef SANTA_AMD_H_
+#define SANTA_AMD_H_
+
+#include <stddef.h>
+#include <stdint.h>
+#include <hip/hip_runtime_api.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Element type of q, K, V and out (the reference accepts bf16 or f16,
+ * flash/santa_cuda.cpp:128-133). */
+enum santa_dtype { SANTA_BF16 = 0, SANTA_F16 = 1 };
+
+/* Return codes.  On failure santa_last_error() holds a message whose text
+ * follows the reference's TORCH_CHECK messages where one exists. */
+enum santa_status {
+  SANTA_OK = 0,
+  SANTA_ERR_INVALID = 1,     /* bad shape / argument */
+  SANTA_ERR_UNSUPPORTED = 2, /* shape outside what the kernels implement */
+  SANTA_ERR_WORKSPACE = 3,   /* workspace too small */
+  SANTA_ERR_HIP = 4          /* a HIP launch failed */
+};
+
+/* Message of the last failure on the calling thread ("" if none). */
+const char* santa_last_error(void);
+
+/* Library version string. */
+const char* santa_version(void);
+
+/* ------------------------------------------------------------- flash */
+
+/* Host planning.  L = valid_len > 0 ? valid_len : L_storage; block_n <= 0
+ * selects 32 (L <= 1536), 64 (L <= 3072) or 256; T_c = ceil(L / block_n);
+ * S_per_tile = S > 0 ? max(1, S / T_c) : 0. */
+int santa_flash_plan(int64_t L_storage, int64_t valid_len, int64_t block_n, int64_t S, int* L_out,
+                     int* block_n_out, int* T_c_out, int* S_per_tile_out);
+
+/* One fused pass over every (b, kv, tile): scores, tile max / mass, seeded
+ * systematic counts, emission compaction and the count-weighted V sum.
+ * Outputs (device): m_tiles, ell_tiles [B,H,T_c] f32; out_tiles [B,H,T_c,D]
+ * f32; emit_cnt [B,KVH,T_c] i32 (rows emitted per tile; replaces the
+ * reference's rowmask); counts [B,H,T_c,block_n] i16 (may be NULL). */
+int santa_flash_fused_tiles(const void* q, const void* K, const void* V, int dtype, int B, int H, int KVH,
+                            int D, int L_valid, int L_storage, int block_n, int S_per_tile, uint64_t seed,
+                            float* m_tiles, float* ell_tiles, float* out_tiles, int* emit_cnt, int16_t* counts,
+                            hipStream_t stream);
+
+/* Split-KV merge across tiles: m* = max_t m_t, w_t = exp(m_t - m*) ell_t,
+ * out = (sum_t w_t out_t) / (Z S_per_tile) cast to dtype; vrows (may be
+ * NULL) = distinct sampled rows per (b, kv). */
+int santa_flash_finalize(const float* m_tiles, const float* ell_tiles, const float* out_tiles,
+                         const int* emit_cnt, int dtype, int B, int H, int KVH, int D, int T_c, int S_per_tile,
+                         void* out, float* m_star, int* vrows, hipStream_t stream);
+
+/* Bytes of device workspace santa_flash_decode needs for this shape. */
+size_t santa_flash_workspace_size(int B, int H, int KVH, int D, int T_c);
+
+/* Whole decode step: santa_flash_fused_tiles + santa_flash_finalize using the
+ * caller's workspace (>= santa_flash_workspace_size bytes, 256-B aligned). */
+int santa_flash_decode(const void* q, const void* K, const void* V, int dtype, int B, int H, int KVH, int D,
+                       int L_valid, int L_storage, int block_n, int S_per_tile, uint64_t seed, void* out,
+                       float* m_star, int* vrows, void* workspace, size_t workspace_bytes, hipStream_t stream);
+
+/* -------------------------------------------------------------- prop */
+
+/* Host planning.  block_n <= 0 selects 256 when pass1_env is "vec"/"gqa_vec",
+ * else the flash heuristic; pass1_path_out = 0 (exact vec path: GH=4, D=128,
+ * block_n=256) or 1 (general MFMA path).  pass1_env may be NULL. */
+int santa_prop_plan(int L, int H, int KVH, int D, int64_t block_n, const char* pass1_env, int* block_n_out,
+                    int* T_c_out, int* pass1_path_out);
+
+/* Pass 1 for one sequence: per-tile max / mass and the u stash [L, H]
+ * (16-bit, index n*H + h).  m_tiles, ell_tiles [H, T_c] f32. */
+int santa_prop_pass1(const void* q, const void* K, int dtype, int H, int KVH, int D, int L, int block_n,
+                     int pass1_path, float* m_tiles, float* ell_tiles, void* u_stash, hipStream_t stream);
+
+/* Largest-remainder tile budgets per head (deterministic Z order):
+ * m_star [H]; S_tiles [H,T_c] i32; invdelta, a0 [H,T_c] f32. */
+int santa_prop_tile_budgets(const float* m_tiles, const float* ell_tiles, int H, int T_c, int S, uint64_t seed,
+                            float* m_star, int* S_tiles, float* invdelta, float* a0, hipStream_t stream);
+
+/* Pass 2 + cast: counts from the stash, count-weighted V sums, a
+ * deterministic ascending-tile reduction and out = dtype(sum / S).
+ * tile_acc [H, T_c, D] f32 and emit_cnt [KVH, T_c] i32 are scratch;
+ * counts [H,T_c,block_n] i16 and vrows [KVH] may be NULL. */
+int santa_prop_pass2(const void* V, const void* u_stash, int dtype, int H, int KVH, int D, int L, int block_n,
+                     int S, const float* invdelta, const float* a0, float* tile_acc, int* emit_cnt,
+                     int16_t* counts, void* out, int* vrows, hipStream_t stream);
+
+/* Bytes of device workspace santa_prop_decode needs. */
+size_t santa_prop_workspace_size(int H, int KVH, int D, int L, int T_c);
+
+/* Whole single-sequence prop decode with the caller's workspace. */
+int santa_prop_decode(const void* q, const void* K, const void* V, int dtype, int H, int KVH, int D, int L,
+                      int block_n, int pass1_path, int S, uint64_t seed, void* out, float* m_star, int* vrows,
+                      void* workspace, size_t workspace_bytes, hipStream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* SANTA_AMD_H_ */

@@ -1,0 +1,162 @@
+// ext_flash.cpp -- the `santa_flash_batch_cuda` Python extension module for
+// PyTorch-ROCm: the drop-in for the reference's module of the same name
+// (flash/santa_cuda.cpp:174-359).  Input checks and their messages, the
+// planning and the return tuple follow the reference; the launches go
+// through the C ABI of libsanta_amd.so on the current HIP stream.
+#include <torch/extension.h>
+#include <c10/core/DeviceGuard.h>
+#include <c10/hip/HIPStream.h>
+
+#include <cstdint>
+#include <tuple>
+
+#include "santa_amd.h"
+
+namespace {
+
+struct ShapeInfo {
+  bool batched;
+  int B, H, D, L_storage, KVH;
+};
+
+// flash/santa_cuda.cpp:123-171
+ShapeInfo check_inputs_q_kv(const at::Tensor& q_h, const at::Tensor& K_g, const at::Tensor& V_g) {
+  TORCH_CHECK(q_h.is_cuda(), "q_h must be CUDA");
+  TORCH_CHECK(K_g.is_cuda() && V_g.is_cuda(), "K_g and V_g must be CUDA");
+  TORCH_CHECK((q_h.scalar_type() == at::kBFloat16 || q_h.scalar_type() == at::kHalf), "q_h must be bf16 or f16");
+  TORCH_CHECK((K_g.scalar_type() == at::kBFloat16 || K_g.scalar_type() == at::kHalf), "K_g must be bf16 or f16");
+  TORCH_CHECK(K_g.scalar_type() == V_g.scalar_type(), "K_g and V_g must have the same dtype");
+  TORCH_CHECK(q_h.scalar_type() == K_g.scalar_type(), "q_h dtype must match K_g/V_g dtype");
+  TORCH_CHECK(q_h.device() == K_g.device() && q_h.device() == V_g.device(), "device mismatch");
+  TORCH_CHECK(K_g.is_contiguous() && V_g.is_contiguous(),
+              "K_g/V_g must be contiguous. Expected [L,KVH,D] for single or [B,L,KVH,D] for batch.");
+  ShapeInfo info{};
+  if (q_h.dim() == 2) {
+    TORCH_CHECK(K_g.dim() == 3 && V_g.dim() == 3, "Single-request path expects q_h [H,D], K_g/V_g [L,KVH,D]");
+    TORCH_CHECK(K_g.size(0) == V_g.size(0) && K_g.size(1) == V_g.size(1) && K_g.size(2) == V_g.size(2),
+                "K_g and V_g must have the same shape");
+    TORCH_CHECK(q_h.size(1) == K_g.size(2), "D mismatch (q_h.size(1) vs K_g.size(2))");
+    info.batched = false;
+    info.B = 1;
+    info.H = static_cast<int>(q_h.size(0));
+    info.D = static_cast<int>(q_h.size(1));
+    info.L_storage = static_cast<int>(K_g.size(0));
+    info.KVH = static_cast<int>(K_g.size(1));
+    return info;
+  }
+  TORCH_CHECK(q_h.dim() == 3 && K_g.dim() == 4 && V_g.dim() == 4,
+              "Batched path expects q_h [B,H,D], K_g/V_g [B,L,KVH,D]");
+  TORCH_CHECK(K_g.size(0) == V_g.size(0) && K_g.size(1) == V_g.size(1) && K_g.size(2) == V_g.size(2) &&
+                  K_g.size(3) == V_g.size(3),
+              "K_g and V_g must have the same shape");
+  TORCH_CHECK(q_h.size(0) == K_g.size(0), "Batch mismatch between q_h and K_g/V_g");
+  TORCH_CHECK(q_h.size(2) == K_g.size(3), "D mismatch (q_h.size(2) vs K_g.size(3))");
+  info.batched = true;
+  info.B = static_cast<int>(q_h.size(0));
+  info.H = static_cast<int>(q_h.size(1));
+  info.D = static_cast<int>(q_h.size(2));
+  info.L_storage = static_cast<int>(K_g.size(1));
+  info.KVH = static_cast<int>(K_g.size(2));
+  return info;
+}
+
+struct Plan {
+  ShapeInfo info;
+  int L, bn, T_c, S_pt, dtype;
+};
+
+// flash/santa_cuda.cpp:182-210 (same order of checks and messages).
+Plan plan_call(const at::Tensor& q, const at::Tensor& K_g, const at::Tensor& V_g, int64_t S, int64_t block_n,
+               int64_t valid_len) {
+  Plan p{};
+  p.info = check_inputs_q_kv(q, K_g, V_g);
+  const int H = p.info.H, KVH = p.info.KVH, D = p.info.D;
+  const int L = (valid_len > 0) ? static_cast<int>(valid_len) : p.info.L_storage;
+  TORCH_CHECK(L > 0, "valid_len must be > 0; got ", L);
+  TORCH_CHECK(L <= p.info.L_storage, "valid_len exceeds storage length: valid_len=", L, " storage=",
+              p.info.L_storage);
+  TORCH_CHECK(D == 128, "This build supports only D=128. Got D=", D);
+  TORCH_CHECK(KVH > 0 && H % KVH == 0, "H must be divisible by KVH. Got H=", H, " KVH=", KVH);
+  const int GH = H / KVH;
+  TORCH_CHECK(GH == 4 || GH == 8, "This build supports only GH=4 or GH=8 (H/KVH). Got GH=", GH, " (H=", H,
+              " KVH=", KVH, ")");
+  const int rc = santa_flash_plan(p.info.L_storage, valid_len, block_n, S, &p.L, &p.bn, &p.T_c, &p.S_pt);
+  TORCH_CHECK(rc == SANTA_OK, santa_last_error());
+  p.dtype = (q.scalar_type() == at::kBFloat16) ? SANTA_BF16 : SANTA_F16;
+  TORCH_CHECK(reinterpret_cast<uintptr_t>(K_g.data_ptr()) % 8 == 0 &&
+                  reinterpret_cast<uintptr_t>(V_g.data_ptr()) % 8 == 0,
+              "K_g/V_g storage must be 8-byte aligned");
+  return p;
+}
+
+at::Tensor aligned_q(const at::Tensor& q_h) {
+  at::Tensor q = q_h.contiguous();
+  if (reinterpret_cast<uintptr_t>(q.data_ptr()) % 8 != 0) q = q.clone();
+  return q;
+}
+
+hipStream_t current_stream(const at::Tensor& t) {
+  return c10::hip::getCurrentHIPStream(t.device().index()).stream();
+}
+
+std::tuple<at::Tensor, at::Tensor, at::Tensor> decode_systematic_scalar(at::Tensor q_h, at::Tensor K_g,
+                                                                        at::Tensor V_g, int64_t S, uint64_t seed,
+                                                                        int64_t block_n, bool want_vrows,
+                                                                        int64_t valid_len) {
+  const Plan p = plan_call(q_h, K_g, V_g, S, block_n, valid_len);
+  c10::DeviceGuard guard(q_h.device());
+  const at::Tensor q = aligned_q(q_h);
+  const ShapeInfo& in = p.info;
+  auto optsF = q.options().dtype(at::kFloat);
+  auto optsI = q.options().dtype(at::kInt);
+  at::Tensor out = in.batched ? at::empty({in.B, in.H, in.D}, q.options()) : at::empty({in.H, in.D}, q.options());
+  at::Tensor m_star = in.batched ? at::empty({in.B, in.H}, optsF) : at::empty({in.H}, optsF);
+  at::Tensor vrows = at::empty({0}, optsI);
+  if (want_vrows) vrows = in.batched ? at::empty({in.B, in.KVH}, optsI) : at::empty({in.KVH}, optsI);
+  const size_t ws_bytes = santa_flash_workspace_size(in.B, in.H, in.KVH, in.D, p.T_c);
+  at::Tensor ws = at::empty({static_cast<int64_t>(ws_bytes)}, q.options().dtype(at::kByte));
+  const int rc = santa_flash_decode(q.data_ptr(), K_g.data_ptr(), V_g.data_ptr(), p.dtype, in.B, in.H, in.KVH, in.D,
+                                    p.L, in.L_storage, p.bn, p.S_pt, seed, out.data_ptr(),
+                                    m_star.data_ptr<float>(), want_vrows ? vrows.data_ptr<int>() : nullptr,
+                                    ws.data_ptr(), ws_bytes, current_stream(q));
+  TORCH_CHECK(rc == SANTA_OK, santa_last_error());
+  return std::make_tuple(out, m_star, vrows);
+}
+
+// Test-only: the per-tile statistics behind one decode call.
+// Returns (m_tiles [B,H,T_c], ell_tiles [B,H,T_c], counts [B,H,T_c,block_n] i16,
+//          out_tiles [B,H,T_c,D] f32, emit_cnt [B,KVH,T_c] i32).
+std::tuple<at::Tensor, at::Tensor, at::Tensor, at::Tensor, at::Tensor> debug_tiles(
+    at::Tensor q_h, at::Tensor K_g, at::Tensor V_g, int64_t S, uint64_t seed, int64_t block_n, int64_t valid_len) {
+  const Plan p = plan_call(q_h, K_g, V_g, S, block_n, valid_len);
+  c10::DeviceGuard guard(q_h.device());
+  const at::Tensor q = aligned_q(q_h);
+  const ShapeInfo& in = p.info;
+  auto optsF = q.options().dtype(at::kFloat);
+  at::Tensor m_tiles = at::empty({in.B, in.H, p.T_c}, optsF);
+  at::Tensor ell_tiles = at::empty({in.B, in.H, p.T_c}, optsF);
+  at::Tensor counts = at::empty({in.B, in.H, p.T_c, p.bn}, q.options().dtype(at::kShort));
+  at::Tensor out_tiles = at::empty({in.B, in.H, p.T_c, in.D}, optsF);
+  at::Tensor emit = at::empty({in.B, in.KVH, p.T_c}, q.options().dtype(at::kInt));
+  const int rc = santa_flash_fused_tiles(q.data_ptr(), K_g.data_ptr(), V_g.data_ptr(), p.dtype, in.B, in.H, in.KVH,
+                                         in.D, p.L, in.L_storage, p.bn, p.S_pt, seed, m_tiles.data_ptr<float>(),
+                                         ell_tiles.data_ptr<float>(), out_tiles.data_ptr<float>(),
+                                         emit.data_ptr<int>(), counts.data_ptr<int16_t>(), current_stream(q));
+  TORCH_CHECK(rc == SANTA_OK, santa_last_error());
+  return std::make_tuple(m_tiles, ell_tiles, counts, out_tiles, emit);
+}
+
+}  // namespace
+
+PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
+  m.doc() = "S^2ANTA-Flash sampled-attention decode for MI355X (gfx950)";
+  m.def("decode_systematic_scalar", &decode_systematic_scalar, py::arg("q_h"), py::arg("K_g"), py::arg("V_g"),
+        py::arg("S"), py::arg("seed") = 42ULL, py::arg("block_n") = 0, py::arg("want_vrows") = false,
+        py::arg("valid_len") = -1);
+  m.def("decode_systematic_batched", &decode_systematic_scalar, py::arg("q_h"), py::arg("K_g"), py::arg("V_g"),
+        py::arg("S"), py::arg("seed") = 42ULL, py::arg("block_n") = 0, py::arg("want_vrows") = false,
+        py::arg("valid_len") = -1);
+  m.def("_debug_tiles", &debug_tiles, py::arg("q_h"), py::arg("K_g"), py::arg("V_g"), py::arg("S"),
+        py::arg("seed") = 42ULL, py::arg("block_n") = 0, py::arg("valid_len") = -1);
+  m.def("_library_version", []() { return std::string(santa_version()); });
+}

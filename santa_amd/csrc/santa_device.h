@@ -1,0 +1,170 @@
+// santa_device.h -- gfx950 device numerics and wave64 primitives shared by
+// the santa_flash and santa_prop kernels.
+//
+// Every routine here is IEEE binary32 with round-to-nearest-even.  The
+// translation units are compiled with -ffp-contract=off so that a*b+c is
+// never fused unless written as fmaf(); the bit patterns the kernels produce
+// (scores, tile softmax statistics, sampled counts) therefore depend only on
+// the association order spelled out in the kernels.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace santa {
+
+// ---------------------------------------------------------------- 16-bit I/O
+// bf16 -> f32 is a 16-bit shift (flash/santa_cuda_kernel.cu:33-36); f16 -> f32
+// is the exact hardware conversion.  Both are exact.
+template <bool BF16>
+__device__ __forceinline__ float lo16_to_f32(uint32_t w) {
+  if constexpr (BF16) {
+    return __uint_as_float(w << 16);
+  } else {
+    return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(w & 0xffffu)));
+  }
+}
+template <bool BF16>
+__device__ __forceinline__ float hi16_to_f32(uint32_t w) {
+  if constexpr (BF16) {
+    return __uint_as_float(w & 0xffff0000u);
+  } else {
+    return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(w >> 16)));
+  }
+}
+template <bool BF16>
+__device__ __forceinline__ float h16_to_f32(uint16_t h) {
+  return lo16_to_f32<BF16>(static_cast<uint32_t>(h));
+}
+
+// f32 -> bf16 / f16, round to nearest even (the reference's __float2bfloat16 /
+// __float2half_rn, flash/santa_cuda_kernel.cu:53-55).
+__device__ __forceinline__ uint16_t f32_to_bf16_rne(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return static_cast<uint16_t>((u >> 16) | 0x0040u);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return static_cast<uint16_t>(u >> 16);
+}
+// f32 -> f16 in integer arithmetic.  A plain (_Float16) cast lets the
+// backend fold a preceding f32 multiply into v_fma_mixlo_f16, which rounds
+// once instead of twice; the integer form keeps the two IEEE roundings.
+__device__ __forceinline__ uint16_t f32_to_f16_rne(float f) {
+  const uint32_t x = __float_as_uint(f);
+  const uint32_t sign = (x >> 16) & 0x8000u;
+  const uint32_t ax = x & 0x7fffffffu;
+  if (ax >= 0x7f800000u) return static_cast<uint16_t>(sign | 0x7c00u | (ax > 0x7f800000u ? 0x0200u : 0u));
+  if (ax >= 0x477ff000u) return static_cast<uint16_t>(sign | 0x7c00u);  // rounds to infinity
+  if (ax < 0x38800000u) {                                                 // f16 subnormal or zero
+    const uint32_t e = ax >> 23;
+    if (e < 101u) return static_cast<uint16_t>(sign);
+    const uint32_t mant = (ax & 0x7fffffu) | 0x800000u;
+    const uint32_t shift = 126u - e;  // 14 .. 25
+    uint32_t q = mant >> shift;
+    const uint32_t rem = mant & ((1u << shift) - 1u);
+    const uint32_t half = 1u << (shift - 1u);
+    if (rem > half || (rem == half && (q & 1u))) ++q;
+    return static_cast<uint16_t>(sign | q);
+  }
+  const uint32_t r = ax + 0x0fffu + ((ax >> 13) & 1u);
+  return static_cast<uint16_t>(sign | ((r - 0x38000000u) >> 13));
+}
+template <bool BF16>
+__device__ __forceinline__ uint16_t f32_to_h16(float f) {
+  if constexpr (BF16) {
+    return f32_to_bf16_rne(f);
+  } else {
+    return f32_to_f16_rne(f);
+  }
+}
+
+// ---------------------------------------------------------------- RNG
+// SplitMix64 (Vigna) and the per-(key, tile) uniform offset of the
+// systematic sampler, flash/santa_cuda_kernel.cu:74-87.
+__device__ __forceinline__ uint64_t splitmix64(uint64_t x) {
+  x += 0x9e3779b97f4a7c15ULL;
+  uint64_t z = x;
+  z = (z ^ (z >> 30)) * 0xbf58476d1ce4e5b9ULL;
+  z = (z ^ (z >> 27)) * 0x94d049bb133111ebULL;
+  return z ^ (z >> 31);
+}
+__device__ __forceinline__ float u01(uint64_t seed, int key, int t) {
+  const uint64_t x = seed ^ ((static_cast<uint64_t>(static_cast<int64_t>(key)) << 32) ^
+                             static_cast<uint64_t>(static_cast<int64_t>(t)));
+  const uint64_t r = splitmix64(x);
+  const double u = static_cast<double>(r >> 11) * (1.0 / 9007199254740992.0);
+  return static_cast<float>(u);
+}
+
+// ---------------------------------------------------------------- EXP
+// This project's binary32 exponential: Cody-Waite reduction with ln2 split
+// hi/lo, degree-7 Taylor polynomial in Horner form with explicit fma, and
+// scaling by 2^n as two exact power-of-two multiplies (one rounding for
+// subnormal results).  exp(0) == 1 exactly; <= 2 ulp from the true value.
+__device__ __forceinline__ float santa_expf(float x) {
+  if (x != x) return x;
+  if (x > 88.72283935546875f) return __builtin_inff();
+  if (x < -103.97208404541015625f) return 0.0f;
+  const float n = __builtin_rintf(x * 1.44269502162933349609375f);
+  float r = fmaf(n, -0.693145751953125f, x);
+  r = fmaf(n, -1.428606765330187045e-06f, r);
+  float p = 1.984126984126984e-4f;
+  p = fmaf(p, r, 1.3888888888888889e-3f);
+  p = fmaf(p, r, 8.3333333333333333e-3f);
+  p = fmaf(p, r, 4.1666666666666667e-2f);
+  p = fmaf(p, r, 1.6666666666666667e-1f);
+  p = fmaf(p, r, 0.5f);
+  p = fmaf(p, r, 1.0f);
+  p = fmaf(p, r, 1.0f);
+  const int ni = static_cast<int>(n);
+  const int n1 = ni / 2;
+  const int n2 = ni - n1;
+  const float s1 = __uint_as_float(static_cast<uint32_t>(n1 + 127) << 23);
+  const float s2 = __uint_as_float(static_cast<uint32_t>(n2 + 127) << 23);
+  return (p * s1) * s2;
+}
+
+// float -> int as the reference's (int)(f_curr - f_prev) sees it for the
+// finite, small differences that occur; NaN maps to 0 (then clamped).
+__device__ __forceinline__ int count_from_floors(float a0, float pg, float cum) {
+  const float d = floorf(a0 + cum) - floorf(a0 + pg);
+  int c = (d != d) ? 0 : static_cast<int>(fminf(fmaxf(d, -2147483648.0f), 2147483520.0f));
+  c = c < 0 ? 0 : c;
+  return c > 32767 ? 32767 : c;
+}
+
+// ---------------------------------------------------------------- DPP
+// gfx9 DPP controls used by the 8-lane score tree.
+enum : int {
+  kDppQuadXor1 = 0xB1,      // quad_perm [1,0,3,2]
+  kDppQuadXor2 = 0x4E,      // quad_perm [2,3,0,1]
+  kDppRowHalfMirror = 0x141 // lane i <-> 7-i within each 8 lanes
+};
+template <int CTRL>
+__device__ __forceinline__ float dpp(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+
+// Max over the 64 lanes of a wave (exact in any order).
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int m = 32; m > 0; m >>= 1) v = fmaxf(v, __shfl_xor(v, m, 64));
+  return v;
+}
+__device__ __forceinline__ int wave_sum_int(int v) {
+#pragma unroll
+  for (int m = 32; m > 0; m >>= 1) v += __shfl_xor(v, m, 64);
+  return v;
+}
+
+// Lane 0 of the reference's 32-lane __shfl_down tree (off 16,8,4,2,1) over
+// 32 values held in registers: the classic pairwise tree.
+__device__ __forceinline__ float tree32(float* v) {
+#pragma unroll
+  for (int off = 16; off > 0; off >>= 1) {
+#pragma unroll
+    for (int l = 0; l < off; ++l) v[l] = v[l] + v[l + off];
+  }
+  return v[0];
+}
+
+}  // namespace santa

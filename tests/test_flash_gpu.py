@@ -1,0 +1,130 @@
+"""GPU parity of santa_flash against the CPU oracle (bit-exact counts/statistics).
+
+Every case prints its name, shape and seed before touching the GPU so that a
+failing run names the case.
+"""
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from helpers import SEED, bits16, gen_qkv, h16_to_f32, tol_check
+
+pytestmark = pytest.mark.gpu
+
+
+def _mod():
+    import santa_flash_batch_cuda as m
+
+    return m
+
+
+def _announce(msg):
+    print(f"\n[case] {msg}", flush=True)
+
+
+def estimator_given_counts(m_tiles, ell_tiles, counts, V, S, L):
+    """fp32 torch: y[b,h] = sum_t w_t sum_r c[b,h,t,r] v[b,t*BN+r,kv] / (Z * S_pt),
+    w_t = exp(m_t - m*) ell_t, from the tile statistics and counts."""
+    if V.dim() == 3:
+        V = V.unsqueeze(0)
+    B, H, T_c, BN = counts.shape
+    KVH = V.shape[2]
+    GH = H // KVH
+    S_pt = oracle.flash_s_per_tile(S, T_c)
+    m = m_tiles.float().cpu()
+    ell = ell_tiles.float().cpu()
+    ms = m.max(dim=2, keepdim=True).values
+    w = torch.exp(m - ms) * ell                                   # [B,H,T_c]
+    Z = w.sum(dim=2)                                              # [B,H]
+    c = counts.float().cpu().reshape(B, H, T_c * BN)[:, :, :L]    # [B,H,L]
+    Vf = V[:, :L].float().cpu()                                   # [B,L,KVH,D]
+    wr = w.repeat_interleave(BN, dim=2)[:, :, :L]                 # weight of each row's tile
+    coef = (c * wr).reshape(B, KVH, GH, L)
+    y = torch.einsum("bkgl,blkd->bkgd", coef, Vf).reshape(B, H, -1)
+    denom = (Z * S_pt).unsqueeze(-1)
+    return torch.where(denom > 0, y / denom.clamp_min(1e-30), torch.zeros_like(y))
+
+
+def _compare_tiles(res, q, K, V, S, seed, block_n=0, valid_len=-1, is_bf16=True):
+    m = _mod()
+    dev = torch.device("cuda:0")
+    qd, Kd, Vd = q.to(dev), K.to(dev), V.to(dev)
+    mt, lt, cnt, ot, ec = m._debug_tiles(qd, Kd, Vd, S, seed=seed, block_n=block_n, valid_len=valid_len)
+    out, ms, vr = m.decode_systematic_batched(qd, Kd, Vd, S, seed=seed, block_n=block_n, want_vrows=True,
+                                              valid_len=valid_len)
+    torch.cuda.synchronize()
+    single = q.dim() == 2
+    exp = oracle.flash_decode(q, K, V, S, seed=seed, block_n=block_n, valid_len=valid_len, is_bf16=is_bf16,
+                              debug=True)
+    c_gpu = cnt.cpu().numpy()
+    if single:
+        c_gpu = c_gpu[0]
+    mt_g, lt_g, ot_g = mt.cpu().numpy(), lt.cpu().numpy(), ot.cpu().numpy()
+    if single:
+        mt_g, lt_g, ot_g = mt_g[0], lt_g[0], ot_g[0]
+    # bit-exact: tile max, tile mass, sampled counts
+    np.testing.assert_array_equal(mt_g.view(np.uint32), exp["m_tiles"].view(np.uint32), err_msg="m_tiles")
+    np.testing.assert_array_equal(lt_g.view(np.uint32), exp["ell_tiles"].view(np.uint32), err_msg="ell_tiles")
+    assert np.array_equal(c_gpu, exp["counts"]), f"counts differ at {np.argwhere(c_gpu != exp['counts'])[:8]}"
+    # the partials and the merge follow the reference's association too
+    np.testing.assert_array_equal(ot_g.view(np.uint32), exp["out_tiles"].view(np.uint32), err_msg="out_tiles")
+    np.testing.assert_array_equal(bits16(out), exp["out16"], err_msg="out")
+    np.testing.assert_array_equal(ms.cpu().numpy().view(np.uint32), exp["m_star"].view(np.uint32), err_msg="m_star")
+    np.testing.assert_array_equal(vr.cpu().numpy(), exp["vrows"], err_msg="vrows")
+    ec_g = ec.cpu().numpy()
+    assert int(ec_g.sum()) == int(exp["vrows"].sum())
+    # independent torch fp32 restatement of the estimator given the GPU's counts
+    ref = estimator_given_counts(mt, lt, cnt, Vd, S, valid_len if valid_len > 0 else K.shape[-3])
+    if single:
+        ref = ref[0]
+    ref16 = ref.to(q.dtype).float().numpy()
+    ok, mabs, mrel = tol_check(h16_to_f32(bits16(out), is_bf16), ref16)
+    assert ok, (mabs, mrel)
+
+
+def test_flash_cfg1_parity():
+    _announce("flash cfg1 B=1 32q/8kv L=4096 S=32 seed=1690")
+    q, K, V = gen_qkv(1, 32, 8, 4096)
+    _compare_tiles(None, q, K, V, 32, SEED)
+
+
+@pytest.mark.parametrize(
+    "B,H,KVH,L,S,block_n,valid_len",
+    [
+        (2, 32, 8, 1000, 64, 0, -1),      # auto BN=32, ragged last tile
+        (2, 32, 8, 2000, 64, 0, -1),      # auto BN=64
+        (2, 32, 8, 5000, 256, 0, -1),     # BN=256, ragged
+        (3, 32, 8, 4096, 100, 0, 3001),   # valid_len < storage
+        (1, 32, 8, 700, 7, 256, -1),      # one ragged tile, explicit BN
+        (2, 64, 8, 3000, 512, 0, -1),     # GH=8
+        (1, 32, 8, 33, 1, 32, -1),        # T_c=2, S_pt=1
+        (2, 32, 8, 1024, 0, 0, -1),       # S=0 -> zeros
+        (1, 32, 8, 2048, 100000, 64, -1), # large S_per_tile
+    ],
+)
+def test_flash_shapes_parity(B, H, KVH, L, S, block_n, valid_len):
+    _announce(f"flash B={B} H={H} KVH={KVH} L={L} S={S} bn={block_n} valid_len={valid_len}")
+    q, K, V = gen_qkv(B, H, KVH, L, seed=SEED + B + L)
+    _compare_tiles(None, q, K, V, S, SEED, block_n=block_n, valid_len=valid_len)
+
+
+def test_flash_single_request_and_f16():
+    _announce("flash single-request [H,D] bf16 and f16 L=3000")
+    q, K, V = gen_qkv(1, 32, 8, 3000, single=True)
+    _compare_tiles(None, q, K, V, 48, 7)
+    q16, K16, V16 = gen_qkv(2, 32, 8, 1500, dtype=torch.float16)
+    _compare_tiles(None, q16, K16, V16, 40, 9, is_bf16=False)
+
+
+def test_flash_uniform_tile_kat():
+    """q = 0: every tile is uniform; seed 1690, b=h=t=0 samples rows 75 and 203."""
+    _announce("flash uniform-tile KAT L=4096 S=32")
+    _, K, V = gen_qkv(1, 32, 8, 4096)
+    q = torch.zeros(1, 32, 128, dtype=torch.bfloat16)
+    m = _mod()
+    dev = torch.device("cuda:0")
+    _, lt, cnt, _, _ = m._debug_tiles(q.to(dev), K.to(dev), V.to(dev), 32, seed=1690)
+    c = cnt[0, 0, 0].cpu().numpy()
+    assert list(np.nonzero(c)[0]) == [75, 203]
+    assert float(lt[0, 0, 0]) == 256.0
