@@ -16,7 +16,7 @@
  *   santa_flash_finalize      <- launch_finalize_weighted_{bf16,f16} + launch_reduce_vrows
  *                                flash/santa_cuda.cpp:98-120, flash/santa_cuda_kernel.cu:628-681
  *   santa_flash_decode        <- the launch sequence of decode_systematic_scalar,
- *                                flash/santa_cuda.cpp:174-343 (minus the torch allocations)
+ *   (+ _decode_tiles/_merge)     flash/santa_cuda.cpp:174-343 (minus the torch allocations)
  *   santa_prop_plan           <- prop/santa_cuda.cpp:39-77,188-229 (block_n, T_c, pass-1 path)
  *   santa_prop_pass1          <- launch_pass1_tiles_{vec,wmma}_gqa_{bf16,f16}
  *                                prop/santa_cuda.cpp:81-101, prop/santa_cuda_kernel.cu:445-519
@@ -89,14 +89,28 @@ int santa_flash_finalize(const float* m_tiles, const float* ell_tiles, const flo
                          const int* emit_cnt, int dtype, int B, int H, int KVH, int D, int T_c, int S_per_tile,
                          void* out, float* m_star, int* vrows, hipStream_t stream);
 
-/* Bytes of device workspace santa_flash_decode needs for this shape. */
+/* Bytes of device workspace santa_flash_decode needs for this shape on the
+ * current device (it depends on the device's compute-unit count). */
 size_t santa_flash_workspace_size(int B, int H, int KVH, int D, int T_c);
 
-/* Whole decode step: santa_flash_fused_tiles + santa_flash_finalize using the
- * caller's workspace (>= santa_flash_workspace_size bytes, 256-B aligned). */
+/* Whole decode step (the production path).  Same results as
+ * santa_flash_fused_tiles + santa_flash_finalize for m_star, vrows and every
+ * sampled count; the output sum is merged per chunk of tiles with a running
+ * max, so `out` agrees with the reference-order merge to rounding.
+ * workspace >= santa_flash_workspace_size bytes, 256-B aligned; its contents
+ * need no initialization. */
 int santa_flash_decode(const void* q, const void* K, const void* V, int dtype, int B, int H, int KVH, int D,
                        int L_valid, int L_storage, int block_n, int S_per_tile, uint64_t seed, void* out,
                        float* m_star, int* vrows, void* workspace, size_t workspace_bytes, hipStream_t stream);
+
+/* The two launches of santa_flash_decode, for callers that schedule them
+ * separately: the tile pass writes chunk partials into the workspace, the
+ * merge pass reads them. */
+int santa_flash_decode_tiles(const void* q, const void* K, const void* V, int dtype, int B, int H, int KVH, int D,
+                             int L_valid, int L_storage, int block_n, int S_per_tile, uint64_t seed, void* workspace,
+                             size_t workspace_bytes, hipStream_t stream);
+int santa_flash_decode_merge(const void* workspace, size_t workspace_bytes, int dtype, int B, int H, int KVH, int D,
+                             int T_c, int S_per_tile, void* out, float* m_star, int* vrows, hipStream_t stream);
 
 /* -------------------------------------------------------------- prop */
 

@@ -83,9 +83,9 @@ Plan plan_call(const at::Tensor& q, const at::Tensor& K_g, const at::Tensor& V_g
   const int rc = santa_flash_plan(p.info.L_storage, valid_len, block_n, S, &p.L, &p.bn, &p.T_c, &p.S_pt);
   TORCH_CHECK(rc == SANTA_OK, santa_last_error());
   p.dtype = (q.scalar_type() == at::kBFloat16) ? SANTA_BF16 : SANTA_F16;
-  TORCH_CHECK(reinterpret_cast<uintptr_t>(K_g.data_ptr()) % 8 == 0 &&
-                  reinterpret_cast<uintptr_t>(V_g.data_ptr()) % 8 == 0,
-              "K_g/V_g storage must be 8-byte aligned");
+  TORCH_CHECK(reinterpret_cast<uintptr_t>(K_g.data_ptr()) % 16 == 0 &&
+                  reinterpret_cast<uintptr_t>(V_g.data_ptr()) % 16 == 0,
+              "K_g/V_g storage must be 16-byte aligned");
   return p;
 }
 
@@ -146,6 +146,60 @@ std::tuple<at::Tensor, at::Tensor, at::Tensor, at::Tensor, at::Tensor> debug_til
   return std::make_tuple(m_tiles, ell_tiles, counts, out_tiles, emit);
 }
 
+// Test-only: the reference-structured launch pair (per-tile partials, then
+// the finalize with the reference's merge association).  Returns the same
+// tuple as decode_systematic_scalar.
+std::tuple<at::Tensor, at::Tensor, at::Tensor> decode_reference_order(at::Tensor q_h, at::Tensor K_g, at::Tensor V_g,
+                                                                      int64_t S, uint64_t seed, int64_t block_n,
+                                                                      bool want_vrows, int64_t valid_len) {
+  const Plan p = plan_call(q_h, K_g, V_g, S, block_n, valid_len);
+  c10::DeviceGuard guard(q_h.device());
+  const at::Tensor q = aligned_q(q_h);
+  const ShapeInfo& in = p.info;
+  auto optsF = q.options().dtype(at::kFloat);
+  auto optsI = q.options().dtype(at::kInt);
+  at::Tensor m_tiles = at::empty({in.B, in.H, p.T_c}, optsF);
+  at::Tensor ell_tiles = at::empty({in.B, in.H, p.T_c}, optsF);
+  at::Tensor out_tiles = at::empty({in.B, in.H, p.T_c, in.D}, optsF);
+  at::Tensor emit = at::empty({in.B, in.KVH, p.T_c}, optsI);
+  hipStream_t st = current_stream(q);
+  int rc = santa_flash_fused_tiles(q.data_ptr(), K_g.data_ptr(), V_g.data_ptr(), p.dtype, in.B, in.H, in.KVH, in.D, p.L,
+                                   in.L_storage, p.bn, p.S_pt, seed, m_tiles.data_ptr<float>(),
+                                   ell_tiles.data_ptr<float>(), out_tiles.data_ptr<float>(), emit.data_ptr<int>(),
+                                   nullptr, st);
+  TORCH_CHECK(rc == SANTA_OK, santa_last_error());
+  at::Tensor out = in.batched ? at::empty({in.B, in.H, in.D}, q.options()) : at::empty({in.H, in.D}, q.options());
+  at::Tensor m_star = in.batched ? at::empty({in.B, in.H}, optsF) : at::empty({in.H}, optsF);
+  at::Tensor vrows = at::empty({0}, optsI);
+  if (want_vrows) vrows = in.batched ? at::empty({in.B, in.KVH}, optsI) : at::empty({in.KVH}, optsI);
+  rc = santa_flash_finalize(m_tiles.data_ptr<float>(), ell_tiles.data_ptr<float>(), out_tiles.data_ptr<float>(),
+                            emit.data_ptr<int>(), p.dtype, in.B, in.H, in.KVH, in.D, p.T_c, p.S_pt, out.data_ptr(),
+                            m_star.data_ptr<float>(), want_vrows ? vrows.data_ptr<int>() : nullptr, st);
+  TORCH_CHECK(rc == SANTA_OK, santa_last_error());
+  return std::make_tuple(out, m_star, vrows);
+}
+
+// Bench-only: the production tile pass alone (chunk partials into `ws`,
+// a uint8 tensor of at least santa_flash_workspace_size bytes).
+void decode_tiles_only(at::Tensor q_h, at::Tensor K_g, at::Tensor V_g, int64_t S, uint64_t seed, int64_t block_n,
+                       int64_t valid_len, at::Tensor ws) {
+  const Plan p = plan_call(q_h, K_g, V_g, S, block_n, valid_len);
+  c10::DeviceGuard guard(q_h.device());
+  const at::Tensor q = aligned_q(q_h);
+  const ShapeInfo& in = p.info;
+  TORCH_CHECK(ws.is_cuda() && ws.scalar_type() == at::kByte && ws.is_contiguous(), "ws must be a CUDA uint8 tensor");
+  const int rc = santa_flash_decode_tiles(q.data_ptr(), K_g.data_ptr(), V_g.data_ptr(), p.dtype, in.B, in.H, in.KVH,
+                                          in.D, p.L, in.L_storage, p.bn, p.S_pt, seed, ws.data_ptr(),
+                                          static_cast<size_t>(ws.numel()), current_stream(q));
+  TORCH_CHECK(rc == SANTA_OK, santa_last_error());
+}
+
+int64_t workspace_bytes(int64_t B, int64_t H, int64_t KVH, int64_t D, int64_t T_c) {
+  return static_cast<int64_t>(santa_flash_workspace_size(static_cast<int>(B), static_cast<int>(H),
+                                                         static_cast<int>(KVH), static_cast<int>(D),
+                                                         static_cast<int>(T_c)));
+}
+
 }  // namespace
 
 PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
@@ -158,5 +212,11 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
         py::arg("valid_len") = -1);
   m.def("_debug_tiles", &debug_tiles, py::arg("q_h"), py::arg("K_g"), py::arg("V_g"), py::arg("S"),
         py::arg("seed") = 42ULL, py::arg("block_n") = 0, py::arg("valid_len") = -1);
+  m.def("_decode_reference_order", &decode_reference_order, py::arg("q_h"), py::arg("K_g"), py::arg("V_g"),
+        py::arg("S"), py::arg("seed") = 42ULL, py::arg("block_n") = 0, py::arg("want_vrows") = false,
+        py::arg("valid_len") = -1);
+  m.def("_decode_tiles_only", &decode_tiles_only, py::arg("q_h"), py::arg("K_g"), py::arg("V_g"), py::arg("S"),
+        py::arg("seed"), py::arg("block_n"), py::arg("valid_len"), py::arg("ws"));
+  m.def("_workspace_bytes", &workspace_bytes);
   m.def("_library_version", []() { return std::string(santa_version()); });
 }

@@ -101,11 +101,11 @@ __device__ __forceinline__ float u01(uint64_t seed, int key, int t) {
 // scaling by 2^n as two exact power-of-two multiplies (one rounding for
 // subnormal results).  exp(0) == 1 exactly; <= 2 ulp from the true value.
 __device__ __forceinline__ float santa_expf(float x) {
-  if (x != x) return x;
-  if (x > 88.72283935546875f) return __builtin_inff();
-  if (x < -103.97208404541015625f) return 0.0f;
-  const float n = __builtin_rintf(x * 1.44269502162933349609375f);
-  float r = fmaf(n, -0.693145751953125f, x);
+  // Evaluated on the clamped argument and patched by selects (no branches);
+  // in range the arithmetic is exactly that of the plain formula.
+  const float xc = fminf(fmaxf(x, -103.97208404541015625f), 88.72283935546875f);
+  const float n = __builtin_rintf(xc * 1.44269502162933349609375f);
+  float r = fmaf(n, -0.693145751953125f, xc);
   r = fmaf(n, -1.428606765330187045e-06f, r);
   float p = 1.984126984126984e-4f;
   p = fmaf(p, r, 1.3888888888888889e-3f);
@@ -120,7 +120,10 @@ __device__ __forceinline__ float santa_expf(float x) {
   const int n2 = ni - n1;
   const float s1 = __uint_as_float(static_cast<uint32_t>(n1 + 127) << 23);
   const float s2 = __uint_as_float(static_cast<uint32_t>(n2 + 127) << 23);
-  return (p * s1) * s2;
+  float res = (p * s1) * s2;
+  res = (x > 88.72283935546875f) ? __builtin_inff() : res;
+  res = (x < -103.97208404541015625f) ? 0.0f : res;
+  return (x != x) ? x : res;
 }
 
 // float -> int as the reference's (int)(f_curr - f_prev) sees it for the
@@ -137,11 +140,32 @@ __device__ __forceinline__ int count_from_floors(float a0, float pg, float cum) 
 enum : int {
   kDppQuadXor1 = 0xB1,      // quad_perm [1,0,3,2]
   kDppQuadXor2 = 0x4E,      // quad_perm [2,3,0,1]
-  kDppRowHalfMirror = 0x141 // lane i <-> 7-i within each 8 lanes
+  kDppRowHalfMirror = 0x141, // lane i <-> 7-i within each 8 lanes
+  kDppRowMirror = 0x140      // lane i <-> 15-i within each 16 lanes
 };
 template <int CTRL>
 __device__ __forceinline__ float dpp(float v) {
   return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+
+// v from lane (i - N) of the same 16-lane row, 0 where that lane is outside it.
+template <int N>
+__device__ __forceinline__ float dpp_shr_zero(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x110 + N, 0xF, 0xF, true));
+}
+
+// Max over the 64 lanes of a wave (exact in any order): DPP inside each
+// 16-lane row, then the four row maxima.
+__device__ __forceinline__ float wave_max_dpp(float v) {
+  v = fmaxf(v, dpp<kDppQuadXor1>(v));
+  v = fmaxf(v, dpp<kDppQuadXor2>(v));
+  v = fmaxf(v, dpp<kDppRowHalfMirror>(v));
+  v = fmaxf(v, dpp<kDppRowMirror>(v));
+  const float m0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));
+  const float m1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 16));
+  const float m2 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32));
+  const float m3 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 48));
+  return fmaxf(fmaxf(m0, m1), fmaxf(m2, m3));
 }
 
 // Max over the 64 lanes of a wave (exact in any order).

@@ -1,30 +1,44 @@
 // santa_flash.hip -- santa_flash (fixed tile budget) decode kernels for gfx950.
 //
-// Work item = one KV tile (block_n consecutive tokens) of one (b, kv) group.
-// A 256-thread workgroup (4 wave64) handles one item:
+// Decomposition.  A KV tile is block_n consecutive tokens of one (b, kv)
+// group.  The tiles of a group are split into contiguous chunks, one chunk
+// per 256-thread workgroup (4 wave64), sized so that the grid is about one
+// resident round on the device.  A workgroup walks its chunk tile by tile and
+// prefetches the next tile's K rows (non-temporal loads) before it runs the
+// current tile's softmax statistics, sampler and V gather, so the HBM stream
+// never waits for that serial tail.
 //
-//  A  scores   Each K row (128 x 16-bit = 256 B) is read by 8 lanes, lane p
-//              holding the reference's virtual lanes {sigma(p) + 8 i}, i < 4
-//              (4 dims each).  The first two levels of the reference's
-//              32-lane score tree are in-lane adds; the last three are DPP
-//              (row_half_mirror, quad xor2, quad xor1).  sigma = [0,1,2,3,7,6,
-//              5,4] makes row_half_mirror pair virtual lanes l and l+4, so the
-//              pairing -- and therefore every score bit -- equals the
-//              reference's (flash/santa_cuda_kernel.cu:183-211).  All GH query
-//              heads of the group reuse the row from registers; q lives in
-//              VGPRs for the whole tile.
-//  B  tile max per head (exact in any order).
-//  C  u = exp(s - m), the 16-bit u, and ell with the reference's
-//     per-thread / 32-lane-tree / per-warp association (:243-273).
-//  D  systematic counts: 32-row Hillis-Steele scans per head run in
-//     parallel; the cross-chunk carries are the reference's sequential
-//     float sums (:275-311).
-//  E  emission compaction by wave ballots, ascending rows (:314-345).
-//  F  count-weighted V sum over the emitted rows, one head per wave,
-//     fma per element in ascending row order (:347-379).
+// Per tile:
+//  A  scores.  Lane i of wave w owns K row 64w+i.  The wave stages its 64
+//     rows in LDS (coalesced non-temporal 16-B loads, 16 lanes per row,
+//     XOR-swizzled 16-B slots) and reads back its own row.  The reference's
+//     per-virtual-lane fma chains (4 dims each) run on the matrix pipe as
+//     v_mfma_f32_4x4x1f32 with the A operand broadcast (CBSZ=4, ABID=dim%16):
+//     q for 16 dims x 4 heads sits in one VGPR (lane 4j+i: head i, dim 16m+j),
+//     k of the lane's own row is the B operand, and each lane accumulates its
+//     row's 4 heads in place.  A K=1 MFMA is one fused multiply-add with a
+//     single rounding, bit-identical to fmaf (checked by a GPU test).  The
+//     reference's 32-lane tree (flash/santa_cuda_kernel.cu:183-211) becomes
+//     in-register adds over the virtual lanes in the same pairing.
+//  B  tile max per head: wave maxima, one LDS exchange (exact in any order).
+//  C  u = exp(s - m), the 16-bit u and ell with the reference's per-thread /
+//     32-lane-tree / per-warp association (:243-273), the 32-lane trees as
+//     in-wave butterflies.
+//  D  systematic counts (:275-311): each wave owns one head (two for GH=8)
+//     and scans its 256 rows as 64-row blocks of two 32-lane Hillis-Steele
+//     chunks; the reference's sequential cross-chunk carries are wave-uniform
+//     scalars, so no workgroup barrier is needed.
+//  E  the head's sampled rows are the set bits of the blocks' ballots, in
+//     ascending order: the reference's emission list with zero counts
+//     skipped (:314-379) -- so the count-weighted V sum reads the rows
+//     straight from the masks, fma per element in ascending row order.
+//  Two workgroup barriers per tile.
 //
-// A second kernel merges the tiles of each (b, h) (split-KV reduction,
-// :386-470) with the same association as the reference's finalize.
+// Outputs.  Mode kOnline merges the chunk's tiles on the fly (running max
+// and rescaled mass / numerator per head) into a chunk partial; a small
+// kernel merges the chunk partials of each (b, h).  Mode kPerTile writes the
+// reference's per-tile m, ell and count-weighted sums (plus, on request, the
+// counts) and finalize_kernel merges them with the reference's association.
 #include "santa_device.h"
 #include "santa_amd.h"
 #include "santa_internal.h"
@@ -34,249 +48,500 @@ namespace flash {
 
 constexpr int kD = 128;
 constexpr int kThreads = 256;
+constexpr int kPartStride = kD + 2;  // chunk partial: M, Z, num[128]
+constexpr int kListCap = 128;        // sampled rows buffered per head before a gather (>= 2 x 64)
+enum Mode : int { kPerTile = 0, kOnline = 1 };
 
-template <bool BF16, int GH, int BN>
-__global__ __launch_bounds__(kThreads, 2) void fused_tile_kernel(
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+// K=1 MFMA with the A operand of block J broadcast to all 16 blocks:
+// d[i] at lane l = a(lane 4J+i) * b(lane l) + c[i], one rounding per element.
+template <int J>
+__device__ __forceinline__ f32x4 mfma_bcast(float a, float b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_4x4x1f32(a, b, c, 4, J, 0);
+}
+
+// The fma chains of virtual lanes 2C (dims 8C..8C+3) and 2C+1 (8C+4..8C+7)
+// for this lane's K row (chunk C of its LDS slot) and every head block.
+template <bool BF16, int NHB, int C>
+__device__ __forceinline__ void score_chunk(const u32x4* wk, int row, const float (&qa)[NHB][8], f32x4 (&pe)[NHB],
+                                            f32x4 (&po)[NHB]) {
+  const u32x4 kc = wk[row * 16 + (C ^ (row & 15))];
+  const float k0 = lo16_to_f32<BF16>(kc.x), k1 = hi16_to_f32<BF16>(kc.x);
+  const float k2 = lo16_to_f32<BF16>(kc.y), k3 = hi16_to_f32<BF16>(kc.y);
+  const float k4 = lo16_to_f32<BF16>(kc.z), k5 = hi16_to_f32<BF16>(kc.z);
+  const float k6 = lo16_to_f32<BF16>(kc.w), k7 = hi16_to_f32<BF16>(kc.w);
+  constexpr int M = C / 2;          // q register: dims 16M .. 16M+15
+  constexpr int J = 8 * (C % 2);    // block of dim 8C inside it
+  const f32x4 z = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+  for (int hb = 0; hb < NHB; ++hb) {
+    const float qv = qa[hb][M];
+    f32x4 de = mfma_bcast<J + 0>(qv, k0, z);
+    f32x4 dd = mfma_bcast<J + 4>(qv, k4, z);
+    de = mfma_bcast<J + 1>(qv, k1, de);
+    dd = mfma_bcast<J + 5>(qv, k5, dd);
+    de = mfma_bcast<J + 2>(qv, k2, de);
+    dd = mfma_bcast<J + 6>(qv, k6, dd);
+    de = mfma_bcast<J + 3>(qv, k3, de);
+    dd = mfma_bcast<J + 7>(qv, k7, dd);
+    pe[hb] = de;
+    po[hb] = dd;
+  }
+}
+
+// B(C) of the reference tree for even and odd virtual lanes: chunks C, C+8
+// (level off16), C+4, C+12 (level off8); four independent chunks so eight
+// MFMA chains overlap.
+template <bool BF16, int NHB, int C>
+__device__ __forceinline__ void score_group(const u32x4* wk, int row, const float (&qa)[NHB][8], f32x4 (&be)[NHB],
+                                            f32x4 (&bo)[NHB]) {
+  f32x4 e0[NHB], o0[NHB], e8[NHB], o8[NHB], e4[NHB], o4[NHB], e12[NHB], o12[NHB];
+  score_chunk<BF16, NHB, C>(wk, row, qa, e0, o0);
+  score_chunk<BF16, NHB, C + 8>(wk, row, qa, e8, o8);
+  score_chunk<BF16, NHB, C + 4>(wk, row, qa, e4, o4);
+  score_chunk<BF16, NHB, C + 12>(wk, row, qa, e12, o12);
+#pragma unroll
+  for (int hb = 0; hb < NHB; ++hb) {
+    be[hb] = (e0[hb] + e8[hb]) + (e4[hb] + e12[hb]);
+    bo[hb] = (o0[hb] + o8[hb]) + (o4[hb] + o12[hb]);
+  }
+}
+
+// Number of rows of a tile sampled by any head of the group: the union of
+// the per-head nonzero-count masks (one 64-row block per lane < NBLK).
+template <int GH, int NBLK>
+__device__ __forceinline__ int union_rows(const uint64_t* s_mask, int lane) {
+  int e = 0;
+  if (lane < NBLK) {
+    uint64_t u = 0;
+#pragma unroll
+    for (int g = 0; g < GH; ++g) u |= s_mask[g * NBLK + lane];
+    e = __popcll(u);
+  }
+#pragma unroll
+  for (int m = 1; m < NBLK; m <<= 1) e += __shfl_xor(e, m, 64);
+  return e;
+}
+
+template <bool BF16, int GH, int BN, int MODE>
+__global__ __launch_bounds__(kThreads, 2) void tile_kernel(
     const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K, const uint16_t* __restrict__ V, int H, int KVH,
-    int L_valid, int L_storage, int T_c, float q_scale, int S_pt, uint64_t seed, float* __restrict__ m_tiles,
-    float* __restrict__ ell_tiles, float* __restrict__ out_tiles, int* __restrict__ emit_cnt,
-    int16_t* __restrict__ dbg_counts) {
+    int L_valid, int L_storage, int T_c, int cs, int cpg, float q_scale, int S_pt, uint64_t seed,
+    float* __restrict__ m_tiles, float* __restrict__ ell_tiles, float* __restrict__ out_tiles,
+    int* __restrict__ emit_cnt, int16_t* __restrict__ dbg_counts, float* __restrict__ part,
+    int* __restrict__ part_emit) {
   static_assert(BN == 32 || BN == 64 || BN == 256, "block_n");
   static_assert(GH == 4 || GH == 8, "group size");
   constexpr int NT_REF = (BN == 256) ? 256 : 128;  // reference block size (launchers :521,:559)
   constexpr int NW_REF = NT_REF / 32;
-  constexpr int ITERS = BN / 32;                   // 32 rows per workgroup iteration
-  constexpr int CHUNKS = BN / 32;
+  constexpr int HPW = GH / 4;                      // heads per wave in phases D-E
+  constexpr int NCH = BN / 32;                     // 32-row scan chunks
+  constexpr int NPAIR = (NCH + 3) / 4;             // two-rows-per-lane scan registers
+  constexpr int KC = BN * GH / NT_REF;             // (row, head) items per reference thread
+  constexpr int LCAP = (MODE == kOnline) ? kListCap : BN;  // sampled rows buffered per head
 
-  // Linear item id with kv fastest: the 8 KV heads of one token range are
-  // read by consecutive workgroups, so each 2 KB NHD token row is streamed
-  // by neighbours at about the same time.
-  const int id = static_cast<int>(blockIdx.x);
-  const int kv = id % KVH;
-  const int t = (id / KVH) % T_c;
-  const int b = id / (KVH * T_c);
+  const int wg = static_cast<int>(blockIdx.x);
+  const int bk = wg / cpg;  // b * KVH + kv
+  const int chunk = wg - bk * cpg;
+  const int kv = bk % KVH;
+  const int b = bk / KVH;
   const int h0 = kv * GH;
-  const int n0 = t * BN;
-  const int len = min(BN, L_valid - n0);
+  const int t_begin = chunk * cs;
+  const int t_end = min(T_c, t_begin + cs);
 
   const int tid = static_cast<int>(threadIdx.x);
   const int lane = tid & 63;
   const int wave = tid >> 6;
-  const int p = lane & 7;
-  const int grp = lane >> 3;
-  const int sig = (p < 4) ? p : (11 - p);
 
-  __shared__ float s_sc[BN * GH];
-  __shared__ uint16_t s_ub[BN * GH];
-  __shared__ int16_t s_cnt[GH * BN];
-  __shared__ int16_t s_emit[BN];
-  __shared__ float s_acc[NT_REF];
+  __shared__ float s_sc[BN * GH];          // scores, [row][head]
+  __shared__ uint16_t s_ub[GH * BN];       // 16-bit u, [head][row]
+  __shared__ float s_wmax[4 * GH];
   __shared__ float s_W[NW_REF * GH];
-  __shared__ float s_m[GH], s_invdel[GH], s_a0[GH];
-  __shared__ float s_T[GH * CHUNKS];
-  __shared__ int s_wcnt[4];
+  __shared__ uint64_t s_mask[GH * NPAIR * 2];
 
   const size_t row_stride = static_cast<size_t>(KVH) * kD;
+  const uint16_t* Kg = K + static_cast<size_t>(b) * L_storage * row_stride + static_cast<size_t>(kv) * kD;
+  const uint16_t* Vg = V + static_cast<size_t>(b) * L_storage * row_stride + static_cast<size_t>(kv) * kD + 2 * lane;
 
-  // ---- q for this lane's 16 dims of every head, scaled once (A.1) --------
-  float qf[GH][4][4];
+  // Online-merge state: per head owned by this wave, running max M, mass Z
+  // and this lane's two numerator dims.
+  float runM[HPW], runZ[HPW], num0[HPW], num1[HPW];
 #pragma unroll
-  for (int g = 0; g < GH; ++g) {
-    const uint16_t* qp = Q + (static_cast<size_t>(b) * H + h0 + g) * kD + 4 * sig;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const uint2 w = *reinterpret_cast<const uint2*>(qp + 32 * i);
-      qf[g][i][0] = lo16_to_f32<BF16>(w.x) * q_scale;
-      qf[g][i][1] = hi16_to_f32<BF16>(w.x) * q_scale;
-      qf[g][i][2] = lo16_to_f32<BF16>(w.y) * q_scale;
-      qf[g][i][3] = hi16_to_f32<BF16>(w.y) * q_scale;
-    }
+  for (int k = 0; k < HPW; ++k) {
+    runM[k] = -__builtin_inff();
+    runZ[k] = 0.0f;
+    num0[k] = 0.0f;
+    num1[k] = 0.0f;
   }
+  int emit_total = 0;
 
-  // ---- A: scores ----------------------------------------------------------
-  const uint16_t* Kt = K + (static_cast<size_t>(b) * L_storage + n0) * row_stride +
-                       static_cast<size_t>(kv) * kD + 4 * sig;
-  uint2 kw[ITERS][4];
+  if (t_begin >= t_end) {
+    if constexpr (MODE == kOnline) {
 #pragma unroll
-  for (int it = 0; it < ITERS; ++it) {
-    const int r = it * 32 + wave * 8 + grp;
-    const int rr = min(r, len - 1);
-    const uint16_t* kp = Kt + static_cast<size_t>(rr) * row_stride;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) kw[it][i] = *reinterpret_cast<const uint2*>(kp + 32 * i);
-  }
-#pragma unroll
-  for (int it = 0; it < ITERS; ++it) {
-    const int r = it * 32 + wave * 8 + grp;
-    float k[4][4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      k[i][0] = lo16_to_f32<BF16>(kw[it][i].x);
-      k[i][1] = hi16_to_f32<BF16>(kw[it][i].x);
-      k[i][2] = lo16_to_f32<BF16>(kw[it][i].y);
-      k[i][3] = hi16_to_f32<BF16>(kw[it][i].y);
-    }
-    float s[GH];
-#pragma unroll
-    for (int g = 0; g < GH; ++g) {
-      float pp[4];
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        float a = fmaf(qf[g][i][0], k[i][0], 0.0f);
-        a = fmaf(qf[g][i][1], k[i][1], a);
-        a = fmaf(qf[g][i][2], k[i][2], a);
-        a = fmaf(qf[g][i][3], k[i][3], a);
-        pp[i] = a;
+      for (int k = 0; k < HPW; ++k) {
+        float* pp = part + (static_cast<size_t>(wg) * GH + wave + 4 * k) * kPartStride;
+        if (lane == 0) {
+          pp[0] = -__builtin_inff();
+          pp[1] = 0.0f;
+        }
+        pp[2 + 2 * lane] = 0.0f;
+        pp[3 + 2 * lane] = 0.0f;
       }
-      const float a0 = pp[0] + pp[2];  // virtual lanes l, l+16
-      const float a1 = pp[1] + pp[3];  // l+8, l+24
-      const float bb = a0 + a1;        // l, l+8
-      const float c = bb + dpp<kDppRowHalfMirror>(bb);  // l, l+4
-      const float d = c + dpp<kDppQuadXor2>(c);         // l, l+2
-      s[g] = d + dpp<kDppQuadXor1>(d);                  // l, l+1
+      if (tid == 0) part_emit[wg] = 0;
     }
-    if (p == 0 && r < len) {
-#pragma unroll
-      for (int g = 0; g < GH; ++g) s_sc[r * GH + g] = s[g];
-    }
-  }
-  __syncthreads();
-
-  // ---- B: tile max per head (A.3) ------------------------------------------
-#pragma unroll
-  for (int g = wave; g < GH; g += 4) {
-    float mx = -__builtin_inff();
-    for (int r = lane; r < len; r += 64) mx = fmaxf(mx, s_sc[r * GH + g]);
-    mx = wave_max(mx);
-    if (lane == 0) s_m[g] = mx;
-  }
-  __syncthreads();
-
-  // ---- C: u, 16-bit u and ell (A.4) ---------------------------------------
-  if (tid < NT_REF) {
-    const int g = tid % GH;
-    const float mg = s_m[g];
-    float acc = 0.0f;
-    for (int idx = tid; idx < len * GH; idx += NT_REF) {
-      const float u = santa_expf(s_sc[idx] - mg);
-      acc += u;
-      s_ub[idx] = f32_to_h16<BF16>(u);
-    }
-    s_acc[tid] = acc;
-  }
-  __syncthreads();
-  if (tid < NW_REF * GH) {
-    const int w = tid / GH;
-    const int g = tid % GH;
-    float v[32];
-#pragma unroll
-    for (int l = 0; l < 32; ++l) v[l] = ((l % GH) == g) ? s_acc[w * 32 + l] : 0.0f;
-    s_W[w * GH + g] = tree32(v);
-  }
-  __syncthreads();
-  if (tid < GH) {
-    float ell = 0.0f;
-#pragma unroll
-    for (int w = 0; w < NW_REF; ++w) ell += s_W[w * GH + tid];
-    const float invdel = (S_pt > 0 && ell > 1e-20f) ? (static_cast<float>(S_pt) / ell) : 0.0f;
-    s_invdel[tid] = invdel;
-    s_a0[tid] = u01(seed, b * H + h0 + tid, t);
-    const size_t mt = (static_cast<size_t>(b) * H + h0 + tid) * T_c + t;
-    m_tiles[mt] = s_m[tid];
-    ell_tiles[mt] = ell;
-  }
-  __syncthreads();
-
-  // ---- D: systematic counts (A.5-A.7) --------------------------------------
-  const int r = tid;
-  const int chunk = r >> 5;
-  const int lam = r & 31;
-  float xg[GH], preg[GH];
-  if (tid < BN) {
-    const int remain = len - chunk * 32;
-    const int last = (remain > 0) ? min(31, remain - 1) : 0;
-#pragma unroll
-    for (int g = 0; g < GH; ++g) {
-      const float invdel = s_invdel[g];
-      const float x = (r < len && invdel > 0.0f) ? h16_to_f32<BF16>(s_ub[r * GH + g]) * invdel : 0.0f;
-      float res = x;
-#pragma unroll
-      for (int o = 1; o < 32; o <<= 1) {
-        const float n = __shfl_up(res, o, 32);
-        if (lam >= o) res = res + n;
-      }
-      const float pre = res - x;
-      xg[g] = x;
-      preg[g] = pre;
-      if (lam == last && remain > 0) s_T[g * CHUNKS + chunk] = pre + x;
-    }
-  }
-  __syncthreads();
-  int flag_sum = 0;
-  if (tid < BN) {
-#pragma unroll
-    for (int g = 0; g < GH; ++g) {
-      int c = 0;
-      if (r < len) {
-        float carry = 0.0f;
-        for (int k = 0; k < chunk; ++k) carry = carry + s_T[g * CHUNKS + k];
-        const float pg = carry + preg[g];
-        const float cum = pg + xg[g];
-        c = count_from_floors(s_a0[g], pg, cum);
-      }
-      s_cnt[g * BN + r] = static_cast<int16_t>(c);
-      flag_sum += c;
-      if (dbg_counts) dbg_counts[((static_cast<size_t>(b) * H + h0 + g) * T_c + t) * BN + r] = static_cast<int16_t>(c);
-    }
+    return;
   }
 
-  // ---- E: emission list (A.8) ----------------------------------------------
-  const bool flag = (tid < BN) && (flag_sum > 0);
-  const uint64_t bal = __ballot(flag);
-  const int pos = __popcll(bal & ((1ull << lane) - 1ull));
-  if (lane == 0) s_wcnt[wave] = __popcll(bal);
-  __syncthreads();
-  int off = 0;
+  // ---- q of the group, scaled once (A.1): qa[hb][m] at lane 4j+i holds head
+  // 4hb+i, dim 16m+j -- the broadcast A operand of the score MFMAs.
+  constexpr int NHB = GH / 4;
+  float qa[NHB][8];
 #pragma unroll
-  for (int w = 0; w < 4; ++w) off += (w < wave) ? s_wcnt[w] : 0;
-  if (flag) s_emit[off + pos] = static_cast<int16_t>(r);
-  const int E = s_wcnt[0] + s_wcnt[1] + s_wcnt[2] + s_wcnt[3];
-  if (tid == 0) emit_cnt[(static_cast<size_t>(b) * KVH + kv) * T_c + t] = E;
+  for (int hb = 0; hb < NHB; ++hb) {
+    const uint16_t* qh = Q + (static_cast<size_t>(b) * H + h0 + 4 * hb + (lane & 3)) * kD + (lane >> 2);
+#pragma unroll
+    for (int m = 0; m < 8; ++m) qa[hb][m] = h16_to_f32<BF16>(qh[16 * m]) * q_scale;
+  }
+  // K staging: wave w's 64 rows, row r chunk c (16 B) at slot r*16 + (c ^ (r & 15)).
+  __shared__ u32x4 s_k[4 * 64 * 16];
+  u32x4* const wk = s_k + wave * 64 * 16;
   __syncthreads();
 
-  // ---- F: count-weighted V sum (A.9) ---------------------------------------
-  const uint16_t* Vt = V + (static_cast<size_t>(b) * L_storage + n0) * row_stride + static_cast<size_t>(kv) * kD +
-                       2 * lane;
+  // Per-head sample lists: each wave owns its heads' lists, so appending and
+  // gathering need no workgroup barrier.  Per-tile mode: (row, count) of the
+  // current tile.  Online mode: (row, count * ell_t, m_t) until a flush.
+  __shared__ float s_lm[(MODE == kOnline) ? GH * LCAP : 1];
+  __shared__ float s_lcw[GH * LCAP];
+  __shared__ int s_lrow[GH * LCAP];
+  int lcnt[HPW];
+  float numM[HPW];
 #pragma unroll
-  for (int g = wave; g < GH; g += 4) {
-    float acc0 = 0.0f, acc1 = 0.0f;
-    for (int base = 0; base < E; base += 8) {
-      uint32_t vw[8];
-      float cf[8];
+  for (int k = 0; k < HPW; ++k) {
+    lcnt[k] = 0;
+    numM[k] = -__builtin_inff();
+  }
+  // num = sum over listed samples of count * ell_t * exp(m_t - M) * v_row,
+  // with M the running max at flush time; earlier flushes are rescaled.
+  auto flush = [&](int k, int g) {
+    if (lcnt[k] == 0) return;
+    const float Mf = runM[k];
+    const float rs = santa_expf(numM[k] - Mf);
+    num0[k] *= rs;
+    num1[k] *= rs;
+    numM[k] = Mf;
+    for (int base = 0; base < lcnt[k]; base += 16) {
+      float coef[16];
+      uint32_t vw[16];
 #pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        const int ii = base + j;
-        const int rr = (ii < E) ? static_cast<int>(s_emit[ii]) : 0;
-        const int c = (ii < E) ? static_cast<int>(s_cnt[g * BN + rr]) : 0;
-        cf[j] = static_cast<float>(c);
-        vw[j] = (c != 0) ? *reinterpret_cast<const uint32_t*>(Vt + static_cast<size_t>(rr) * row_stride) : 0u;
+      for (int q = 0; q < 16; ++q) {
+        const int i = base + q;
+        const bool ok = i < lcnt[k];
+        const int row = ok ? s_lrow[g * LCAP + i] : 0;
+        coef[q] = ok ? s_lcw[g * LCAP + i] * santa_expf(s_lm[g * LCAP + i] - Mf) : 0.0f;
+        vw[q] = *reinterpret_cast<const uint32_t*>(Vg + static_cast<size_t>(row) * row_stride);
       }
 #pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        if (cf[j] != 0.0f) {
-          acc0 = fmaf(cf[j], lo16_to_f32<BF16>(vw[j]), acc0);
-          acc1 = fmaf(cf[j], hi16_to_f32<BF16>(vw[j]), acc1);
+      for (int q = 0; q < 16; ++q) {
+        if (base + q < lcnt[k]) {
+          num0[k] = fmaf(coef[q], lo16_to_f32<BF16>(vw[q]), num0[k]);
+          num1[k] = fmaf(coef[q], hi16_to_f32<BF16>(vw[q]), num1[k]);
         }
       }
     }
-    float2* op = reinterpret_cast<float2*>(out_tiles + ((static_cast<size_t>(b) * H + h0 + g) * T_c + t) * kD) + lane;
-    *op = make_float2(acc0, acc1);
+    lcnt[k] = 0;
+  };
+
+  // This wave's 64 rows of a tile: 16 loads of 16 B per lane, 4 rows each.
+  u32x4 kw[16];
+  auto load_k = [&](int t) {
+    const int n0 = t * BN;
+    const int len = min(BN, L_valid - n0);
+    if (64 * wave >= len) return;  // no rows for this wave (short tiles)
+#pragma unroll
+    for (int c = 0; c < 16; ++c) {
+      const int rr = min(64 * wave + 4 * c + (lane >> 4), len - 1);
+      kw[c] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(Kg + static_cast<size_t>(n0 + rr) * row_stride) +
+                                         (lane & 15));
+    }
+  };
+  load_k(t_begin);
+
+  for (int t = t_begin; t < t_end; ++t) {
+    const int n0 = t * BN;
+    const int len = min(BN, L_valid - n0);
+
+    // ---- A: scores -----------------------------------------------------------
+    float lmax[GH];
+#pragma unroll
+    for (int g = 0; g < GH; ++g) lmax[g] = -__builtin_inff();
+    if (64 * wave < len) {
+#pragma unroll
+      for (int c = 0; c < 16; ++c) {
+        const int r = 4 * c + (lane >> 4);
+        wk[r * 16 + ((lane & 15) ^ (r & 15))] = kw[c];
+      }
+      // the next tile's rows stream in through this tile's scores and tail
+      if (t + 1 < t_end) load_k(t + 1);
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+
+      // score = D_even + D_odd with C(c) = B(c) + B(c+2), D = C(0) + C(1)
+      const int row = lane;
+      f32x4 be0[NHB], bo0[NHB], be2[NHB], bo2[NHB], be1[NHB], bo1[NHB], be3[NHB], bo3[NHB];
+      score_group<BF16, NHB, 0>(wk, row, qa, be0, bo0);
+      score_group<BF16, NHB, 2>(wk, row, qa, be2, bo2);
+      score_group<BF16, NHB, 1>(wk, row, qa, be1, bo1);
+      score_group<BF16, NHB, 3>(wk, row, qa, be3, bo3);
+      const int r = 64 * wave + row;
+#pragma unroll
+      for (int hb = 0; hb < NHB; ++hb) {
+        const f32x4 de = (be0[hb] + be2[hb]) + (be1[hb] + be3[hb]);
+        const f32x4 dd = (bo0[hb] + bo2[hb]) + (bo1[hb] + bo3[hb]);
+        const f32x4 sc = de + dd;  // heads 4hb .. 4hb+3 of row r
+        if (BN == 256 || r < BN) reinterpret_cast<f32x4*>(s_sc + r * GH)[hb] = sc;
+        // rows past len hold copies of row len-1, so they leave the max unchanged
+#pragma unroll
+        for (int i = 0; i < 4; ++i) lmax[4 * hb + i] = sc[i];
+      }
+    } else {
+      if (t + 1 < t_end) load_k(t + 1);
+    }
+
+    // ---- B: tile max per head (A.3) ------------------------------------------
+#pragma unroll
+    for (int g = 0; g < GH; ++g) {
+      const float mx = wave_max_dpp(lmax[g]);
+      if (lane == 0) s_wmax[wave * GH + g] = mx;
+    }
+    __syncthreads();  // (1) scores and wave maxima visible
+    if constexpr (MODE == kOnline) {
+      // union of the previous tile's sampled rows: its masks were published
+      // before barrier (1) and are rewritten only after barrier (2).
+      if (wave == 0 && t > t_begin) emit_total += union_rows<GH, 2 * NPAIR>(s_mask, lane);
+    }
+
+    // ---- C: u, 16-bit u and ell partials (A.4) ---------------------------------
+    // Thread tid plays the reference's thread tid: items idx = tid + NT_REF k.
+    if (tid < NT_REF) {
+      const int g = tid % GH;
+      float mg = s_wmax[g];
+#pragma unroll
+      for (int w = 1; w < 4; ++w) mg = fmaxf(mg, s_wmax[w * GH + g]);
+      float sv[KC];
+#pragma unroll
+      for (int k = 0; k < KC; ++k) {
+        const int idx = tid + NT_REF * k;
+        sv[k] = (idx < len * GH) ? s_sc[idx] : 0.0f;
+      }
+      float acc = 0.0f;
+#pragma unroll
+      for (int k = 0; k < KC; ++k) {
+        const int idx = tid + NT_REF * k;
+        if (idx < len * GH) {
+          const float u = santa_expf(sv[k] - mg);
+          acc += u;
+          s_ub[g * BN + idx / GH] = f32_to_h16<BF16>(u);
+        }
+      }
+      // the reference's 32-lane tree for lane g of each warp: pairs at lane
+      // distance 16, 8, ... GH; the remaining levels only add +0.
+#pragma unroll
+      for (int m = 16; m >= GH; m >>= 1) acc = acc + __shfl_xor(acc, m, 32);
+      if ((tid & 31) < GH) s_W[(tid >> 5) * GH + (tid & 31)] = acc;
+    }
+    __syncthreads();  // (2) 16-bit u and warp masses visible
+
+    // ---- D/E: per-head counts, sample lists -------------------------------------
+#pragma unroll
+    for (int k = 0; k < HPW; ++k) {
+      const int g = wave + 4 * k;
+      const int h = h0 + g;
+      float mg = s_wmax[g];
+#pragma unroll
+      for (int w = 1; w < 4; ++w) mg = fmaxf(mg, s_wmax[w * GH + g]);
+      float ell = 0.0f;
+#pragma unroll
+      for (int w = 0; w < NW_REF; ++w) ell += s_W[w * GH + g];
+      const float invdel = (S_pt > 0 && ell > 1e-20f) ? (static_cast<float>(S_pt) / ell) : 0.0f;
+      const float a0 = u01(seed, b * H + h, t);
+
+      // 32-row chunks, two rows per lane: lane 16j+q of pair p holds rows
+      // 32(4p+j) + 2q and +1, so every Hillis-Steele step (offsets 1..16)
+      // stays inside a 16-lane DPP row; same pairing as the reference's
+      // 32-lane scan (flash/santa_cuda_kernel.cu:60-69).
+      const int jrow = lane >> 4;
+      const int qq = lane & 15;
+      float x0[NPAIR], x1[NPAIR], r0[NPAIR], r1[NPAIR];
+#pragma unroll
+      for (int pp = 0; pp < NPAIR; ++pp) {
+        const int row = 32 * (4 * pp + jrow) + 2 * qq;
+        const uint32_t w2 = (BN >= 128 || row < BN) ? *reinterpret_cast<const uint32_t*>(s_ub + g * BN + row) : 0u;
+        x0[pp] = (row < len && invdel > 0.0f) ? lo16_to_f32<BF16>(w2) * invdel : 0.0f;
+        x1[pp] = (row + 1 < len && invdel > 0.0f) ? hi16_to_f32<BF16>(w2) * invdel : 0.0f;
+        r1[pp] = x1[pp] + x0[pp];
+        r0[pp] = x0[pp] + dpp_shr_zero<1>(x1[pp]);
+      }
+#pragma unroll
+      for (int pp = 0; pp < NPAIR; ++pp) {
+        r0[pp] = r0[pp] + dpp_shr_zero<1>(r0[pp]);
+        r1[pp] = r1[pp] + dpp_shr_zero<1>(r1[pp]);
+        r0[pp] = r0[pp] + dpp_shr_zero<2>(r0[pp]);
+        r1[pp] = r1[pp] + dpp_shr_zero<2>(r1[pp]);
+        r0[pp] = r0[pp] + dpp_shr_zero<4>(r0[pp]);
+        r1[pp] = r1[pp] + dpp_shr_zero<4>(r1[pp]);
+        r0[pp] = r0[pp] + dpp_shr_zero<8>(r0[pp]);
+        r1[pp] = r1[pp] + dpp_shr_zero<8>(r1[pp]);
+      }
+      // exclusive prefixes and the reference's sequential cross-chunk carries
+      float pre0[NPAIR], pre1[NPAIR], car[NPAIR];
+      float carry = 0.0f;
+#pragma unroll
+      for (int pp = 0; pp < NPAIR; ++pp) {
+        pre0[pp] = r0[pp] - x0[pp];
+        pre1[pp] = r1[pp] - x1[pp];
+        const float tot0 = pre0[pp] + x0[pp];
+        const float tot1 = pre1[pp] + x1[pp];
+        float cj[4];
+#pragma unroll
+        for (int jj = 0; jj < 4; ++jj) {
+          const int rem = len - 32 * (4 * pp + jj);
+          cj[jj] = carry;
+          if (4 * pp + jj < NCH && rem > 0) {
+            const int last = min(31, rem - 1);
+            const int src = 16 * jj + (last >> 1);
+            const float tot = (last & 1) ? __int_as_float(__builtin_amdgcn_readlane(__float_as_int(tot1), src))
+                                         : __int_as_float(__builtin_amdgcn_readlane(__float_as_int(tot0), src));
+            carry = carry + tot;
+          }
+        }
+        car[pp] = (jrow == 0) ? cj[0] : (jrow == 1) ? cj[1] : (jrow == 2) ? cj[2] : cj[3];
+      }
+      int c0[NPAIR], c1[NPAIR];
+      uint64_t nz0[NPAIR], nz1[NPAIR];
+#pragma unroll
+      for (int pp = 0; pp < NPAIR; ++pp) {
+        const int row = 32 * (4 * pp + jrow) + 2 * qq;
+        const float pg0 = car[pp] + pre0[pp];
+        const float pg1 = car[pp] + pre1[pp];
+        c0[pp] = (row < len) ? count_from_floors(a0, pg0, pg0 + x0[pp]) : 0;
+        c1[pp] = (row + 1 < len) ? count_from_floors(a0, pg1, pg1 + x1[pp]) : 0;
+        nz0[pp] = __ballot(c0[pp] != 0);
+        nz1[pp] = __ballot(c1[pp] != 0);
+        if (lane == 0) {
+          s_mask[(g * NPAIR + pp) * 2 + 0] = nz0[pp];
+          s_mask[(g * NPAIR + pp) * 2 + 1] = nz1[pp];
+        }
+        if constexpr (MODE == kPerTile) {
+          if (dbg_counts && row < BN) {
+            int16_t* dc = dbg_counts + ((static_cast<size_t>(b) * H + h) * T_c + t) * BN + row;
+            dc[0] = static_cast<int16_t>(c0[pp]);
+            dc[1] = static_cast<int16_t>(c1[pp]);
+          }
+        }
+      }
+
+      if constexpr (MODE == kOnline) {
+        // running max and mass of the chunk
+        if (mg > runM[k]) {
+          runZ[k] = fmaf(runZ[k], santa_expf(runM[k] - mg), ell);
+          runM[k] = mg;
+        } else {
+          runZ[k] = fmaf(santa_expf(mg - runM[k]), ell, runZ[k]);
+        }
+      }
+      // Append the head's sampled rows in ascending order: (row, count[*ell_t], m_t).
+      const uint64_t below = (1ull << lane) - 1ull;
+#pragma unroll
+      for (int pp = 0; pp < NPAIR; ++pp) {
+        const int row = 32 * (4 * pp + jrow) + 2 * qq;
+        if constexpr (MODE == kOnline) {
+          // at most 128 new rows per register pair; the list holds that many
+          if (lcnt[k] + __popcll(nz0[pp]) + __popcll(nz1[pp]) > LCAP) flush(k, g);
+        }
+        const int pos0 = lcnt[k] + __popcll(nz0[pp] & below) + __popcll(nz1[pp] & below);
+        const int pos1 = pos0 + (c0[pp] != 0 ? 1 : 0);
+        if (c0[pp] != 0) {
+          s_lrow[g * LCAP + pos0] = n0 + row;
+          s_lcw[g * LCAP + pos0] = (MODE == kOnline) ? static_cast<float>(c0[pp]) * ell : static_cast<float>(c0[pp]);
+          if constexpr (MODE == kOnline) s_lm[g * LCAP + pos0] = mg;
+        }
+        if (c1[pp] != 0) {
+          s_lrow[g * LCAP + pos1] = n0 + row + 1;
+          s_lcw[g * LCAP + pos1] = (MODE == kOnline) ? static_cast<float>(c1[pp]) * ell : static_cast<float>(c1[pp]);
+          if constexpr (MODE == kOnline) s_lm[g * LCAP + pos1] = mg;
+        }
+        lcnt[k] += __popcll(nz0[pp]) + __popcll(nz1[pp]);
+      }
+
+      if constexpr (MODE == kPerTile) {
+        // count-weighted V sum over the head's sampled rows, ascending, one fma
+        // per element (flash/santa_cuda_kernel.cu:347-379)
+        float acc0 = 0.0f, acc1 = 0.0f;
+        for (int base = 0; base < lcnt[k]; base += 8) {
+          float cf[8];
+          uint32_t vw[8];
+#pragma unroll
+          for (int q = 0; q < 8; ++q) {
+            const int i = base + q;
+            const bool ok = i < lcnt[k];
+            const int rr = ok ? s_lrow[g * LCAP + i] : n0;
+            cf[q] = ok ? s_lcw[g * LCAP + i] : 0.0f;
+            vw[q] = *reinterpret_cast<const uint32_t*>(Vg + static_cast<size_t>(rr) * row_stride);
+          }
+#pragma unroll
+          for (int q = 0; q < 8; ++q) {
+            if (base + q < lcnt[k]) {
+              acc0 = fmaf(cf[q], lo16_to_f32<BF16>(vw[q]), acc0);
+              acc1 = fmaf(cf[q], hi16_to_f32<BF16>(vw[q]), acc1);
+            }
+          }
+        }
+        lcnt[k] = 0;
+        const size_t mt = (static_cast<size_t>(b) * H + h) * T_c + t;
+        if (lane == 0) {
+          m_tiles[mt] = mg;
+          ell_tiles[mt] = ell;
+        }
+        reinterpret_cast<float2*>(out_tiles + mt * kD)[lane] = make_float2(acc0, acc1);
+      }
+    }
+
+    if constexpr (MODE == kPerTile) {
+      // rows sampled by any head of the group -> emit_cnt
+      __syncthreads();
+      if (wave == 0) {
+        const int e = union_rows<GH, 2 * NPAIR>(s_mask, lane);
+        if (lane == 0) emit_cnt[static_cast<size_t>(bk) * T_c + t] = e;
+      }
+    }
+  }
+
+  if constexpr (MODE == kOnline) {
+    __syncthreads();  // last tile's masks visible
+    if (wave == 0) emit_total += union_rows<GH, 2 * NPAIR>(s_mask, lane);
+#pragma unroll
+    for (int k = 0; k < HPW; ++k) flush(k, wave + 4 * k);
+#pragma unroll
+    for (int k = 0; k < HPW; ++k) {
+      float* pp = part + (static_cast<size_t>(wg) * GH + wave + 4 * k) * kPartStride;
+      if (lane == 0) {
+        pp[0] = runM[k];
+        pp[1] = runZ[k];
+      }
+      pp[2 + 2 * lane] = num0[k];
+      pp[3 + 2 * lane] = num1[k];
+    }
+    if (tid == 0) part_emit[wg] = emit_total;
   }
 }
 
-// Split-KV merge (flash/santa_cuda_kernel.cu:386-470): one workgroup per
-// (b, h); max and Z trees with the reference's pairing (strides 128 .. 1),
-// numerator accumulated over tiles in ascending order with fma.
+// Split-KV merge of per-tile partials (flash/santa_cuda_kernel.cu:386-470):
+// one workgroup per (b, h); max and Z trees with the reference's pairing
+// (strides 128 .. 1), numerator accumulated over tiles in ascending order
+// with fma.
 template <bool BF16>
 __global__ __launch_bounds__(kThreads) void finalize_kernel(const float* __restrict__ m_tiles,
                                                             const float* __restrict__ ell_tiles,
@@ -347,35 +612,110 @@ __global__ __launch_bounds__(kThreads) void finalize_kernel(const float* __restr
   }
 }
 
-template <bool BF16, int GH, int BN>
-static hipError_t launch_tiles_t(const void* q, const void* K, const void* V, int B, int H, int KVH, int L_valid,
-                                 int L_storage, int T_c, int S_pt, uint64_t seed, float* m_tiles, float* ell_tiles,
-                                 float* out_tiles, int* emit_cnt, int16_t* counts, hipStream_t stream) {
+// Merge of the chunk partials of one (b, h): m* = max_c M_c,
+// w_c = exp(M_c - m*), out = (sum_c w_c num_c) / ((sum_c w_c Z_c) S_pt).
+template <bool BF16, int GH>
+__global__ __launch_bounds__(kD) void merge_kernel(const float* __restrict__ part, const int* __restrict__ part_emit,
+                                                   int H, int KVH, int cpg, int S_pt, uint16_t* __restrict__ out,
+                                                   float* __restrict__ m_star, int* __restrict__ vrows) {
+  const int bh = static_cast<int>(blockIdx.x);
+  const int b = bh / H;
+  const int h = bh % H;
+  const int kv = h / GH;
+  const int g = h % GH;
+  const int bk = b * KVH + kv;
+  const int d = static_cast<int>(threadIdx.x);
+  const float* pb = part + (static_cast<size_t>(bk) * cpg * GH + g) * kPartStride;
+  float ms = -__builtin_inff();
+  for (int c = 0; c < cpg; ++c) ms = fmaxf(ms, pb[static_cast<size_t>(c) * GH * kPartStride]);
+  float Z = 0.0f, num = 0.0f;
+  for (int c = 0; c < cpg; ++c) {
+    const float* pc = pb + static_cast<size_t>(c) * GH * kPartStride;
+    const float w = santa_expf(pc[0] - ms);
+    Z = fmaf(w, pc[1], Z);
+    num = fmaf(w, pc[2 + d], num);
+  }
+  const float inv_norm = (S_pt > 0 && Z > 0.0f) ? (1.0f / (Z * static_cast<float>(S_pt))) : 0.0f;
+  out[static_cast<size_t>(bh) * kD + d] = f32_to_h16<BF16>(num * inv_norm);
+  if (d == 0 && m_star) m_star[bh] = ms;
+  if (vrows && g == 0 && d == 0) {
+    int e = 0;
+    for (int c = 0; c < cpg; ++c) e += part_emit[static_cast<size_t>(bk) * cpg + c];
+    vrows[bk] = e;
+  }
+}
+
+struct Args {
+  const void* q;
+  const void* K;
+  const void* V;
+  int B, H, KVH, L_valid, L_storage, T_c, S_pt;
+  uint64_t seed;
+  float *m_tiles, *ell_tiles, *out_tiles;
+  int* emit_cnt;
+  int16_t* counts;
+  float* part;
+  int* part_emit;
+  int cs, cpg;
+};
+
+template <bool BF16, int GH, int BN, int MODE>
+static hipError_t launch_t(const Args& a, hipStream_t stream) {
   const float q_scale = 1.0f / sqrtf(static_cast<float>(kD));
-  const unsigned grid = static_cast<unsigned>(B) * static_cast<unsigned>(KVH) * static_cast<unsigned>(T_c);
-  hipLaunchKernelGGL((fused_tile_kernel<BF16, GH, BN>), dim3(grid), dim3(kThreads), 0, stream,
-                     static_cast<const uint16_t*>(q), static_cast<const uint16_t*>(K),
-                     static_cast<const uint16_t*>(V), H, KVH, L_valid, L_storage, T_c, q_scale, S_pt, seed, m_tiles,
-                     ell_tiles, out_tiles, emit_cnt, counts);
+  const unsigned grid = static_cast<unsigned>(a.B) * static_cast<unsigned>(a.KVH) * static_cast<unsigned>(a.cpg);
+  hipLaunchKernelGGL((tile_kernel<BF16, GH, BN, MODE>), dim3(grid), dim3(kThreads), 0, stream,
+                     static_cast<const uint16_t*>(a.q), static_cast<const uint16_t*>(a.K),
+                     static_cast<const uint16_t*>(a.V), a.H, a.KVH, a.L_valid, a.L_storage, a.T_c, a.cs, a.cpg,
+                     q_scale, a.S_pt, a.seed, a.m_tiles, a.ell_tiles, a.out_tiles, a.emit_cnt, a.counts, a.part,
+                     a.part_emit);
   return hipGetLastError();
 }
 
-template <bool BF16, int GH>
-static hipError_t launch_tiles_bn(int bn, const void* q, const void* K, const void* V, int B, int H, int KVH,
-                                  int L_valid, int L_storage, int T_c, int S_pt, uint64_t seed, float* m_tiles,
-                                  float* ell_tiles, float* out_tiles, int* emit_cnt, int16_t* counts,
-                                  hipStream_t stream) {
+template <bool BF16, int GH, int MODE>
+static hipError_t launch_bn(int bn, const Args& a, hipStream_t stream) {
   switch (bn) {
     case 32:
-      return launch_tiles_t<BF16, GH, 32>(q, K, V, B, H, KVH, L_valid, L_storage, T_c, S_pt, seed, m_tiles,
-                                          ell_tiles, out_tiles, emit_cnt, counts, stream);
+      return launch_t<BF16, GH, 32, MODE>(a, stream);
     case 64:
-      return launch_tiles_t<BF16, GH, 64>(q, K, V, B, H, KVH, L_valid, L_storage, T_c, S_pt, seed, m_tiles,
-                                          ell_tiles, out_tiles, emit_cnt, counts, stream);
+      return launch_t<BF16, GH, 64, MODE>(a, stream);
     default:
-      return launch_tiles_t<BF16, GH, 256>(q, K, V, B, H, KVH, L_valid, L_storage, T_c, S_pt, seed, m_tiles,
-                                           ell_tiles, out_tiles, emit_cnt, counts, stream);
+      return launch_t<BF16, GH, 256, MODE>(a, stream);
   }
+}
+
+template <int MODE>
+static hipError_t launch_tiles(int dtype, int GH, int bn, const Args& a, hipStream_t stream) {
+  if (dtype == SANTA_BF16)
+    return (GH == 4) ? launch_bn<true, 4, MODE>(bn, a, stream) : launch_bn<true, 8, MODE>(bn, a, stream);
+  return (GH == 4) ? launch_bn<false, 4, MODE>(bn, a, stream) : launch_bn<false, 8, MODE>(bn, a, stream);
+}
+
+// Workgroups resident per device: CUs x 2 (two 256-thread workgroups per CU
+// at the tile kernel's register budget).
+static int resident_workgroups() {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return 512;
+  static int cached_dev = -1;
+  static int cached = 512;
+  if (dev != cached_dev) {
+    int cus = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) cus = 256;
+    cached = 2 * cus;
+    cached_dev = dev;
+  }
+  return cached;
+}
+
+// Chunking of each group's T_c tiles so that B*KVH*cpg is about one resident
+// round: cpg chunks of cs tiles (the last may be shorter).
+static void chunk_plan(int B, int KVH, int T_c, int* cs, int* cpg) {
+  const long long groups = static_cast<long long>(B) * KVH;
+  long long want = (resident_workgroups() + groups / 2) / groups;
+  if (want < 1) want = 1;
+  if (want > T_c) want = T_c;
+  const int c = static_cast<int>((T_c + want - 1) / want);
+  *cs = c;
+  *cpg = (T_c + c - 1) / c;
 }
 
 }  // namespace flash
@@ -436,20 +776,10 @@ extern "C" int santa_flash_fused_tiles(const void* q, const void* K, const void*
   if (st != SANTA_OK) return st;
   if (!q || !K || !V || !m_tiles || !ell_tiles || !out_tiles || !emit_cnt)
     return set_error(SANTA_ERR_INVALID, "null pointer argument");
-  const int T_c = (L_valid + block_n - 1) / block_n;
-  const int GH = H / KVH;
-  hipError_t e;
-  if (dtype == SANTA_BF16) {
-    e = (GH == 4) ? flash::launch_tiles_bn<true, 4>(block_n, q, K, V, B, H, KVH, L_valid, L_storage, T_c, S_per_tile,
-                                                    seed, m_tiles, ell_tiles, out_tiles, emit_cnt, counts, stream)
-                  : flash::launch_tiles_bn<true, 8>(block_n, q, K, V, B, H, KVH, L_valid, L_storage, T_c, S_per_tile,
-                                                    seed, m_tiles, ell_tiles, out_tiles, emit_cnt, counts, stream);
-  } else {
-    e = (GH == 4) ? flash::launch_tiles_bn<false, 4>(block_n, q, K, V, B, H, KVH, L_valid, L_storage, T_c, S_per_tile,
-                                                     seed, m_tiles, ell_tiles, out_tiles, emit_cnt, counts, stream)
-                  : flash::launch_tiles_bn<false, 8>(block_n, q, K, V, B, H, KVH, L_valid, L_storage, T_c, S_per_tile,
-                                                     seed, m_tiles, ell_tiles, out_tiles, emit_cnt, counts, stream);
-  }
+  flash::Args a{q, K, V, B, H, KVH, L_valid, L_storage, (L_valid + block_n - 1) / block_n, S_per_tile, seed,
+                m_tiles, ell_tiles, out_tiles, emit_cnt, counts, nullptr, nullptr, 0, 0};
+  flash::chunk_plan(B, KVH, a.T_c, &a.cs, &a.cpg);
+  hipError_t e = flash::launch_tiles<flash::kPerTile>(dtype, H / KVH, block_n, a, stream);
   if (e != hipSuccess) return set_error(SANTA_ERR_HIP, "fused tile launch failed: %s", hipGetErrorString(e));
   return clear_error();
 }
@@ -463,7 +793,7 @@ extern "C" int santa_flash_finalize(const float* m_tiles, const float* ell_tiles
   if (!m_tiles || !ell_tiles || !out_tiles || !out || (vrows && !emit_cnt))
     return set_error(SANTA_ERR_INVALID, "null pointer argument");
   const size_t shmem = static_cast<size_t>(T_c + flash::kThreads) * sizeof(float);
-  if (shmem > 160 * 1024) return set_error(SANTA_ERR_UNSUPPORTED, "T_c too large for the finalize kernel");
+  if (shmem > 64 * 1024) return set_error(SANTA_ERR_UNSUPPORTED, "T_c too large for the finalize kernel");
   const unsigned grid = static_cast<unsigned>(B) * static_cast<unsigned>(H);
   if (dtype == SANTA_BF16)
     hipLaunchKernelGGL(flash::finalize_kernel<true>, dim3(grid), dim3(flash::kThreads), shmem, stream, m_tiles,
@@ -480,47 +810,97 @@ extern "C" int santa_flash_finalize(const float* m_tiles, const float* ell_tiles
 
 namespace {
 struct FlashWs {
-  size_t m, ell, out, emit, total;
+  size_t part, emit, total;
+  int cs, cpg;
 };
-FlashWs flash_ws_layout(int B, int H, int KVH, int D, int T_c) {
+FlashWs flash_ws_layout(int B, int H, int KVH, int T_c) {
   FlashWs w{};
-  const size_t bht = static_cast<size_t>(B) * H * T_c;
+  flash::chunk_plan(B, KVH, T_c, &w.cs, &w.cpg);
+  const size_t chunks = static_cast<size_t>(B) * KVH * w.cpg;
+  const int GH = H / KVH;
   size_t off = 0;
-  w.m = off;
-  off = santa::align_up(off + bht * sizeof(float));
-  w.ell = off;
-  off = santa::align_up(off + bht * sizeof(float));
-  w.out = off;
-  off = santa::align_up(off + bht * static_cast<size_t>(D) * sizeof(float));
+  w.part = off;
+  off = santa::align_up(off + chunks * GH * flash::kPartStride * sizeof(float));
   w.emit = off;
-  off = santa::align_up(off + static_cast<size_t>(B) * KVH * T_c * sizeof(int));
+  off = santa::align_up(off + chunks * sizeof(int));
   w.total = off;
   return w;
 }
 }  // namespace
 
 extern "C" size_t santa_flash_workspace_size(int B, int H, int KVH, int D, int T_c) {
-  return flash_ws_layout(B, H, KVH, D, T_c).total;
+  (void)D;
+  if (B <= 0 || H <= 0 || KVH <= 0 || T_c <= 0 || H % KVH != 0) return 0;
+  return flash_ws_layout(B, H, KVH, T_c).total;
+}
+
+static int flash_ws_check(int B, int H, int KVH, int T_c, void* workspace, size_t workspace_bytes, FlashWs* w) {
+  *w = flash_ws_layout(B, H, KVH, T_c);
+  if (!workspace || workspace_bytes < w->total)
+    return set_error(SANTA_ERR_WORKSPACE, "workspace too small: need %zu bytes, got %zu", w->total, workspace_bytes);
+  return SANTA_OK;
+}
+
+extern "C" int santa_flash_decode_tiles(const void* q, const void* K, const void* V, int dtype, int B, int H, int KVH,
+                                        int D, int L_valid, int L_storage, int block_n, int S_per_tile, uint64_t seed,
+                                        void* workspace, size_t workspace_bytes, hipStream_t stream) {
+  int st = check_flash_shape(dtype, B, H, KVH, D, L_valid, L_storage, block_n);
+  if (st != SANTA_OK) return st;
+  if (!q || !K || !V) return set_error(SANTA_ERR_INVALID, "null pointer argument");
+  const int T_c = (L_valid + block_n - 1) / block_n;
+  FlashWs w;
+  if ((st = flash_ws_check(B, H, KVH, T_c, workspace, workspace_bytes, &w)) != SANTA_OK) return st;
+  char* base = static_cast<char*>(workspace);
+  flash::Args a{q, K, V, B, H, KVH, L_valid, L_storage, T_c, S_per_tile, seed, nullptr, nullptr, nullptr, nullptr,
+                nullptr, reinterpret_cast<float*>(base + w.part), reinterpret_cast<int*>(base + w.emit), w.cs, w.cpg};
+  const hipError_t e = flash::launch_tiles<flash::kOnline>(dtype, H / KVH, block_n, a, stream);
+  if (e != hipSuccess) return set_error(SANTA_ERR_HIP, "tile launch failed: %s", hipGetErrorString(e));
+  return clear_error();
+}
+
+extern "C" int santa_flash_decode_merge(const void* workspace, size_t workspace_bytes, int dtype, int B, int H,
+                                        int KVH, int D, int T_c, int S_per_tile, void* out, float* m_star, int* vrows,
+                                        hipStream_t stream) {
+  if (D != 128) return set_error(SANTA_ERR_UNSUPPORTED, "This build supports only D=128. Got D=%d", D);
+  if (B <= 0 || H <= 0 || KVH <= 0 || H % KVH != 0 || T_c <= 0 || (H / KVH != 4 && H / KVH != 8))
+    return set_error(SANTA_ERR_INVALID, "bad merge shape");
+  if (!out) return set_error(SANTA_ERR_INVALID, "null pointer argument");
+  FlashWs w;
+  int st = flash_ws_check(B, H, KVH, T_c, const_cast<void*>(workspace), workspace_bytes, &w);
+  if (st != SANTA_OK) return st;
+  const char* base = static_cast<const char*>(workspace);
+  const float* part = reinterpret_cast<const float*>(base + w.part);
+  const int* pe = reinterpret_cast<const int*>(base + w.emit);
+  const int GH = H / KVH;
+  const unsigned grid = static_cast<unsigned>(B) * static_cast<unsigned>(H);
+  uint16_t* o = static_cast<uint16_t*>(out);
+  if (dtype == SANTA_BF16) {
+    if (GH == 4)
+      hipLaunchKernelGGL((flash::merge_kernel<true, 4>), dim3(grid), dim3(flash::kD), 0, stream, part, pe, H, KVH,
+                         w.cpg, S_per_tile, o, m_star, vrows);
+    else
+      hipLaunchKernelGGL((flash::merge_kernel<true, 8>), dim3(grid), dim3(flash::kD), 0, stream, part, pe, H, KVH,
+                         w.cpg, S_per_tile, o, m_star, vrows);
+  } else {
+    if (GH == 4)
+      hipLaunchKernelGGL((flash::merge_kernel<false, 4>), dim3(grid), dim3(flash::kD), 0, stream, part, pe, H, KVH,
+                         w.cpg, S_per_tile, o, m_star, vrows);
+    else
+      hipLaunchKernelGGL((flash::merge_kernel<false, 8>), dim3(grid), dim3(flash::kD), 0, stream, part, pe, H, KVH,
+                         w.cpg, S_per_tile, o, m_star, vrows);
+  }
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return set_error(SANTA_ERR_HIP, "merge launch failed: %s", hipGetErrorString(e));
+  return clear_error();
 }
 
 extern "C" int santa_flash_decode(const void* q, const void* K, const void* V, int dtype, int B, int H, int KVH,
                                   int D, int L_valid, int L_storage, int block_n, int S_per_tile, uint64_t seed,
                                   void* out, float* m_star, int* vrows, void* workspace, size_t workspace_bytes,
                                   hipStream_t stream) {
-  int st = check_flash_shape(dtype, B, H, KVH, D, L_valid, L_storage, block_n);
+  const int st = santa_flash_decode_tiles(q, K, V, dtype, B, H, KVH, D, L_valid, L_storage, block_n, S_per_tile, seed,
+                                          workspace, workspace_bytes, stream);
   if (st != SANTA_OK) return st;
-  const int T_c = (L_valid + block_n - 1) / block_n;
-  const FlashWs w = flash_ws_layout(B, H, KVH, D, T_c);
-  if (!workspace || workspace_bytes < w.total)
-    return set_error(SANTA_ERR_WORKSPACE, "workspace too small: need %zu bytes, got %zu", w.total, workspace_bytes);
-  char* base = static_cast<char*>(workspace);
-  float* m_tiles = reinterpret_cast<float*>(base + w.m);
-  float* ell_tiles = reinterpret_cast<float*>(base + w.ell);
-  float* out_tiles = reinterpret_cast<float*>(base + w.out);
-  int* emit = reinterpret_cast<int*>(base + w.emit);
-  st = santa_flash_fused_tiles(q, K, V, dtype, B, H, KVH, D, L_valid, L_storage, block_n, S_per_tile, seed, m_tiles,
-                               ell_tiles, out_tiles, emit, nullptr, stream);
-  if (st != SANTA_OK) return st;
-  return santa_flash_finalize(m_tiles, ell_tiles, out_tiles, emit, dtype, B, H, KVH, D, T_c, S_per_tile, out, m_star,
-                              vrows, stream);
+  return santa_flash_decode_merge(workspace, workspace_bytes, dtype, B, H, KVH, D, (L_valid + block_n - 1) / block_n,
+                                  S_per_tile, out, m_star, vrows, stream);
 }

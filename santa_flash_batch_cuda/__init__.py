@@ -12,7 +12,10 @@ import torch  # noqa: F401  (must precede the native module)
 
 from ._C import (  # noqa: F401
     _debug_tiles,
+    _decode_reference_order,
+    _decode_tiles_only,
     _library_version,
+    _workspace_bytes,
     decode_systematic_batched,
     decode_systematic_scalar,
 )
