@@ -130,15 +130,17 @@ int santa_prop_pass1(const void* q, const void* K, int dtype, int H, int KVH, in
 int santa_prop_tile_budgets(const float* m_tiles, const float* ell_tiles, int H, int T_c, int S, uint64_t seed,
                             float* m_star, int* S_tiles, float* invdelta, float* a0, hipStream_t stream);
 
-/* Pass 2 + cast: counts from the stash, count-weighted V sums, a
- * deterministic ascending-tile reduction and out = dtype(sum / S).
- * tile_acc [H, T_c, D] f32 and emit_cnt [KVH, T_c] i32 are scratch;
- * counts [H,T_c,block_n] i16 and vrows [KVH] may be NULL. */
+/* Pass 2 + cast: counts from the stash, count-weighted V sums summed per
+ * chunk of tiles in a fixed order (deterministic), out = dtype(sum / S)
+ * (0 when S <= 0).  counts [H,T_c,block_n] i16 and vrows [KVH] may be NULL.
+ * workspace >= santa_prop_workspace_size bytes (its chunk-partial region is
+ * used; contents need no initialization). */
 int santa_prop_pass2(const void* V, const void* u_stash, int dtype, int H, int KVH, int D, int L, int block_n,
-                     int S, const float* invdelta, const float* a0, float* tile_acc, int* emit_cnt,
-                     int16_t* counts, void* out, int* vrows, hipStream_t stream);
+                     int S, const float* invdelta, const float* a0, int16_t* counts, void* out, int* vrows,
+                     void* workspace, size_t workspace_bytes, hipStream_t stream);
 
-/* Bytes of device workspace santa_prop_decode needs. */
+/* Bytes of device workspace santa_prop_decode / santa_prop_pass2 need on the
+ * current device (m, ell, budgets, the u stash and chunk partials). */
 size_t santa_prop_workspace_size(int H, int KVH, int D, int L, int T_c);
 
 /* Whole single-sequence prop decode with the caller's workspace. */

@@ -463,11 +463,12 @@ int so_flash_decode(const uint16_t* Q, const uint16_t* K, const uint16_t* V, int
 /* ------------------------------------------------------------------ */
 
 /* Pass-1 of the general ("WMMA") path, prop/santa_cuda_kernel.cu:87-267:
- * q' = TK(f32(q) * scale); scores are a 16x16x16-tiled MMA whose internal
- * association is unspecified, restated here as the exactly-rounded float64
- * dot product (tolerance-level parity only).  ell: per 16-column warp
- * slice a sequential sum (:229-246), then a sequential sum over warps
- * (:257-259). */
+ * q' = TK(f32(q) * scale) (:121-140).  The reference's scores come from a
+ * 16x16x16 MMA whose internal association is unspecified; this build fixes
+ * it to the vec path's (4-element fma chains per virtual lane and the
+ * 32-lane tree, A.2) so that the GPU kernel and this restatement agree bit
+ * for bit.  ell: per 16-row slab a sequential sum (:229-246), then a
+ * sequential sum over slabs (:257-259). */
 static void tile_stats_general(const uint16_t* Qh /*[GH][D] raw*/, const uint16_t* K, size_t row0_off,
                                size_t row_stride, int len, int BN, int GH, int is_bf16, float q_scale,
                                tile_stats_t* ts, float* scores) {
@@ -476,15 +477,26 @@ static void tile_stats_general(const uint16_t* Qh /*[GH][D] raw*/, const uint16_
   for (int g = 0; g < GH; ++g)
     for (int d = 0; d < SO_D; ++d) {
       const float qv = ld16(Qh, (size_t)g * SO_D + d, is_bf16) * q_scale;
-      qr[g * SO_D + d] = ld16((const uint16_t[]){st16(qv, is_bf16)}, 0, is_bf16);
+      const uint16_t qb = st16(qv, is_bf16);
+      qr[g * SO_D + d] = ld16(&qb, 0, is_bf16);
     }
   for (int g = 0; g < GH; ++g) ts->m[g] = -INFINITY;
   for (int r = 0; r < len; ++r) {
     const uint16_t* krow = K + row0_off + (size_t)r * row_stride;
+    float kf[SO_D];
+    for (int d = 0; d < SO_D; ++d) kf[d] = ld16(krow, (size_t)d, is_bf16);
     for (int g = 0; g < GH; ++g) {
-      double s = 0.0;
-      for (int d = 0; d < SO_D; ++d) s += (double)qr[g * SO_D + d] * (double)ld16(krow, (size_t)d, is_bf16);
-      const float sf = (float)s;
+      const float* q = qr + (size_t)g * SO_D;
+      float lanes[SO_LANES];
+      for (int l = 0; l < SO_LANES; ++l) {
+        float sl = 0.0f;
+        sl = fmaf(q[4 * l + 0], kf[4 * l + 0], sl);
+        sl = fmaf(q[4 * l + 1], kf[4 * l + 1], sl);
+        sl = fmaf(q[4 * l + 2], kf[4 * l + 2], sl);
+        sl = fmaf(q[4 * l + 3], kf[4 * l + 3], sl);
+        lanes[l] = sl;
+      }
+      const float sf = lane_tree_down(lanes);
       scores[r * GH + g] = sf;
       ts->m[g] = fmaxf(ts->m[g], sf);
     }
@@ -597,8 +609,9 @@ void so_prop_budgets(const float* m_tiles, const float* ell_tiles, int T_c, int 
 }
 
 /* santa_prop decode for one sequence: prop/santa_cuda.cpp:270-352.
- * pass1_mode: 0 = vec path (GH=4, D=128, BN=256, exact association),
- *             1 = general path (q rounded to the storage dtype, tolerance).
+ * pass1_mode: 0 = vec path (GH=4, D=128, BN=256),
+ *             1 = general path (q rounded to the storage dtype after scaling,
+ *                 per-slab ell; see tile_stats_general).
  * Layouts: q [H,128]; K,V [L,KVH,128]. Optional outputs may be NULL:
  *   m_tiles, ell_tiles, invdelta, a0 [H,T_c]; S_tiles [H,T_c] int32;
  *   u_stash [L,H] 16-bit; counts [H,T_c*BN] int16; rowmask [KVH,L]. */

@@ -1,0 +1,136 @@
+// ext_prop.cpp -- the `santa_prop_batch_cuda` Python extension module for
+// PyTorch-ROCm: the drop-in for the reference's module of the same name
+// (prop/santa_cuda.cpp:270-358).  Input checks and their messages, the
+// SANTA_PASS1 environment switch (read on every call), the block_n
+// normalization and the return tuple follow the reference; the launches go
+// through the C ABI of libsanta_amd.so on the current HIP stream.
+#include <torch/extension.h>
+#include <c10/core/DeviceGuard.h>
+#include <c10/hip/HIPStream.h>
+
+#include <cstdint>
+#include <cstdlib>
+#include <tuple>
+
+#include "santa_amd.h"
+
+namespace {
+
+// prop/santa_cuda.cpp:144-166
+void check_inputs_q_kv(const at::Tensor& q_h, const at::Tensor& K_g, const at::Tensor& V_g) {
+  TORCH_CHECK(q_h.is_cuda(), "q_h must be CUDA");
+  TORCH_CHECK(K_g.is_cuda() && V_g.is_cuda(), "K_g and V_g must be CUDA");
+  TORCH_CHECK((q_h.scalar_type() == at::kBFloat16 || q_h.scalar_type() == at::kHalf), "q_h must be bf16 or f16");
+  TORCH_CHECK((K_g.scalar_type() == at::kBFloat16 || K_g.scalar_type() == at::kHalf) &&
+                  K_g.scalar_type() == V_g.scalar_type(),
+              "K_g/V_g must be bf16 or f16 and match");
+  TORCH_CHECK(q_h.scalar_type() == K_g.scalar_type(), "q_h dtype must match K_g/V_g");
+  TORCH_CHECK(q_h.dim() == 2 && K_g.dim() == 3 && V_g.dim() == 3, "bad ranks");
+  TORCH_CHECK(q_h.device() == K_g.device() && q_h.device() == V_g.device(), "device mismatch");
+  TORCH_CHECK(K_g.size(0) == V_g.size(0) && K_g.size(1) == V_g.size(1) && K_g.size(2) == V_g.size(2),
+              "K_g and V_g must have the same shape");
+  TORCH_CHECK(q_h.size(1) == K_g.size(2), "D mismatch (q_h.size(1) vs K_g.size(2))");
+  TORCH_CHECK(K_g.size(1) > 0 && q_h.size(0) % K_g.size(1) == 0,
+              "H must be divisible by KVH (expected KVH == K_g.size(1) for NHD)");
+  TORCH_CHECK(K_g.is_contiguous() && V_g.is_contiguous(), "K_g/V_g must be contiguous with layout [L, KVH, D] (NHD)");
+}
+
+struct Plan {
+  int H, D, L, KVH, bn, T_c, path, dtype;
+};
+
+Plan plan_call(const at::Tensor& q_h, const at::Tensor& K_g, const at::Tensor& V_g, int64_t block_n) {
+  check_inputs_q_kv(q_h, K_g, V_g);
+  Plan p{};
+  p.H = static_cast<int>(q_h.size(0));
+  p.D = static_cast<int>(q_h.size(1));
+  p.L = static_cast<int>(K_g.size(0));
+  p.KVH = static_cast<int>(K_g.size(1));
+  const int rc = santa_prop_plan(p.L, p.H, p.KVH, p.D, block_n, std::getenv("SANTA_PASS1"), &p.bn, &p.T_c, &p.path);
+  TORCH_CHECK(rc == SANTA_OK, santa_last_error());
+  p.dtype = (q_h.scalar_type() == at::kBFloat16) ? SANTA_BF16 : SANTA_F16;
+  TORCH_CHECK(reinterpret_cast<uintptr_t>(V_g.data_ptr()) % 4 == 0 && reinterpret_cast<uintptr_t>(K_g.data_ptr()) % 16 == 0,
+              "K_g/V_g storage must be 16-byte aligned");
+  return p;
+}
+
+at::Tensor aligned_q(const at::Tensor& q_h) {
+  at::Tensor q = q_h.contiguous();
+  if (reinterpret_cast<uintptr_t>(q.data_ptr()) % 8 != 0) q = q.clone();
+  return q;
+}
+
+hipStream_t current_stream(const at::Tensor& t) {
+  return c10::hip::getCurrentHIPStream(t.device().index()).stream();
+}
+
+// Returns (out [H,D] in q's dtype, m_star [H] f32, vrows [KVH] i32 or [0]).
+std::tuple<at::Tensor, at::Tensor, at::Tensor> decode_systematic_scalar(at::Tensor q_h, at::Tensor K_g,
+                                                                        at::Tensor V_g, int64_t S, uint64_t seed,
+                                                                        int64_t block_n, bool want_vrows) {
+  const Plan p = plan_call(q_h, K_g, V_g, block_n);
+  c10::DeviceGuard guard(q_h.device());
+  const at::Tensor q = aligned_q(q_h);
+  auto optsF = q.options().dtype(at::kFloat);
+  auto optsI = q.options().dtype(at::kInt);
+  at::Tensor out = at::empty({p.H, p.D}, q.options());
+  at::Tensor m_star = at::empty({p.H}, optsF);
+  at::Tensor vrows = want_vrows ? at::empty({p.KVH}, optsI) : at::empty({0}, optsI);
+  const size_t ws_bytes = santa_prop_workspace_size(p.H, p.KVH, p.D, p.L, p.T_c);
+  at::Tensor ws = at::empty({static_cast<int64_t>(ws_bytes)}, q.options().dtype(at::kByte));
+  const int rc = santa_prop_decode(q.data_ptr(), K_g.data_ptr(), V_g.data_ptr(), p.dtype, p.H, p.KVH, p.D, p.L, p.bn,
+                                   p.path, static_cast<int>(S), seed, out.data_ptr(), m_star.data_ptr<float>(),
+                                   want_vrows ? vrows.data_ptr<int>() : nullptr, ws.data_ptr(), ws_bytes,
+                                   current_stream(q));
+  TORCH_CHECK(rc == SANTA_OK, santa_last_error());
+  return std::make_tuple(out, m_star, vrows);
+}
+
+// Test-only: every intermediate of one call through the three stage entry
+// points.  Returns (m_tiles [H,T_c], ell_tiles, m_star [H], S_tiles [H,T_c]
+// i32, invdelta, a0, u_stash [L,H] (q dtype), counts [H,T_c,block_n] i16,
+// out [H,D], vrows [KVH]).
+std::vector<at::Tensor> debug_pass(at::Tensor q_h, at::Tensor K_g, at::Tensor V_g, int64_t S, uint64_t seed,
+                                   int64_t block_n) {
+  const Plan p = plan_call(q_h, K_g, V_g, block_n);
+  c10::DeviceGuard guard(q_h.device());
+  const at::Tensor q = aligned_q(q_h);
+  auto optsF = q.options().dtype(at::kFloat);
+  auto optsI = q.options().dtype(at::kInt);
+  at::Tensor m_tiles = at::empty({p.H, p.T_c}, optsF);
+  at::Tensor ell_tiles = at::empty({p.H, p.T_c}, optsF);
+  at::Tensor m_star = at::empty({p.H}, optsF);
+  at::Tensor S_tiles = at::empty({p.H, p.T_c}, optsI);
+  at::Tensor invdelta = at::empty({p.H, p.T_c}, optsF);
+  at::Tensor a0 = at::empty({p.H, p.T_c}, optsF);
+  at::Tensor stash = at::empty({p.L, p.H}, q.options());
+  at::Tensor counts = at::empty({p.H, p.T_c, p.bn}, q.options().dtype(at::kShort));
+  at::Tensor out = at::empty({p.H, p.D}, q.options());
+  at::Tensor vrows = at::empty({p.KVH}, optsI);
+  const size_t ws_bytes = santa_prop_workspace_size(p.H, p.KVH, p.D, p.L, p.T_c);
+  at::Tensor ws = at::empty({static_cast<int64_t>(ws_bytes)}, q.options().dtype(at::kByte));
+  hipStream_t st = current_stream(q);
+  int rc = santa_prop_pass1(q.data_ptr(), K_g.data_ptr(), p.dtype, p.H, p.KVH, p.D, p.L, p.bn, p.path,
+                            m_tiles.data_ptr<float>(), ell_tiles.data_ptr<float>(), stash.data_ptr(), st);
+  TORCH_CHECK(rc == SANTA_OK, santa_last_error());
+  rc = santa_prop_tile_budgets(m_tiles.data_ptr<float>(), ell_tiles.data_ptr<float>(), p.H, p.T_c,
+                               static_cast<int>(S), seed, m_star.data_ptr<float>(), S_tiles.data_ptr<int>(),
+                               invdelta.data_ptr<float>(), a0.data_ptr<float>(), st);
+  TORCH_CHECK(rc == SANTA_OK, santa_last_error());
+  rc = santa_prop_pass2(V_g.data_ptr(), stash.data_ptr(), p.dtype, p.H, p.KVH, p.D, p.L, p.bn, static_cast<int>(S),
+                        invdelta.data_ptr<float>(), a0.data_ptr<float>(), counts.data_ptr<int16_t>(), out.data_ptr(),
+                        vrows.data_ptr<int>(), ws.data_ptr(), ws_bytes, st);
+  TORCH_CHECK(rc == SANTA_OK, santa_last_error());
+  return {m_tiles, ell_tiles, m_star, S_tiles, invdelta, a0, stash, counts, out, vrows};
+}
+
+}  // namespace
+
+PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
+  m.doc() = "S^2ANTA-Prop sampled-attention decode for MI355X (gfx950)";
+  m.def("decode_systematic_scalar", &decode_systematic_scalar, py::arg("q_h"), py::arg("K_g"), py::arg("V_g"),
+        py::arg("S"), py::arg("seed") = 42ULL, py::arg("block_n") = 0, py::arg("want_vrows") = false);
+  m.def("_debug_pass", &debug_pass, py::arg("q_h"), py::arg("K_g"), py::arg("V_g"), py::arg("S"),
+        py::arg("seed") = 42ULL, py::arg("block_n") = 0);
+  m.def("_library_version", []() { return std::string(santa_version()); });
+}

@@ -168,6 +168,68 @@ __device__ __forceinline__ float wave_max_dpp(float v) {
   return fmaxf(fmaxf(m0, m1), fmaxf(m2, m3));
 }
 
+// ------------------------------------------------------ systematic counts
+// Counts of one head over one tile of len <= 32 * NCH rows (A.5-A.7 of the
+// sampler, flash/santa_cuda_kernel.cu:275-311; prop/santa_cuda_kernel.cu:
+// 771-807).  Rows are held two per lane: lane 16j+q of register pair p holds
+// rows 32(4p+j)+2q (x0) and 32(4p+j)+2q+1 (x1), so every step of the 32-row
+// Hillis-Steele scan (offsets 1, 2, 4, 8, 16) stays inside one 16-lane DPP
+// row and pairs the same elements as the reference's 32-lane scan
+// (flash/santa_cuda_kernel.cu:60-69).  x = f32(u16) * invdel, 0 past len.
+// The 32-row chunk totals (pre + x at the chunk's last row) are carried
+// sequentially; c = floor(a0 + pre + x) - floor(a0 + pre) clamped to
+// [0, 32767].
+template <int NCH, int NP = (NCH + 3) / 4>
+__device__ __forceinline__ void systematic_counts(const float (&x0)[NP], const float (&x1)[NP], int len, float a0,
+                                                  int lane, int (&c0)[NP], int (&c1)[NP]) {
+  const int jrow = lane >> 4;
+  const int qq = lane & 15;
+  float r0[NP], r1[NP];
+#pragma unroll
+  for (int p = 0; p < NP; ++p) {
+    r1[p] = x1[p] + x0[p];
+    r0[p] = x0[p] + dpp_shr_zero<1>(x1[p]);
+  }
+#pragma unroll
+  for (int p = 0; p < NP; ++p) {
+    r0[p] = r0[p] + dpp_shr_zero<1>(r0[p]);
+    r1[p] = r1[p] + dpp_shr_zero<1>(r1[p]);
+    r0[p] = r0[p] + dpp_shr_zero<2>(r0[p]);
+    r1[p] = r1[p] + dpp_shr_zero<2>(r1[p]);
+    r0[p] = r0[p] + dpp_shr_zero<4>(r0[p]);
+    r1[p] = r1[p] + dpp_shr_zero<4>(r1[p]);
+    r0[p] = r0[p] + dpp_shr_zero<8>(r0[p]);
+    r1[p] = r1[p] + dpp_shr_zero<8>(r1[p]);
+  }
+  float carry = 0.0f;
+#pragma unroll
+  for (int p = 0; p < NP; ++p) {
+    const float pre0 = r0[p] - x0[p];
+    const float pre1 = r1[p] - x1[p];
+    const float tot0 = pre0 + x0[p];
+    const float tot1 = pre1 + x1[p];
+    float cj[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int rem = len - 32 * (4 * p + j);
+      cj[j] = carry;
+      if (4 * p + j < NCH && rem > 0) {
+        const int last = min(31, rem - 1);
+        const int src = 16 * j + (last >> 1);
+        const float tot = (last & 1) ? __int_as_float(__builtin_amdgcn_readlane(__float_as_int(tot1), src))
+                                     : __int_as_float(__builtin_amdgcn_readlane(__float_as_int(tot0), src));
+        carry = carry + tot;
+      }
+    }
+    const float car = (jrow == 0) ? cj[0] : (jrow == 1) ? cj[1] : (jrow == 2) ? cj[2] : cj[3];
+    const int row = 32 * (4 * p + jrow) + 2 * qq;
+    const float pg0 = car + pre0;
+    const float pg1 = car + pre1;
+    c0[p] = (row < len) ? count_from_floors(a0, pg0, pg0 + x0[p]) : 0;
+    c1[p] = (row + 1 < len) ? count_from_floors(a0, pg1, pg1 + x1[p]) : 0;
+  }
+}
+
 // Max over the 64 lanes of a wave (exact in any order).
 __device__ __forceinline__ float wave_max(float v) {
 #pragma unroll

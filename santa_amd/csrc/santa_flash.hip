@@ -25,14 +25,18 @@
 //     32-lane-tree / per-warp association (:243-273), the 32-lane trees as
 //     in-wave butterflies.
 //  D  systematic counts (:275-311): each wave owns one head (two for GH=8)
-//     and scans its 256 rows as 64-row blocks of two 32-lane Hillis-Steele
-//     chunks; the reference's sequential cross-chunk carries are wave-uniform
-//     scalars, so no workgroup barrier is needed.
-//  E  the head's sampled rows are the set bits of the blocks' ballots, in
-//     ascending order: the reference's emission list with zero counts
-//     skipped (:314-379) -- so the count-weighted V sum reads the rows
-//     straight from the masks, fma per element in ascending row order.
+//     and scans the tile two rows per lane (systematic_counts), the
+//     reference's sequential cross-chunk carries as wave-uniform scalars, so
+//     no workgroup barrier is needed.
+//  E  the head's sampled rows, in ascending order (ballot prefix counts),
+//     go to a wave-private LDS list: the reference's emission list with zero
+//     counts skipped (:314-379).  The count-weighted V sum gathers the
+//     listed rows, fma per element in ascending row order.
 //  Two workgroup barriers per tile.
+//
+// The same kernel runs santa_prop's pass 1 (modes kPass1Vec / kPass1Gen):
+// phases A-C, then the tile's m, ell and the 16-bit u stash [L, H]
+// (prop/santa_cuda_kernel.cu:87-267, 278-441).
 //
 // Outputs.  Mode kOnline merges the chunk's tiles on the fly (running max
 // and rescaled mass / numerator per head) into a chunk partial; a small
@@ -50,7 +54,13 @@ constexpr int kD = 128;
 constexpr int kThreads = 256;
 constexpr int kPartStride = kD + 2;  // chunk partial: M, Z, num[128]
 constexpr int kListCap = 128;        // sampled rows buffered per head before a gather (>= 2 x 64)
-enum Mode : int { kPerTile = 0, kOnline = 1 };
+// kPerTile / kOnline: santa_flash.  kPass1Vec: santa_prop pass 1 with the
+// vec kernel's numerics (= the flash tile statistics).  kPass1Gen: santa_prop
+// pass 1 of the general path: q rounded to the 16-bit type after scaling and
+// ell summed per 16-row slab, then over slabs (the reference's WMMA kernel,
+// prop/santa_cuda_kernel.cu:121-140,225-262); scores keep the vec
+// association, one fixed order for what the reference leaves to its MMA.
+enum Mode : int { kPerTile = 0, kOnline = 1, kPass1Vec = 2, kPass1Gen = 3 };
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
@@ -131,7 +141,7 @@ __global__ __launch_bounds__(kThreads, 2) void tile_kernel(
     int L_valid, int L_storage, int T_c, int cs, int cpg, float q_scale, int S_pt, uint64_t seed,
     float* __restrict__ m_tiles, float* __restrict__ ell_tiles, float* __restrict__ out_tiles,
     int* __restrict__ emit_cnt, int16_t* __restrict__ dbg_counts, float* __restrict__ part,
-    int* __restrict__ part_emit) {
+    int* __restrict__ part_emit, uint16_t* __restrict__ u_stash) {
   static_assert(BN == 32 || BN == 64 || BN == 256, "block_n");
   static_assert(GH == 4 || GH == 8, "group size");
   constexpr int NT_REF = (BN == 256) ? 256 : 128;  // reference block size (launchers :521,:559)
@@ -140,7 +150,10 @@ __global__ __launch_bounds__(kThreads, 2) void tile_kernel(
   constexpr int NCH = BN / 32;                     // 32-row scan chunks
   constexpr int NPAIR = (NCH + 3) / 4;             // two-rows-per-lane scan registers
   constexpr int KC = BN * GH / NT_REF;             // (row, head) items per reference thread
-  constexpr int LCAP = (MODE == kOnline) ? kListCap : BN;  // sampled rows buffered per head
+  constexpr bool PASS1 = (MODE == kPass1Vec || MODE == kPass1Gen);
+  constexpr int NSLAB = BN / 16;                   // 16-row slabs of the general pass 1
+  constexpr int NWS = (MODE == kPass1Gen) ? NSLAB : NW_REF;  // ell partials per head
+  constexpr int LCAP = (MODE == kOnline) ? kListCap : (PASS1 ? 1 : BN);  // sampled rows buffered per head
 
   const int wg = static_cast<int>(blockIdx.x);
   const int bk = wg / cpg;  // b * KVH + kv
@@ -158,7 +171,7 @@ __global__ __launch_bounds__(kThreads, 2) void tile_kernel(
   __shared__ float s_sc[BN * GH];          // scores, [row][head]
   __shared__ uint16_t s_ub[GH * BN];       // 16-bit u, [head][row]
   __shared__ float s_wmax[4 * GH];
-  __shared__ float s_W[NW_REF * GH];
+  __shared__ float s_W[NWS * GH];
   __shared__ uint64_t s_mask[GH * NPAIR * 2];
 
   const size_t row_stride = static_cast<size_t>(KVH) * kD;
@@ -202,7 +215,10 @@ __global__ __launch_bounds__(kThreads, 2) void tile_kernel(
   for (int hb = 0; hb < NHB; ++hb) {
     const uint16_t* qh = Q + (static_cast<size_t>(b) * H + h0 + 4 * hb + (lane & 3)) * kD + (lane >> 2);
 #pragma unroll
-    for (int m = 0; m < 8; ++m) qa[hb][m] = h16_to_f32<BF16>(qh[16 * m]) * q_scale;
+    for (int m = 0; m < 8; ++m) {
+      qa[hb][m] = h16_to_f32<BF16>(qh[16 * m]) * q_scale;
+      if constexpr (MODE == kPass1Gen) qa[hb][m] = h16_to_f32<BF16>(f32_to_h16<BF16>(qa[hb][m]));
+    }
   }
   // K staging: wave w's 64 rows, row r chunk c (16 B) at slot r*16 + (c ^ (r & 15)).
   __shared__ u32x4 s_k[4 * 64 * 16];
@@ -324,8 +340,28 @@ __global__ __launch_bounds__(kThreads, 2) void tile_kernel(
     }
 
     // ---- C: u, 16-bit u and ell partials (A.4) ---------------------------------
-    // Thread tid plays the reference's thread tid: items idx = tid + NT_REF k.
-    if (tid < NT_REF) {
+    if constexpr (MODE == kPass1Gen) {
+      // thread (slab w, head g): the slab's 16 rows in order
+      if (tid < NSLAB * GH) {
+        const int g = tid % GH;
+        const int w = tid / GH;
+        float mg = s_wmax[g];
+#pragma unroll
+        for (int ww = 1; ww < 4; ++ww) mg = fmaxf(mg, s_wmax[ww * GH + g]);
+        float part_ell = 0.0f;
+#pragma unroll
+        for (int j = 0; j < 16; ++j) {
+          const int r = 16 * w + j;
+          if (r < len) {
+            const float u = santa_expf(s_sc[r * GH + g] - mg);
+            part_ell += u;
+            s_ub[g * BN + r] = f32_to_h16<BF16>(u);
+          }
+        }
+        s_W[w * GH + g] = part_ell;
+      }
+    } else if (tid < NT_REF) {
+      // Thread tid plays the reference's thread tid: items idx = tid + NT_REF k.
       const int g = tid % GH;
       float mg = s_wmax[g];
 #pragma unroll
@@ -354,6 +390,42 @@ __global__ __launch_bounds__(kThreads, 2) void tile_kernel(
     }
     __syncthreads();  // (2) 16-bit u and warp masses visible
 
+    if constexpr (PASS1) {
+      // tile statistics and the 16-bit u of every (row, head) of the group
+#pragma unroll
+      for (int k = 0; k < HPW; ++k) {
+        const int g = wave + 4 * k;
+        float mg = s_wmax[g];
+#pragma unroll
+        for (int w = 1; w < 4; ++w) mg = fmaxf(mg, s_wmax[w * GH + g]);
+        float ell = 0.0f;
+#pragma unroll
+        for (int w = 0; w < NWS; ++w) ell += s_W[w * GH + g];
+        if (lane == 0) {
+          const size_t mt = (static_cast<size_t>(b) * H + h0 + g) * T_c + t;
+          m_tiles[mt] = mg;
+          ell_tiles[mt] = ell;
+        }
+      }
+      if (tid < len) {
+        uint16_t* dst = u_stash + (static_cast<size_t>(b) * L_storage + n0 + tid) * H + h0;
+        if constexpr (GH == 4) {
+          uint2 w;
+          w.x = s_ub[0 * BN + tid] | (static_cast<uint32_t>(s_ub[1 * BN + tid]) << 16);
+          w.y = s_ub[2 * BN + tid] | (static_cast<uint32_t>(s_ub[3 * BN + tid]) << 16);
+          *reinterpret_cast<uint2*>(dst) = w;
+        } else {
+          uint4 w;
+          w.x = s_ub[0 * BN + tid] | (static_cast<uint32_t>(s_ub[1 * BN + tid]) << 16);
+          w.y = s_ub[2 * BN + tid] | (static_cast<uint32_t>(s_ub[3 * BN + tid]) << 16);
+          w.z = s_ub[4 * BN + tid] | (static_cast<uint32_t>(s_ub[5 * BN + tid]) << 16);
+          w.w = s_ub[6 * BN + tid] | (static_cast<uint32_t>(s_ub[7 * BN + tid]) << 16);
+          *reinterpret_cast<uint4*>(dst) = w;
+        }
+      }
+      continue;
+    }
+
     // ---- D/E: per-head counts, sample lists -------------------------------------
 #pragma unroll
     for (int k = 0; k < HPW; ++k) {
@@ -368,66 +440,23 @@ __global__ __launch_bounds__(kThreads, 2) void tile_kernel(
       const float invdel = (S_pt > 0 && ell > 1e-20f) ? (static_cast<float>(S_pt) / ell) : 0.0f;
       const float a0 = u01(seed, b * H + h, t);
 
-      // 32-row chunks, two rows per lane: lane 16j+q of pair p holds rows
-      // 32(4p+j) + 2q and +1, so every Hillis-Steele step (offsets 1..16)
-      // stays inside a 16-lane DPP row; same pairing as the reference's
-      // 32-lane scan (flash/santa_cuda_kernel.cu:60-69).
+      // rows two per lane, in the layout systematic_counts takes
       const int jrow = lane >> 4;
       const int qq = lane & 15;
-      float x0[NPAIR], x1[NPAIR], r0[NPAIR], r1[NPAIR];
+      float x0[NPAIR], x1[NPAIR];
 #pragma unroll
       for (int pp = 0; pp < NPAIR; ++pp) {
         const int row = 32 * (4 * pp + jrow) + 2 * qq;
         const uint32_t w2 = (BN >= 128 || row < BN) ? *reinterpret_cast<const uint32_t*>(s_ub + g * BN + row) : 0u;
         x0[pp] = (row < len && invdel > 0.0f) ? lo16_to_f32<BF16>(w2) * invdel : 0.0f;
         x1[pp] = (row + 1 < len && invdel > 0.0f) ? hi16_to_f32<BF16>(w2) * invdel : 0.0f;
-        r1[pp] = x1[pp] + x0[pp];
-        r0[pp] = x0[pp] + dpp_shr_zero<1>(x1[pp]);
-      }
-#pragma unroll
-      for (int pp = 0; pp < NPAIR; ++pp) {
-        r0[pp] = r0[pp] + dpp_shr_zero<1>(r0[pp]);
-        r1[pp] = r1[pp] + dpp_shr_zero<1>(r1[pp]);
-        r0[pp] = r0[pp] + dpp_shr_zero<2>(r0[pp]);
-        r1[pp] = r1[pp] + dpp_shr_zero<2>(r1[pp]);
-        r0[pp] = r0[pp] + dpp_shr_zero<4>(r0[pp]);
-        r1[pp] = r1[pp] + dpp_shr_zero<4>(r1[pp]);
-        r0[pp] = r0[pp] + dpp_shr_zero<8>(r0[pp]);
-        r1[pp] = r1[pp] + dpp_shr_zero<8>(r1[pp]);
-      }
-      // exclusive prefixes and the reference's sequential cross-chunk carries
-      float pre0[NPAIR], pre1[NPAIR], car[NPAIR];
-      float carry = 0.0f;
-#pragma unroll
-      for (int pp = 0; pp < NPAIR; ++pp) {
-        pre0[pp] = r0[pp] - x0[pp];
-        pre1[pp] = r1[pp] - x1[pp];
-        const float tot0 = pre0[pp] + x0[pp];
-        const float tot1 = pre1[pp] + x1[pp];
-        float cj[4];
-#pragma unroll
-        for (int jj = 0; jj < 4; ++jj) {
-          const int rem = len - 32 * (4 * pp + jj);
-          cj[jj] = carry;
-          if (4 * pp + jj < NCH && rem > 0) {
-            const int last = min(31, rem - 1);
-            const int src = 16 * jj + (last >> 1);
-            const float tot = (last & 1) ? __int_as_float(__builtin_amdgcn_readlane(__float_as_int(tot1), src))
-                                         : __int_as_float(__builtin_amdgcn_readlane(__float_as_int(tot0), src));
-            carry = carry + tot;
-          }
-        }
-        car[pp] = (jrow == 0) ? cj[0] : (jrow == 1) ? cj[1] : (jrow == 2) ? cj[2] : cj[3];
       }
       int c0[NPAIR], c1[NPAIR];
+      systematic_counts<NCH>(x0, x1, len, a0, lane, c0, c1);
       uint64_t nz0[NPAIR], nz1[NPAIR];
 #pragma unroll
       for (int pp = 0; pp < NPAIR; ++pp) {
         const int row = 32 * (4 * pp + jrow) + 2 * qq;
-        const float pg0 = car[pp] + pre0[pp];
-        const float pg1 = car[pp] + pre1[pp];
-        c0[pp] = (row < len) ? count_from_floors(a0, pg0, pg0 + x0[pp]) : 0;
-        c1[pp] = (row + 1 < len) ? count_from_floors(a0, pg1, pg1 + x1[pp]) : 0;
         nz0[pp] = __ballot(c0[pp] != 0);
         nz1[pp] = __ballot(c1[pp] != 0);
         if (lane == 0) {
@@ -657,6 +686,7 @@ struct Args {
   float* part;
   int* part_emit;
   int cs, cpg;
+  uint16_t* u_stash;
 };
 
 template <bool BF16, int GH, int BN, int MODE>
@@ -667,7 +697,7 @@ static hipError_t launch_t(const Args& a, hipStream_t stream) {
                      static_cast<const uint16_t*>(a.q), static_cast<const uint16_t*>(a.K),
                      static_cast<const uint16_t*>(a.V), a.H, a.KVH, a.L_valid, a.L_storage, a.T_c, a.cs, a.cpg,
                      q_scale, a.S_pt, a.seed, a.m_tiles, a.ell_tiles, a.out_tiles, a.emit_cnt, a.counts, a.part,
-                     a.part_emit);
+                     a.part_emit, a.u_stash);
   return hipGetLastError();
 }
 
@@ -717,6 +747,28 @@ static void chunk_plan(int B, int KVH, int T_c, int* cs, int* cpg) {
   *cs = c;
   *cpg = (T_c + c - 1) / c;
 }
+
+// santa_prop pass 1 on the tile kernel (declared in santa_internal.h).
+hipError_t launch_prop_pass1(const void* q, const void* K, int dtype, int B, int H, int KVH, int L, int L_storage,
+                             int block_n, int path, float* m_tiles, float* ell_tiles, uint16_t* u_stash,
+                             hipStream_t stream) {
+  Args a{q, K, nullptr, B, H, KVH, L, L_storage, (L + block_n - 1) / block_n, 0, 0, m_tiles, ell_tiles, nullptr,
+         nullptr, nullptr, nullptr, nullptr, 0, 0, u_stash};
+  chunk_plan(B, KVH, a.T_c, &a.cs, &a.cpg);
+  const int GH = H / KVH;
+  if (path == 0) {
+    return (dtype == SANTA_BF16) ? launch_t<true, 4, 256, kPass1Vec>(a, stream)
+                                 : launch_t<false, 4, 256, kPass1Vec>(a, stream);
+  }
+  if (dtype == SANTA_BF16)
+    return (GH == 4) ? launch_bn<true, 4, kPass1Gen>(block_n, a, stream)
+                     : launch_bn<true, 8, kPass1Gen>(block_n, a, stream);
+  return (GH == 4) ? launch_bn<false, 4, kPass1Gen>(block_n, a, stream)
+                   : launch_bn<false, 8, kPass1Gen>(block_n, a, stream);
+}
+
+// Tile chunking shared with santa_prop's pass 2.
+void plan_chunks(int B, int KVH, int T_c, int* cs, int* cpg) { chunk_plan(B, KVH, T_c, cs, cpg); }
 
 }  // namespace flash
 }  // namespace santa
@@ -777,7 +829,7 @@ extern "C" int santa_flash_fused_tiles(const void* q, const void* K, const void*
   if (!q || !K || !V || !m_tiles || !ell_tiles || !out_tiles || !emit_cnt)
     return set_error(SANTA_ERR_INVALID, "null pointer argument");
   flash::Args a{q, K, V, B, H, KVH, L_valid, L_storage, (L_valid + block_n - 1) / block_n, S_per_tile, seed,
-                m_tiles, ell_tiles, out_tiles, emit_cnt, counts, nullptr, nullptr, 0, 0};
+                m_tiles, ell_tiles, out_tiles, emit_cnt, counts, nullptr, nullptr, 0, 0, nullptr};
   flash::chunk_plan(B, KVH, a.T_c, &a.cs, &a.cpg);
   hipError_t e = flash::launch_tiles<flash::kPerTile>(dtype, H / KVH, block_n, a, stream);
   if (e != hipSuccess) return set_error(SANTA_ERR_HIP, "fused tile launch failed: %s", hipGetErrorString(e));
@@ -852,7 +904,8 @@ extern "C" int santa_flash_decode_tiles(const void* q, const void* K, const void
   if ((st = flash_ws_check(B, H, KVH, T_c, workspace, workspace_bytes, &w)) != SANTA_OK) return st;
   char* base = static_cast<char*>(workspace);
   flash::Args a{q, K, V, B, H, KVH, L_valid, L_storage, T_c, S_per_tile, seed, nullptr, nullptr, nullptr, nullptr,
-                nullptr, reinterpret_cast<float*>(base + w.part), reinterpret_cast<int*>(base + w.emit), w.cs, w.cpg};
+                nullptr, reinterpret_cast<float*>(base + w.part), reinterpret_cast<int*>(base + w.emit), w.cs, w.cpg,
+                nullptr};
   const hipError_t e = flash::launch_tiles<flash::kOnline>(dtype, H / KVH, block_n, a, stream);
   if (e != hipSuccess) return set_error(SANTA_ERR_HIP, "tile launch failed: %s", hipGetErrorString(e));
   return clear_error();

@@ -2,6 +2,8 @@
 #pragma once
 
 #include <stddef.h>
+#include <stdint.h>
+#include <hip/hip_runtime_api.h>
 
 namespace santa {
 
@@ -13,5 +15,17 @@ int clear_error();
 
 constexpr size_t kWsAlign = 256;
 inline size_t align_up(size_t x) { return (x + kWsAlign - 1) & ~(kWsAlign - 1); }
+
+namespace flash {
+// santa_prop pass 1 on the flash tile kernel: per-tile m, ell [B, H, T_c] and
+// the 16-bit u stash [B, L_storage, H].  path 0 = vec numerics (GH 4,
+// block_n 256), 1 = general numerics.  Shapes are checked by the caller.
+hipError_t launch_prop_pass1(const void* q, const void* K, int dtype, int B, int H, int KVH, int L, int L_storage,
+                             int block_n, int path, float* m_tiles, float* ell_tiles, uint16_t* u_stash,
+                             hipStream_t stream);
+// Chunks of cs tiles per workgroup, cpg chunks per (b, kv) group, sized to
+// about one resident round of 256-thread workgroups on the current device.
+void plan_chunks(int B, int KVH, int T_c, int* cs, int* cpg);
+}  // namespace flash
 
 }  // namespace santa

@@ -1,0 +1,634 @@
+// santa_prop.hip -- santa_prop (proportional tile budgets) decode kernels for
+// gfx950, after prop/santa_cuda_kernel.cu and prop/santa_cuda.cpp:270-352.
+//
+// One decode step of one sequence (or of B sequences in the batched form)
+// is four launches on one stream:
+//  1. pass 1 (the flash tile kernel in a pass-1 mode, santa_flash.hip): per
+//     (kv, tile) scores, tile max m_t and mass ell_t per head, and the 16-bit
+//     u = exp(s - m_t) stashed as [L, H] -- all of K is read once here;
+//  2. budgets_kernel: per head, m* = max m_t, W_t = exp(m_t - m*) ell_t and
+//     the largest-remainder split of S over the tiles (the reference's
+//     bitonic network), invdelta_t = S_t / ell_t and a0_t = u01(seed, h, t);
+//  3. pass2_kernel: per (kv, chunk of tiles) workgroup, the systematic counts
+//     of every head from the stash, the sampled rows' count-weighted V sums
+//     accumulated over the chunk (rows ascending, tiles ascending);
+//  4. finalize_kernel: out = dtype(sum over chunks * (1/S)), vrows.
+//
+// Determinism.  The reference sums Z and out with float atomics (order
+// unspecified).  Here Z is 128 per-thread partials (tiles tid, tid+128, ...
+// in order) reduced by a pairwise tree with strides 64 .. 1, and out is a
+// fixed chunk order, so repeated calls give identical bits.  The sampled
+// counts depend only on (m_t, ell_t, u stash), which are bit-exact to the
+// restatement of the reference algorithm.
+#include "santa_device.h"
+#include "santa_amd.h"
+#include "santa_internal.h"
+
+#include <cctype>
+#include <cfloat>
+#include <cstring>
+
+namespace santa {
+namespace prop {
+
+constexpr int kD = 128;
+constexpr int kThreads = 256;
+constexpr int kBudgetThreads = 128;  // the reference's budget block (prop/santa_cuda_kernel.cu:904-915)
+constexpr int kMaxTiles = 4096;      // budgets keep frac, idx and S_t of every tile in LDS
+
+// ---------------------------------------------------------------- budgets
+// prop/santa_cuda_kernel.cu:577-726, one workgroup per (b, h); the RNG key is
+// h (the reference's per-sequence call).  LDS: frac[T_c], idx[T_c], st[T_c].
+__global__ __launch_bounds__(kBudgetThreads) void budgets_kernel(const float* __restrict__ m_tiles,
+                                                                 const float* __restrict__ ell_tiles, int H, int T_c,
+                                                                 int S, uint64_t seed, float* __restrict__ m_star,
+                                                                 int* __restrict__ S_tiles,
+                                                                 float* __restrict__ invdelta,
+                                                                 float* __restrict__ a0_tile) {
+  extern __shared__ float smem[];
+  float* frac = smem;
+  int* idx = reinterpret_cast<int*>(smem + T_c);
+  int* st = idx + T_c;
+  __shared__ float red[kBudgetThreads];
+  __shared__ int ired[kBudgetThreads];
+
+  const int bh = static_cast<int>(blockIdx.x);
+  const int h = bh % H;
+  const int tid = static_cast<int>(threadIdx.x);
+  const size_t off = static_cast<size_t>(bh) * T_c;
+  const float* mt = m_tiles + off;
+  const float* lt = ell_tiles + off;
+
+  // m* = max_t m_t (exact in any order); -FLT_MAX start as in :597
+  float lm = -FLT_MAX;
+  for (int t = tid; t < T_c; t += kBudgetThreads) lm = fmaxf(lm, mt[t]);
+  red[tid] = lm;
+  __syncthreads();
+  for (int s = kBudgetThreads / 2; s > 0; s >>= 1) {
+    if (tid < s) red[tid] = fmaxf(red[tid], red[tid + s]);
+    __syncthreads();
+  }
+  const float ms = red[0];
+  __syncthreads();
+  if (tid == 0 && m_star) m_star[bh] = ms;
+
+  // W_t and Z in the fixed order
+  float z = 0.0f;
+  for (int t = tid; t < T_c; t += kBudgetThreads) {
+    const float wt = santa_expf(mt[t] - ms) * lt[t];
+    frac[t] = wt;
+    z += wt;
+  }
+  red[tid] = z;
+  __syncthreads();
+  for (int s = kBudgetThreads / 2; s > 0; s >>= 1) {
+    if (tid < s) red[tid] = red[tid] + red[tid + s];
+    __syncthreads();
+  }
+  const float Z = red[0];
+
+  if (S <= 0 || !(Z > 0.0f)) {
+    for (int t = tid; t < T_c; t += kBudgetThreads) {
+      S_tiles[off + t] = 0;
+      invdelta[off + t] = 0.0f;
+      a0_tile[off + t] = u01(seed, h, t);
+    }
+    return;
+  }
+
+  // integer bases and jittered fractional parts (:662-678)
+  int base = 0;
+  for (int t = tid; t < T_c; t += kBudgetThreads) {
+    const float q = static_cast<float>(S) * (frac[t] / Z);
+    const float fq = floorf(q);
+    const int bt = (fq != fq) ? 0 : (fq >= 2147483648.0f ? 2147483647 : static_cast<int>(fq));
+    st[t] = bt;
+    base += bt;
+    const float ft = q - static_cast<float>(bt);
+    const float jitter = 1.0e-7f * u01(seed, h, t);
+    frac[t] = ft + jitter;
+    idx[t] = t;
+  }
+  ired[tid] = base;
+  __syncthreads();
+  for (int s = kBudgetThreads / 2; s > 0; s >>= 1) {
+    if (tid < s) ired[tid] += ired[tid + s];
+    __syncthreads();
+  }
+  int rem = S - ired[0];
+  if (rem < 0) rem = 0;
+  if (rem > T_c) rem = T_c;
+
+  // bitonic network over N = next power of two >= T_c, descending; reads
+  // past T_c see (-inf, -1) and writes past T_c are dropped (:686-707)
+  int N = 1;
+  while (N < T_c) N <<= 1;
+  for (int k = 2; k <= N; k <<= 1) {
+    for (int j = k >> 1; j > 0; j >>= 1) {
+      for (int i = tid; i < N; i += kBudgetThreads) {
+        const int ixj = i ^ j;
+        if (ixj > i) {
+          const bool up = (i & k) != 0;
+          float ai = (i < T_c) ? frac[i] : -__builtin_inff();
+          float aj = (ixj < T_c) ? frac[ixj] : -__builtin_inff();
+          int ii = (i < T_c) ? idx[i] : -1;
+          int ij = (ixj < T_c) ? idx[ixj] : -1;
+          if ((ai > aj) == up) {
+            const float tf = ai;
+            ai = aj;
+            aj = tf;
+            const int ti = ii;
+            ii = ij;
+            ij = ti;
+          }
+          if (i < T_c) {
+            frac[i] = ai;
+            idx[i] = ii;
+          }
+          if (ixj < T_c) {
+            frac[ixj] = aj;
+            idx[ixj] = ij;
+          }
+        }
+      }
+      __syncthreads();
+    }
+  }
+  // +1 to the top `rem` (distinct tiles, :710-716)
+  for (int r = tid; r < rem; r += kBudgetThreads) {
+    const int best = idx[r];
+    if (best >= 0) st[best] += 1;
+  }
+  __syncthreads();
+  for (int t = tid; t < T_c; t += kBudgetThreads) {
+    const float ell = lt[t];
+    const int s_t = st[t];
+    S_tiles[off + t] = s_t;
+    invdelta[off + t] = (s_t > 0 && ell > 1e-20f) ? (static_cast<float>(s_t) / ell) : 0.0f;
+    a0_tile[off + t] = u01(seed, h, t);
+  }
+}
+
+// Number of rows of a tile sampled by any head of the group (union of the
+// per-head nonzero masks, one 64-bit mask per lane < NM).
+template <int GH, int NM>
+__device__ __forceinline__ int union_rows(const uint64_t* s_mask, int lane) {
+  int e = 0;
+  if (lane < NM) {
+    uint64_t u = 0;
+#pragma unroll
+    for (int g = 0; g < GH; ++g) u |= s_mask[g * NM + lane];
+    e = __popcll(u);
+  }
+#pragma unroll
+  for (int m = 1; m < NM; m <<= 1) e += __shfl_xor(e, m, 64);
+  return e;
+}
+
+// ---------------------------------------------------------------- pass 2
+// prop/santa_cuda_kernel.cu:734-864.  Workgroup = (b, kv, chunk of cs
+// tiles); wave w owns heads w and w+4.  Per tile and head: x_r = f32(u16
+// stash) * invdelta_t, counts by systematic_counts (the reference's 32-lane
+// scan with carry), the sampled rows in ascending order in a wave-private
+// LDS list, then the count-weighted V rows (fma per element) added to the
+// head's running sum.  The next tile's stash entries are loaded before the
+// current tile's V gather.
+template <bool BF16, int GH, int BN>
+__global__ __launch_bounds__(kThreads) void pass2_kernel(const uint16_t* __restrict__ V,
+                                                         const uint16_t* __restrict__ u_stash, int H, int KVH,
+                                                         int L, int L_storage, int T_c, int cs, int cpg,
+                                                         const float* __restrict__ invdelta,
+                                                         const float* __restrict__ a0_tile,
+                                                         int16_t* __restrict__ dbg_counts, float* __restrict__ part,
+                                                         int* __restrict__ part_emit, int want_emit) {
+  constexpr int NCH = BN / 32;
+  constexpr int NPAIR = (NCH + 3) / 4;
+  constexpr int HPW = GH / 4;
+  constexpr int NM = 2 * NPAIR;  // 64-bit row masks per head and tile
+
+  const int wg = static_cast<int>(blockIdx.x);
+  const int bk = wg / cpg;
+  const int chunk = wg - bk * cpg;
+  const int kv = bk % KVH;
+  const int b = bk / KVH;
+  const int h0 = kv * GH;
+  const int t_begin = chunk * cs;
+  const int t_end = min(T_c, t_begin + cs);
+  const int tid = static_cast<int>(threadIdx.x);
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int jrow = lane >> 4;
+  const int qq = lane & 15;
+
+  __shared__ uint64_t s_mask[2][GH * NM];
+  __shared__ float s_lcw[GH * BN];
+  __shared__ int s_lrow[GH * BN];
+
+  const size_t row_stride = static_cast<size_t>(KVH) * kD;
+  const uint16_t* Vg = V + static_cast<size_t>(b) * L_storage * row_stride + static_cast<size_t>(kv) * kD + 2 * lane;
+  const uint16_t* ub = u_stash + static_cast<size_t>(b) * L_storage * H;
+
+  float acc0[HPW], acc1[HPW];
+#pragma unroll
+  for (int k = 0; k < HPW; ++k) {
+    acc0[k] = 0.0f;
+    acc1[k] = 0.0f;
+  }
+  int emit_total = 0;
+
+  // stash entries of tile t for this lane's rows: u[k][p][0/1]
+  uint16_t un0[HPW][NPAIR], un1[HPW][NPAIR];
+  auto load_u = [&](int t) {
+    const int n0 = t * BN;
+    const int len = min(BN, L - n0);
+#pragma unroll
+    for (int k = 0; k < HPW; ++k) {
+      const int h = h0 + wave + 4 * k;
+#pragma unroll
+      for (int p = 0; p < NPAIR; ++p) {
+        const int row = 32 * (4 * p + jrow) + 2 * qq;
+        un0[k][p] = (row < len) ? ub[static_cast<size_t>(n0 + row) * H + h] : static_cast<uint16_t>(0);
+        un1[k][p] = (row + 1 < len) ? ub[static_cast<size_t>(n0 + row + 1) * H + h] : static_cast<uint16_t>(0);
+      }
+    }
+  };
+  if (t_begin < t_end) load_u(t_begin);
+
+  for (int t = t_begin; t < t_end; ++t) {
+    const int n0 = t * BN;
+    const int len = min(BN, L - n0);
+    const int par = (t - t_begin) & 1;
+    float x0[HPW][NPAIR], x1[HPW][NPAIR], inv[HPW], a0v[HPW];
+#pragma unroll
+    for (int k = 0; k < HPW; ++k) {
+      const size_t ht = (static_cast<size_t>(b) * H + h0 + wave + 4 * k) * T_c + t;
+      inv[k] = invdelta[ht];
+      a0v[k] = a0_tile[ht];
+#pragma unroll
+      for (int p = 0; p < NPAIR; ++p) {
+        x0[k][p] = (inv[k] > 0.0f) ? h16_to_f32<BF16>(un0[k][p]) * inv[k] : 0.0f;
+        x1[k][p] = (inv[k] > 0.0f) ? h16_to_f32<BF16>(un1[k][p]) * inv[k] : 0.0f;
+      }
+    }
+    if (t + 1 < t_end) load_u(t + 1);
+
+#pragma unroll
+    for (int k = 0; k < HPW; ++k) {
+      const int g = wave + 4 * k;
+      const int h = h0 + g;
+      int c0[NPAIR], c1[NPAIR];
+      systematic_counts<NCH>(x0[k], x1[k], len, a0v[k], lane, c0, c1);
+      const uint64_t below = (1ull << lane) - 1ull;
+      int cnt = 0;
+#pragma unroll
+      for (int p = 0; p < NPAIR; ++p) {
+        const int row = 32 * (4 * p + jrow) + 2 * qq;
+        const uint64_t nz0 = __ballot(c0[p] != 0);
+        const uint64_t nz1 = __ballot(c1[p] != 0);
+        if (lane == 0) {
+          s_mask[par][g * NM + 2 * p + 0] = nz0;
+          s_mask[par][g * NM + 2 * p + 1] = nz1;
+        }
+        if (dbg_counts && row < BN) {
+          int16_t* dc = dbg_counts + ((static_cast<size_t>(b) * H + h) * T_c + t) * BN + row;
+          dc[0] = static_cast<int16_t>(c0[p]);
+          dc[1] = static_cast<int16_t>(c1[p]);
+        }
+        const int pos0 = cnt + __popcll(nz0 & below) + __popcll(nz1 & below);
+        const int pos1 = pos0 + (c0[p] != 0 ? 1 : 0);
+        if (c0[p] != 0) {
+          s_lrow[g * BN + pos0] = n0 + row;
+          s_lcw[g * BN + pos0] = static_cast<float>(c0[p]);
+        }
+        if (c1[p] != 0) {
+          s_lrow[g * BN + pos1] = n0 + row + 1;
+          s_lcw[g * BN + pos1] = static_cast<float>(c1[p]);
+        }
+        cnt += __popcll(nz0) + __popcll(nz1);
+      }
+      // count-weighted V rows, ascending, one fma per element (:843-857)
+      for (int base = 0; base < cnt; base += 8) {
+        float cf[8];
+        uint32_t vw[8];
+#pragma unroll
+        for (int q = 0; q < 8; ++q) {
+          const int i = base + q;
+          const bool ok = i < cnt;
+          const int rr = ok ? s_lrow[g * BN + i] : n0;
+          cf[q] = ok ? s_lcw[g * BN + i] : 0.0f;
+          vw[q] = *reinterpret_cast<const uint32_t*>(Vg + static_cast<size_t>(rr) * row_stride);
+        }
+#pragma unroll
+        for (int q = 0; q < 8; ++q) {
+          if (base + q < cnt) {
+            acc0[k] = fmaf(cf[q], lo16_to_f32<BF16>(vw[q]), acc0[k]);
+            acc1[k] = fmaf(cf[q], hi16_to_f32<BF16>(vw[q]), acc1[k]);
+          }
+        }
+      }
+    }
+    if (want_emit) {
+      // masks double-buffered by tile parity: one barrier per tile
+      __syncthreads();
+      if (wave == 0) emit_total += union_rows<GH, NM>(s_mask[par], lane);
+    }
+  }
+
+#pragma unroll
+  for (int k = 0; k < HPW; ++k) {
+    float* pp = part + (static_cast<size_t>(wg) * GH + wave + 4 * k) * kD;
+    reinterpret_cast<float2*>(pp)[lane] = make_float2(acc0[k], acc1[k]);
+  }
+  if (tid == 0) part_emit[wg] = emit_total;
+}
+
+// ---------------------------------------------------------------- finalize
+// out[b, h, :] = dtype((sum over the chunks of (b, kv), ascending) * scale_out)
+// (prop/santa_cuda_kernel.cu:976-985 with the chunk sums in place of the
+// atomics); vrows[b, kv] = rows emitted by any head of the group.
+template <bool BF16, int GH>
+__global__ __launch_bounds__(kD) void finalize_kernel(const float* __restrict__ part,
+                                                      const int* __restrict__ part_emit, int H, int KVH, int cpg,
+                                                      float scale_out, uint16_t* __restrict__ out,
+                                                      int* __restrict__ vrows) {
+  const int bh = static_cast<int>(blockIdx.x);
+  const int b = bh / H;
+  const int h = bh % H;
+  const int kv = h / GH;
+  const int g = h % GH;
+  const int bk = b * KVH + kv;
+  const int d = static_cast<int>(threadIdx.x);
+  const float* pb = part + (static_cast<size_t>(bk) * cpg * GH + g) * kD + d;
+  float s = 0.0f;
+  for (int c = 0; c < cpg; ++c) s += pb[static_cast<size_t>(c) * GH * kD];
+  out[static_cast<size_t>(bh) * kD + d] = f32_to_h16<BF16>(s * scale_out);
+  if (vrows && g == 0 && d == 0) {
+    int e = 0;
+    for (int c = 0; c < cpg; ++c) e += part_emit[static_cast<size_t>(bk) * cpg + c];
+    vrows[bk] = e;
+  }
+}
+
+template <bool BF16, int GH, int BN>
+static hipError_t launch_pass2_t(const uint16_t* V, const uint16_t* u_stash, int B, int H, int KVH, int L,
+                                 int L_storage, int T_c, int cs, int cpg, const float* invdelta, const float* a0,
+                                 int16_t* counts, float* part, int* part_emit, int want_emit, hipStream_t stream) {
+  const unsigned grid = static_cast<unsigned>(B) * static_cast<unsigned>(KVH) * static_cast<unsigned>(cpg);
+  hipLaunchKernelGGL((pass2_kernel<BF16, GH, BN>), dim3(grid), dim3(kThreads), 0, stream, V, u_stash, H, KVH, L,
+                     L_storage, T_c, cs, cpg, invdelta, a0, counts, part, part_emit, want_emit);
+  return hipGetLastError();
+}
+
+template <bool BF16, int GH>
+static hipError_t launch_pass2_bn(int bn, const uint16_t* V, const uint16_t* u_stash, int B, int H, int KVH, int L,
+                                  int L_storage, int T_c, int cs, int cpg, const float* invdelta, const float* a0,
+                                  int16_t* counts, float* part, int* part_emit, int want_emit, hipStream_t stream) {
+  switch (bn) {
+    case 32:
+      return launch_pass2_t<BF16, GH, 32>(V, u_stash, B, H, KVH, L, L_storage, T_c, cs, cpg, invdelta, a0, counts,
+                                          part, part_emit, want_emit, stream);
+    case 64:
+      return launch_pass2_t<BF16, GH, 64>(V, u_stash, B, H, KVH, L, L_storage, T_c, cs, cpg, invdelta, a0, counts,
+                                          part, part_emit, want_emit, stream);
+    default:
+      return launch_pass2_t<BF16, GH, 256>(V, u_stash, B, H, KVH, L, L_storage, T_c, cs, cpg, invdelta, a0, counts,
+                                           part, part_emit, want_emit, stream);
+  }
+}
+
+// Workspace of one decode call (offsets 256-B aligned).
+struct PropWs {
+  size_t m, ell, st, inv, a0, stash, part, emit, total;
+  int cs, cpg;
+};
+static PropWs prop_ws_layout(int B, int H, int KVH, int L_storage, int T_c) {
+  PropWs w{};
+  flash::plan_chunks(B, KVH, T_c, &w.cs, &w.cpg);
+  const size_t bht = static_cast<size_t>(B) * H * T_c;
+  const size_t chunks = static_cast<size_t>(B) * KVH * w.cpg;
+  size_t off = 0;
+  w.m = off;
+  off = align_up(off + bht * sizeof(float));
+  w.ell = off;
+  off = align_up(off + bht * sizeof(float));
+  w.st = off;
+  off = align_up(off + bht * sizeof(int));
+  w.inv = off;
+  off = align_up(off + bht * sizeof(float));
+  w.a0 = off;
+  off = align_up(off + bht * sizeof(float));
+  w.stash = off;
+  off = align_up(off + static_cast<size_t>(B) * L_storage * H * sizeof(uint16_t));
+  w.part = off;
+  off = align_up(off + chunks * (H / KVH) * kD * sizeof(float));
+  w.emit = off;
+  off = align_up(off + chunks * sizeof(int));
+  w.total = off;
+  return w;
+}
+
+// SANTA_PASS1 as the reference reads it (prop/santa_cuda.cpp:39-51):
+// 0 auto, 1 force the general path, 2 force the vec path.
+static int pass1_mode(const char* env) {
+  if (!env) return 0;
+  char s[32];
+  size_t n = 0;
+  for (; env[n] && n + 1 < sizeof(s); ++n) s[n] = static_cast<char>(std::tolower(static_cast<unsigned char>(env[n])));
+  s[n] = 0;
+  if (env[n] != 0) return 0;
+  if (!std::strcmp(s, "gqa") || !std::strcmp(s, "perhead")) return 1;
+  if (!std::strcmp(s, "vec") || !std::strcmp(s, "gqa_vec")) return 2;
+  return 0;
+}
+
+static int check_common(int dtype, int H, int KVH, int D) {
+  if (dtype != SANTA_BF16 && dtype != SANTA_F16) return set_error(SANTA_ERR_INVALID, "q_h must be bf16 or f16");
+  if (H <= 0 || KVH <= 0) return set_error(SANTA_ERR_INVALID, "empty head dimension");
+  if (H % KVH != 0)
+    return set_error(SANTA_ERR_INVALID, "H must be divisible by KVH (expected KVH == K_g.size(1) for NHD)");
+  if (D != kD) return set_error(SANTA_ERR_UNSUPPORTED, "This build supports only D=128. Got D=%d", D);
+  const int GH = H / KVH;
+  if (GH != 4 && GH != 8)
+    return set_error(SANTA_ERR_UNSUPPORTED, "This build supports only GH=4 or GH=8 (H/KVH). Got GH=%d (H=%d KVH=%d)",
+                     GH, H, KVH);
+  return SANTA_OK;
+}
+
+static int check_bn(int block_n, int T_c) {
+  if (!(block_n == 32 || block_n == 64 || block_n == 256))
+    return set_error(SANTA_ERR_UNSUPPORTED, "This build supports block_n in {32,64,256} for santa_prop. Got block_n=%d",
+                     block_n);
+  if (T_c > kMaxTiles)
+    return set_error(SANTA_ERR_UNSUPPORTED, "too many tiles per sequence: T_c=%d (max %d)", T_c, kMaxTiles);
+  return SANTA_OK;
+}
+
+}  // namespace prop
+}  // namespace santa
+
+using namespace santa;
+
+extern "C" int santa_prop_plan(int L, int H, int KVH, int D, int64_t block_n, const char* pass1_env,
+                               int* block_n_out, int* T_c_out, int* pass1_path_out) {
+  const int mode = prop::pass1_mode(pass1_env);
+  int64_t bn = block_n;
+  if (bn <= 0) bn = (mode == 2) ? 256 : ((L <= 1536) ? 32 : ((L <= 3072) ? 64 : 256));
+  if (L <= 0) return set_error(SANTA_ERR_INVALID, "empty KV cache: L=%d", L);
+  if (KVH <= 0 || H % KVH != 0) return set_error(SANTA_ERR_INVALID, "H must be divisible by KVH");
+  const int GH = H / KVH;
+  const bool can_vec = GH == 4 && D == 128 && bn == 256;
+  if (mode == 2 && !can_vec)
+    return set_error(SANTA_ERR_INVALID, "SANTA_PASS1=vec requires GH=4, D=128, block_n=256. Got GH=%d D=%d block_n=%lld",
+                     GH, D, static_cast<long long>(bn));
+  const bool use_vec = (mode == 0 && can_vec) || mode == 2;
+  if (!use_vec && (((D & 15) != 0) || ((bn & 15) != 0)))
+    return set_error(SANTA_ERR_INVALID, "Pass-1 WMMA-GQA requires D %% 16 == 0 and block_n %% 16 == 0. Got D=%d block_n=%lld",
+                     D, static_cast<long long>(bn));
+  const int64_t T_c = (L + bn - 1) / bn;
+  if (block_n_out) *block_n_out = static_cast<int>(bn);
+  if (T_c_out) *T_c_out = static_cast<int>(T_c);
+  if (pass1_path_out) *pass1_path_out = use_vec ? 0 : 1;
+  return clear_error();
+}
+
+extern "C" int santa_prop_pass1(const void* q, const void* K, int dtype, int H, int KVH, int D, int L, int block_n,
+                                int pass1_path, float* m_tiles, float* ell_tiles, void* u_stash, hipStream_t stream) {
+  int st = prop::check_common(dtype, H, KVH, D);
+  if (st != SANTA_OK) return st;
+  if (L <= 0) return set_error(SANTA_ERR_INVALID, "empty KV cache: L=%d", L);
+  const int T_c = (L + block_n - 1) / block_n;
+  if ((st = prop::check_bn(block_n, T_c)) != SANTA_OK) return st;
+  if (pass1_path == 0 && !(H / KVH == 4 && block_n == 256))
+    return set_error(SANTA_ERR_INVALID, "SANTA_PASS1=vec requires GH=4, D=128, block_n=256. Got GH=%d D=%d block_n=%d",
+                     H / KVH, D, block_n);
+  if (!q || !K || !m_tiles || !ell_tiles || !u_stash) return set_error(SANTA_ERR_INVALID, "null pointer argument");
+  const hipError_t e = flash::launch_prop_pass1(q, K, dtype, 1, H, KVH, L, L, block_n, pass1_path, m_tiles, ell_tiles,
+                                                static_cast<uint16_t*>(u_stash), stream);
+  if (e != hipSuccess) return set_error(SANTA_ERR_HIP, "pass-1 launch failed: %s", hipGetErrorString(e));
+  return clear_error();
+}
+
+static int prop_budgets_launch(const float* m_tiles, const float* ell_tiles, int BH, int H, int T_c, int S,
+                               uint64_t seed, float* m_star, int* S_tiles, float* invdelta, float* a0,
+                               hipStream_t stream) {
+  const size_t shmem = static_cast<size_t>(T_c) * (2 * sizeof(float) + sizeof(int));
+  hipLaunchKernelGGL(prop::budgets_kernel, dim3(BH), dim3(prop::kBudgetThreads), shmem, stream, m_tiles, ell_tiles, H,
+                     T_c, S, seed, m_star, S_tiles, invdelta, a0);
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return set_error(SANTA_ERR_HIP, "budget launch failed: %s", hipGetErrorString(e));
+  return SANTA_OK;
+}
+
+extern "C" int santa_prop_tile_budgets(const float* m_tiles, const float* ell_tiles, int H, int T_c, int S,
+                                       uint64_t seed, float* m_star, int* S_tiles, float* invdelta, float* a0,
+                                       hipStream_t stream) {
+  if (H <= 0 || T_c <= 0) return set_error(SANTA_ERR_INVALID, "bad budget shape: H=%d T_c=%d", H, T_c);
+  if (T_c > prop::kMaxTiles)
+    return set_error(SANTA_ERR_UNSUPPORTED, "too many tiles per sequence: T_c=%d (max %d)", T_c, prop::kMaxTiles);
+  if (!m_tiles || !ell_tiles || !S_tiles || !invdelta || !a0)
+    return set_error(SANTA_ERR_INVALID, "null pointer argument");
+  const int st = prop_budgets_launch(m_tiles, ell_tiles, H, H, T_c, S, seed, m_star, S_tiles, invdelta, a0, stream);
+  if (st != SANTA_OK) return st;
+  return clear_error();
+}
+
+static int prop_pass2_launch(const void* V, const uint16_t* u_stash, int dtype, int B, int H, int KVH, int L,
+                             int L_storage, int block_n, int T_c, int S, const float* invdelta, const float* a0,
+                             int16_t* counts, void* out, int* vrows, const prop::PropWs& w, char* base,
+                             hipStream_t stream) {
+  float* part = reinterpret_cast<float*>(base + w.part);
+  int* pe = reinterpret_cast<int*>(base + w.emit);
+  const int GH = H / KVH;
+  const uint16_t* Vh = static_cast<const uint16_t*>(V);
+  hipError_t e;
+  const int want_emit = vrows ? 1 : 0;
+  if (dtype == SANTA_BF16)
+    e = (GH == 4) ? prop::launch_pass2_bn<true, 4>(block_n, Vh, u_stash, B, H, KVH, L, L_storage, T_c, w.cs, w.cpg,
+                                                   invdelta, a0, counts, part, pe, want_emit, stream)
+                  : prop::launch_pass2_bn<true, 8>(block_n, Vh, u_stash, B, H, KVH, L, L_storage, T_c, w.cs, w.cpg,
+                                                   invdelta, a0, counts, part, pe, want_emit, stream);
+  else
+    e = (GH == 4) ? prop::launch_pass2_bn<false, 4>(block_n, Vh, u_stash, B, H, KVH, L, L_storage, T_c, w.cs, w.cpg,
+                                                    invdelta, a0, counts, part, pe, want_emit, stream)
+                  : prop::launch_pass2_bn<false, 8>(block_n, Vh, u_stash, B, H, KVH, L, L_storage, T_c, w.cs, w.cpg,
+                                                    invdelta, a0, counts, part, pe, want_emit, stream);
+  if (e != hipSuccess) return set_error(SANTA_ERR_HIP, "pass-2 launch failed: %s", hipGetErrorString(e));
+  const float scale_out = (S > 0) ? (1.0f / static_cast<float>(S)) : 0.0f;
+  const unsigned grid = static_cast<unsigned>(B) * static_cast<unsigned>(H);
+  uint16_t* o = static_cast<uint16_t*>(out);
+  if (dtype == SANTA_BF16) {
+    if (GH == 4)
+      hipLaunchKernelGGL((prop::finalize_kernel<true, 4>), dim3(grid), dim3(prop::kD), 0, stream, part, pe, H, KVH,
+                         w.cpg, scale_out, o, vrows);
+    else
+      hipLaunchKernelGGL((prop::finalize_kernel<true, 8>), dim3(grid), dim3(prop::kD), 0, stream, part, pe, H, KVH,
+                         w.cpg, scale_out, o, vrows);
+  } else {
+    if (GH == 4)
+      hipLaunchKernelGGL((prop::finalize_kernel<false, 4>), dim3(grid), dim3(prop::kD), 0, stream, part, pe, H, KVH,
+                         w.cpg, scale_out, o, vrows);
+    else
+      hipLaunchKernelGGL((prop::finalize_kernel<false, 8>), dim3(grid), dim3(prop::kD), 0, stream, part, pe, H, KVH,
+                         w.cpg, scale_out, o, vrows);
+  }
+  e = hipGetLastError();
+  if (e != hipSuccess) return set_error(SANTA_ERR_HIP, "finalize launch failed: %s", hipGetErrorString(e));
+  return SANTA_OK;
+}
+
+extern "C" size_t santa_prop_workspace_size(int H, int KVH, int D, int L, int T_c) {
+  (void)D;
+  if (H <= 0 || KVH <= 0 || H % KVH != 0 || L <= 0 || T_c <= 0) return 0;
+  return prop::prop_ws_layout(1, H, KVH, L, T_c).total;
+}
+
+extern "C" int santa_prop_pass2(const void* V, const void* u_stash, int dtype, int H, int KVH, int D, int L,
+                                int block_n, int S, const float* invdelta, const float* a0, int16_t* counts,
+                                void* out, int* vrows, void* workspace, size_t workspace_bytes, hipStream_t stream) {
+  int st = prop::check_common(dtype, H, KVH, D);
+  if (st != SANTA_OK) return st;
+  if (L <= 0) return set_error(SANTA_ERR_INVALID, "empty KV cache: L=%d", L);
+  const int T_c = (L + block_n - 1) / block_n;
+  if ((st = prop::check_bn(block_n, T_c)) != SANTA_OK) return st;
+  if (!V || !u_stash || !invdelta || !a0 || !out) return set_error(SANTA_ERR_INVALID, "null pointer argument");
+  const prop::PropWs w = prop::prop_ws_layout(1, H, KVH, L, T_c);
+  if (!workspace || workspace_bytes < w.total)
+    return set_error(SANTA_ERR_WORKSPACE, "workspace too small: need %zu bytes, got %zu", w.total, workspace_bytes);
+  st = prop_pass2_launch(V, static_cast<const uint16_t*>(u_stash), dtype, 1, H, KVH, L, L, block_n, T_c, S, invdelta,
+                         a0, counts, out, vrows, w, static_cast<char*>(workspace), stream);
+  if (st != SANTA_OK) return st;
+  return clear_error();
+}
+
+extern "C" int santa_prop_decode(const void* q, const void* K, const void* V, int dtype, int H, int KVH, int D, int L,
+                                 int block_n, int pass1_path, int S, uint64_t seed, void* out, float* m_star,
+                                 int* vrows, void* workspace, size_t workspace_bytes, hipStream_t stream) {
+  int st = prop::check_common(dtype, H, KVH, D);
+  if (st != SANTA_OK) return st;
+  if (L <= 0) return set_error(SANTA_ERR_INVALID, "empty KV cache: L=%d", L);
+  const int T_c = (L + block_n - 1) / block_n;
+  if ((st = prop::check_bn(block_n, T_c)) != SANTA_OK) return st;
+  if (pass1_path == 0 && !(H / KVH == 4 && block_n == 256))
+    return set_error(SANTA_ERR_INVALID, "SANTA_PASS1=vec requires GH=4, D=128, block_n=256. Got GH=%d D=%d block_n=%d",
+                     H / KVH, D, block_n);
+  if (!q || !K || !V || !out) return set_error(SANTA_ERR_INVALID, "null pointer argument");
+  const prop::PropWs w = prop::prop_ws_layout(1, H, KVH, L, T_c);
+  if (!workspace || workspace_bytes < w.total)
+    return set_error(SANTA_ERR_WORKSPACE, "workspace too small: need %zu bytes, got %zu", w.total, workspace_bytes);
+  char* base = static_cast<char*>(workspace);
+  float* m_tiles = reinterpret_cast<float*>(base + w.m);
+  float* ell_tiles = reinterpret_cast<float*>(base + w.ell);
+  int* S_tiles = reinterpret_cast<int*>(base + w.st);
+  float* inv = reinterpret_cast<float*>(base + w.inv);
+  float* a0 = reinterpret_cast<float*>(base + w.a0);
+  uint16_t* stash = reinterpret_cast<uint16_t*>(base + w.stash);
+  hipError_t e = flash::launch_prop_pass1(q, K, dtype, 1, H, KVH, L, L, block_n, pass1_path, m_tiles, ell_tiles,
+                                          stash, stream);
+  if (e != hipSuccess) return set_error(SANTA_ERR_HIP, "pass-1 launch failed: %s", hipGetErrorString(e));
+  if ((st = prop_budgets_launch(m_tiles, ell_tiles, H, H, T_c, S, seed, m_star, S_tiles, inv, a0, stream)) != SANTA_OK)
+    return st;
+  if ((st = prop_pass2_launch(V, stash, dtype, 1, H, KVH, L, L, block_n, T_c, S, inv, a0, nullptr, out, vrows, w, base,
+                              stream)) != SANTA_OK)
+    return st;
+  return clear_error();
+}

@@ -1,0 +1,16 @@
+"""S^2ANTA-Prop sampled-attention decode on MI355X -- drop-in for the
+reference's `santa_prop_batch_cuda` extension module
+(santa_fused_proportional_tile_budgets/santa_cuda.cpp:354-358).
+
+    decode_systematic_scalar(q_h, K_g, V_g, S, seed=42, block_n=0,
+                             want_vrows=False) -> (out, m_star, vrows)
+
+Single sequence: q_h [H, D], K_g / V_g [L, KVH, D].  The environment variable
+SANTA_PASS1 (auto / gqa / vec) selects the pass-1 numerics on every call, as
+in the reference.
+
+torch is imported first so that the native module binds to torch's HIP runtime.
+"""
+import torch  # noqa: F401  (must precede the native module)
+
+from ._C import _debug_pass, _library_version, decode_systematic_scalar  # noqa: F401

@@ -1,0 +1,128 @@
+"""GPU parity of santa_prop against the CPU oracle.
+
+Bit-exact: per-tile max and mass, the u stash, m*, the largest-remainder
+budgets S_t, invdelta_t, a0_t and every sampled count; vrows exact.  The
+output is summed in a different (fixed) order than the oracle's, so it is
+checked to the north-star bf16 tolerance against the oracle and against an
+independent torch fp32 restatement of the estimator given the GPU's counts.
+
+Every case prints its name, shape and seed before touching the GPU.
+"""
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from helpers import SEED, bits16, gen_qkv, h16_to_f32, tol_check
+
+pytestmark = pytest.mark.gpu
+
+
+def _mod():
+    import santa_prop_batch_cuda as m
+
+    return m
+
+
+def _announce(msg):
+    print(f"\n[case] {msg}", flush=True)
+
+
+def prop_estimator_given_counts(counts, V, S):
+    """fp32 torch: out[h] = sum_t sum_r c[h,t,r] v[t*BN+r, kv(h)] / S (0 if S <= 0)."""
+    H, T_c, BN = counts.shape
+    L, KVH, D = V.shape
+    GH = H // KVH
+    c = counts.float().cpu().reshape(H, T_c * BN)[:, :L].reshape(KVH, GH, L)
+    y = torch.einsum("kgl,lkd->kgd", c, V.float().cpu()).reshape(H, D)
+    return y / S if S > 0 else torch.zeros_like(y)
+
+
+def _check(q, K, V, S, seed, block_n=0, pass1_env=None, is_bf16=True, monkeypatch=None):
+    m = _mod()
+    if pass1_env is None:
+        monkeypatch.delenv("SANTA_PASS1", raising=False)
+    else:
+        monkeypatch.setenv("SANTA_PASS1", pass1_env)
+    dev = torch.device("cuda:0")
+    qd, Kd, Vd = q.to(dev), K.to(dev), V.to(dev)
+    dbg = m._debug_pass(qd, Kd, Vd, S, seed=seed, block_n=block_n)
+    out, ms, vr = m.decode_systematic_scalar(qd, Kd, Vd, S, seed=seed, block_n=block_n, want_vrows=True)
+    out2, ms2, vr2 = m.decode_systematic_scalar(qd, Kd, Vd, S, seed=seed, block_n=block_n)
+    torch.cuda.synchronize()
+    mt, lt, mstar, St, inv, a0, stash, cnt, out_d, vr_d = [t.cpu() for t in dbg]
+    exp = oracle.prop_decode(q, K, V, S, seed=seed, block_n=block_n, is_bf16=is_bf16, debug=True)
+    for name, got in (("m_tiles", mt), ("ell_tiles", lt), ("invdelta", inv), ("a0", a0)):
+        np.testing.assert_array_equal(got.numpy().view(np.uint32), exp[name].view(np.uint32), err_msg=name)
+    np.testing.assert_array_equal(St.numpy(), exp["S_tiles"], err_msg="S_tiles")
+    np.testing.assert_array_equal(bits16(stash), exp["u_stash"], err_msg="u_stash")
+    c_gpu = cnt.numpy()
+    assert np.array_equal(c_gpu, exp["counts"]), f"counts differ at {np.argwhere(c_gpu != exp['counts'])[:8]}"
+    for got in (mstar, ms.cpu()):
+        np.testing.assert_array_equal(got.numpy().view(np.uint32), exp["m_star"].view(np.uint32), err_msg="m_star")
+    np.testing.assert_array_equal(vr.cpu().numpy(), exp["vrows"], err_msg="vrows")
+    np.testing.assert_array_equal(vr_d.numpy(), exp["vrows"], err_msg="vrows (stages)")
+    assert vr2.numel() == 0
+    # the three stage entry points and the fused decode give the same bits
+    np.testing.assert_array_equal(bits16(out), bits16(out_d), err_msg="decode vs stages")
+    np.testing.assert_array_equal(bits16(out), bits16(out2), err_msg="repeat call")
+    if S > 0:
+        assert (St.sum(dim=1) == S).all(), "budgets must sum to S per head"
+    got = h16_to_f32(bits16(out), is_bf16)
+    ok, mabs, mrel = tol_check(got, h16_to_f32(exp["out16"], is_bf16))
+    assert ok, ("vs oracle", mabs, mrel)
+    ref = prop_estimator_given_counts(cnt, V, S).to(q.dtype).float().numpy()
+    ok, mabs, mrel = tol_check(got, ref)
+    assert ok, ("vs torch estimator", mabs, mrel)
+    return exp
+
+
+@pytest.mark.parametrize(
+    "H,KVH,L,S,block_n,env",
+    [
+        (32, 8, 5000, 5000 // 64, 0, None),     # vec path, BN 256, ragged last tile
+        (32, 8, 32768, 512, 0, None),           # vec path, 128 tiles
+        (32, 8, 1000, 40, 0, None),             # general path, BN 32
+        (32, 8, 2000, 64, 0, None),             # general path, BN 64
+        (32, 8, 4096, 64, 0, "gqa"),            # general path forced at BN 256
+        (32, 8, 3000, 300, 0, "vec"),           # vec forced: BN 256 chosen by the env
+        (64, 8, 3000, 100, 0, None),            # GH 8 (general path), BN 64
+        (64, 8, 9000, 150, 0, None),            # GH 8 (general path), BN 256
+        (32, 8, 700, 0, 256, None),             # S = 0 -> zeros
+        (32, 8, 2048, 100000, 256, None),       # S far above the tile count
+        (32, 8, 33, 3, 32, None),               # two tiles, one of one row
+    ],
+)
+def test_prop_parity(H, KVH, L, S, block_n, env, monkeypatch):
+    _announce(f"prop H={H} KVH={KVH} L={L} S={S} bn={block_n} SANTA_PASS1={env}")
+    q, K, V = gen_qkv(1, H, KVH, L, seed=SEED + L + H, single=True)
+    exp = _check(q, K, V, S, SEED, block_n=block_n, pass1_env=env, monkeypatch=monkeypatch)
+    if S == 0:
+        assert not exp["out16"].any()
+
+
+def test_prop_f16_and_peaky(monkeypatch):
+    _announce("prop f16 L=6000 S=100 and bf16 low-rank keys L=20000 S=312")
+    q, K, V = gen_qkv(1, 32, 8, 6000, seed=SEED, dtype=torch.float16, single=True)
+    _check(q, K, V, 100, SEED, is_bf16=False, monkeypatch=monkeypatch)
+    q, K, V = gen_qkv(1, 32, 8, 20000, seed=SEED + 7, lowrank=0.5, single=True)
+    _check(q, K, V, 312, 1690, monkeypatch=monkeypatch)
+
+
+def test_prop_errors(monkeypatch):
+    _announce("prop input errors")
+    m = _mod()
+    dev = torch.device("cuda:0")
+    q, K, V = gen_qkv(1, 32, 8, 512, single=True)
+    qd, Kd, Vd = q.to(dev), K.to(dev), V.to(dev)
+    with pytest.raises(RuntimeError, match="bad ranks"):
+        m.decode_systematic_scalar(qd[None], Kd, Vd, 8)
+    Kn = Kd.transpose(1, 2).contiguous().transpose(1, 2)  # [L, KVH, D], not contiguous
+    with pytest.raises(RuntimeError, match=r"K_g/V_g must be contiguous with layout \[L, KVH, D\] \(NHD\)"):
+        m.decode_systematic_scalar(qd, Kn, Vd, 8)
+    monkeypatch.setenv("SANTA_PASS1", "vec")
+    with pytest.raises(RuntimeError, match="SANTA_PASS1=vec requires GH=4, D=128, block_n=256"):
+        m.decode_systematic_scalar(qd, Kd, Vd, 8, block_n=64)
+    monkeypatch.delenv("SANTA_PASS1")
+    with pytest.raises(TypeError):
+        m.decode_systematic_scalar(qd, Kd, Vd, 8, valid_len=3)
