@@ -66,6 +66,10 @@ def lib() -> ctypes.CDLL:
         L.so_flash_decode.restype = i32
         L.so_flash_decode.argtypes = [P, P, P, i32, i32, i32, i32, i32, i32, i32, i32, u64,
                                       P, P, P, P, P, P, P, P, i32]
+        L.so_f32_to_h16_array.restype = None
+        L.so_f32_to_h16_array.argtypes = [P, P, i64, i32]
+        L.so_h16_to_f32_array.restype = None
+        L.so_h16_to_f32_array.argtypes = [P, P, i64, i32]
         L.so_prop_budgets.restype = None
         L.so_prop_budgets.argtypes = [P, P, i32, i32, u64, i32, P, P, P, P]
         L.so_prop_decode.restype = i32
@@ -104,6 +108,21 @@ def expf(x: np.ndarray) -> np.ndarray:
     x = np.ascontiguousarray(x, dtype=np.float32)
     y = np.empty_like(x)
     lib().so_expf_array(_ptr(x), _ptr(y), x.size)
+    return y
+
+
+def f32_to_h16(x: np.ndarray, is_bf16: bool = True) -> np.ndarray:
+    """f32 -> bf16 / f16 bits, round to nearest even (the kernels' conversion)."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    y = np.empty(x.shape, dtype=np.uint16)
+    lib().so_f32_to_h16_array(_ptr(x), _ptr(y), x.size, int(is_bf16))
+    return y
+
+
+def h16_to_f32(bits: np.ndarray, is_bf16: bool = True) -> np.ndarray:
+    b = np.ascontiguousarray(bits, dtype=np.uint16)
+    y = np.empty(b.shape, dtype=np.float32)
+    lib().so_h16_to_f32_array(_ptr(b), _ptr(y), b.size, int(is_bf16))
     return y
 
 

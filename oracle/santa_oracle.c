@@ -730,3 +730,9 @@ void so_u01_array(uint64_t seed, const int* key, const int* t, float* out, long 
 void so_counts_1d(const uint16_t* ub, int len, float invdel, float a0, int is_bf16, int16_t* c_out) {
   tile_counts(ub, 1, len, invdel, a0, is_bf16, c_out);
 }
+void so_f32_to_h16_array(const float* x, uint16_t* y, long n, int is_bf16) {
+  for (long i = 0; i < n; ++i) y[i] = st16(x[i], is_bf16);
+}
+void so_h16_to_f32_array(const uint16_t* x, float* y, long n, int is_bf16) {
+  for (long i = 0; i < n; ++i) y[i] = ld16(x, (size_t)i, is_bf16);
+}
