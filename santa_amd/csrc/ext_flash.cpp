@@ -11,6 +11,7 @@
 #include <tuple>
 
 #include "santa_amd.h"
+#include "santa_internal.h"
 
 namespace {
 
@@ -194,6 +195,18 @@ void decode_tiles_only(at::Tensor q_h, at::Tensor K_g, at::Tensor V_g, int64_t S
   TORCH_CHECK(rc == SANTA_OK, santa_last_error());
 }
 
+// Test-only: the kernels' exponential applied to a float32 CUDA tensor.
+at::Tensor device_expf(at::Tensor x) {
+  TORCH_CHECK(x.is_cuda() && x.scalar_type() == at::kFloat, "x must be a CUDA float32 tensor");
+  c10::DeviceGuard guard(x.device());
+  at::Tensor xc = x.contiguous();
+  at::Tensor y = at::empty_like(xc);
+  const hipError_t e = santa::flash::launch_expf(xc.data_ptr<float>(), y.data_ptr<float>(),
+                                                 static_cast<size_t>(xc.numel()), current_stream(xc));
+  TORCH_CHECK(e == hipSuccess, "expf launch failed: ", hipGetErrorString(e));
+  return y;
+}
+
 int64_t workspace_bytes(int64_t B, int64_t H, int64_t KVH, int64_t D, int64_t T_c) {
   return static_cast<int64_t>(santa_flash_workspace_size(static_cast<int>(B), static_cast<int>(H),
                                                          static_cast<int>(KVH), static_cast<int>(D),
@@ -218,5 +231,6 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
   m.def("_decode_tiles_only", &decode_tiles_only, py::arg("q_h"), py::arg("K_g"), py::arg("V_g"), py::arg("S"),
         py::arg("seed"), py::arg("block_n"), py::arg("valid_len"), py::arg("ws"));
   m.def("_workspace_bytes", &workspace_bytes);
+  m.def("_device_expf", &device_expf, py::arg("x"));
   m.def("_library_version", []() { return std::string(santa_version()); });
 }

@@ -101,9 +101,11 @@ __device__ __forceinline__ float u01(uint64_t seed, int key, int t) {
 // scaling by 2^n as two exact power-of-two multiplies (one rounding for
 // subnormal results).  exp(0) == 1 exactly; <= 2 ulp from the true value.
 __device__ __forceinline__ float santa_expf(float x) {
-  // Evaluated on the clamped argument and patched by selects (no branches);
-  // in range the arithmetic is exactly that of the plain formula.
-  const float xc = fminf(fmaxf(x, -103.97208404541015625f), 88.72283935546875f);
+  // Branch-free: the argument is clamped to [-104, 89] (outside it the
+  // result is 0 or inf either way) and 2^n is applied by one v_ldexp_f32,
+  // which rounds p * 2^n once -- the same value as the two exact
+  // power-of-two multiplies of the restatement.  NaN passes through.
+  const float xc = fminf(fmaxf(x, -104.0f), 89.0f);
   const float n = __builtin_rintf(xc * 1.44269502162933349609375f);
   float r = fmaf(n, -0.693145751953125f, xc);
   r = fmaf(n, -1.428606765330187045e-06f, r);
@@ -115,14 +117,7 @@ __device__ __forceinline__ float santa_expf(float x) {
   p = fmaf(p, r, 0.5f);
   p = fmaf(p, r, 1.0f);
   p = fmaf(p, r, 1.0f);
-  const int ni = static_cast<int>(n);
-  const int n1 = ni / 2;
-  const int n2 = ni - n1;
-  const float s1 = __uint_as_float(static_cast<uint32_t>(n1 + 127) << 23);
-  const float s2 = __uint_as_float(static_cast<uint32_t>(n2 + 127) << 23);
-  float res = (p * s1) * s2;
-  res = (x > 88.72283935546875f) ? __builtin_inff() : res;
-  res = (x < -103.97208404541015625f) ? 0.0f : res;
+  const float res = __builtin_amdgcn_ldexpf(p, static_cast<int>(n));
   return (x != x) ? x : res;
 }
 

@@ -54,6 +54,10 @@ constexpr int kD = 128;
 constexpr int kThreads = 256;
 constexpr int kPartStride = kD + 2;  // chunk partial: M, Z, num[128]
 constexpr int kListCap = 128;        // sampled rows buffered per head before a gather (>= 2 x 64)
+// Buffer descriptor word 3 for raw (untyped) loads on gfx9-family parts, and
+// the cache-policy bits of a non-temporal load (the "nt" bit).
+constexpr int kBufferWord3 = 0x00020000;
+constexpr int kBufferNontemporal = 2;
 // kPerTile / kOnline: santa_flash.  kPass1Vec: santa_prop pass 1 with the
 // vec kernel's numerics (= the flash tile statistics).  kPass1Gen: santa_prop
 // pass 1 of the general path: q rounded to the 16-bit type after scaling and
@@ -166,7 +170,7 @@ __global__ __launch_bounds__(kThreads, 2) void tile_kernel(
 
   const int tid = static_cast<int>(threadIdx.x);
   const int lane = tid & 63;
-  const int wave = tid >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform for the compiler
 
   __shared__ float s_sc[BN * GH];          // scores, [row][head]
   __shared__ uint16_t s_ub[GH * BN];       // 16-bit u, [head][row]
@@ -174,9 +178,15 @@ __global__ __launch_bounds__(kThreads, 2) void tile_kernel(
   __shared__ float s_W[NWS * GH];
   __shared__ uint64_t s_mask[GH * NPAIR * 2];
 
+  // Addresses: a wave-uniform 64-bit base (SGPRs) plus a 32-bit per-lane byte
+  // offset, so loads take the scalar-base form and need no 64-bit VALU math.
   const size_t row_stride = static_cast<size_t>(KVH) * kD;
-  const uint16_t* Kg = K + static_cast<size_t>(b) * L_storage * row_stride + static_cast<size_t>(kv) * kD;
-  const uint16_t* Vg = V + static_cast<size_t>(b) * L_storage * row_stride + static_cast<size_t>(kv) * kD + 2 * lane;
+  const uint32_t row_bytes = static_cast<uint32_t>(KVH) * kD * 2u;
+  const char* Kg = reinterpret_cast<const char*>(K + static_cast<size_t>(b) * L_storage * row_stride +
+                                                 static_cast<size_t>(kv) * kD);
+  const char* Vg = reinterpret_cast<const char*>(V + static_cast<size_t>(b) * L_storage * row_stride +
+                                                 static_cast<size_t>(kv) * kD);
+  const uint32_t v_lane_off = 4u * static_cast<uint32_t>(lane);  // dims 2*lane, 2*lane+1
 
   // Online-merge state: per head owned by this wave, running max M, mass Z
   // and this lane's two numerator dims.
@@ -247,39 +257,58 @@ __global__ __launch_bounds__(kThreads, 2) void tile_kernel(
     num0[k] *= rs;
     num1[k] *= rs;
     numM[k] = Mf;
-    for (int base = 0; base < lcnt[k]; base += 16) {
-      float coef[16];
-      uint32_t vw[16];
+    for (int base = 0; base < lcnt[k]; base += 64) {
+      // lane i prepares element base+i; the gather then walks the elements in
+      // order with the row and coefficient broadcast from their lane
+      const int i = base + lane;
+      const bool ok = i < lcnt[k];
+      const int rowv = ok ? s_lrow[g * LCAP + i] : 0;
+      const float coefv = ok ? s_lcw[g * LCAP + i] * santa_expf(s_lm[g * LCAP + i] - Mf) : 0.0f;
+      const int nb = min(64, lcnt[k] - base);
+      for (int q0 = 0; q0 < nb; q0 += 16) {
+        float coef[16];
+        uint32_t vw[16];
 #pragma unroll
-      for (int q = 0; q < 16; ++q) {
-        const int i = base + q;
-        const bool ok = i < lcnt[k];
-        const int row = ok ? s_lrow[g * LCAP + i] : 0;
-        coef[q] = ok ? s_lcw[g * LCAP + i] * santa_expf(s_lm[g * LCAP + i] - Mf) : 0.0f;
-        vw[q] = *reinterpret_cast<const uint32_t*>(Vg + static_cast<size_t>(row) * row_stride);
-      }
+        for (int q = 0; q < 16; ++q) {
+          const int j = min(q0 + q, nb - 1);
+          const int row = __builtin_amdgcn_readlane(rowv, j);
+          coef[q] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(coefv), j));
+          vw[q] = *reinterpret_cast<const uint32_t*>(Vg + static_cast<size_t>(row) * row_bytes + v_lane_off);
+        }
 #pragma unroll
-      for (int q = 0; q < 16; ++q) {
-        if (base + q < lcnt[k]) {
-          num0[k] = fmaf(coef[q], lo16_to_f32<BF16>(vw[q]), num0[k]);
-          num1[k] = fmaf(coef[q], hi16_to_f32<BF16>(vw[q]), num1[k]);
+        for (int q = 0; q < 16; ++q) {
+          if (q0 + q < nb) {
+            num0[k] = fmaf(coef[q], lo16_to_f32<BF16>(vw[q]), num0[k]);
+            num1[k] = fmaf(coef[q], hi16_to_f32<BF16>(vw[q]), num1[k]);
+          }
         }
       }
     }
     lcnt[k] = 0;
   };
 
-  // This wave's 64 rows of a tile: 16 loads of 16 B per lane, 4 rows each.
+  // This wave's 64 rows of a tile: 16 buffer loads of 16 B per lane, 4 rows
+  // each.  Load c reads rows 64w+4c .. 64w+4c+3 through its own descriptor
+  // (base and record count in SGPRs); every lane's offset inside the 4-row
+  // group is the same constant VGPR.  Rows at or past the tile's end are out
+  // of the descriptor's range: they read as zero and cost no memory traffic,
+  // so one unconditional call site covers short tiles, waves without rows and
+  // the missing successor of a chunk's last tile (no branches, so the loaded
+  // registers are never copied and no wait lands before the scores).
   u32x4 kw[16];
+  const int k_lane_off = static_cast<int>((lane >> 4) * row_bytes + 16u * (lane & 15));
   auto load_k = [&](int t) {
     const int n0 = t * BN;
-    const int len = min(BN, L_valid - n0);
-    if (64 * wave >= len) return;  // no rows for this wave (short tiles)
+    const int len = (t < t_end) ? min(BN, L_valid - n0) : 0;
+    const char* kt = Kg + static_cast<size_t>(n0 + 64 * wave) * row_bytes;
 #pragma unroll
     for (int c = 0; c < 16; ++c) {
-      const int rr = min(64 * wave + 4 * c + (lane >> 4), len - 1);
-      kw[c] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(Kg + static_cast<size_t>(n0 + rr) * row_stride) +
-                                         (lane & 15));
+      // wave-uniform; readfirstlane keeps the descriptor in SGPRs
+      const int nvalid = __builtin_amdgcn_readfirstlane(min(max(len - 64 * wave - 4 * c, 0), 4));
+      const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+          const_cast<char*>(kt + static_cast<size_t>(4 * c) * row_bytes), static_cast<short>(0),
+          nvalid * static_cast<int>(row_bytes), kBufferWord3);
+      kw[c] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rs, k_lane_off, 0, kBufferNontemporal));
     }
   };
   load_k(t_begin);
@@ -292,18 +321,20 @@ __global__ __launch_bounds__(kThreads, 2) void tile_kernel(
     float lmax[GH];
 #pragma unroll
     for (int g = 0; g < GH; ++g) lmax[g] = -__builtin_inff();
-    if (64 * wave < len) {
+    const bool has_rows = 64 * wave < len;
+    if (has_rows) {
 #pragma unroll
       for (int c = 0; c < 16; ++c) {
         const int r = 4 * c + (lane >> 4);
         wk[r * 16 + ((lane & 15) ^ (r & 15))] = kw[c];
       }
-      // the next tile's rows stream in through this tile's scores and tail
-      if (t + 1 < t_end) load_k(t + 1);
-      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-      __builtin_amdgcn_wave_barrier();
-      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-
+    }
+    // the next tile's rows stream in through this tile's scores and tail
+    load_k(t + 1);
+    // LDS operations of one wave complete in order; the barrier only keeps
+    // the compiler from moving the reads above the writes
+    __builtin_amdgcn_wave_barrier();
+    if (has_rows) {
       // score = D_even + D_odd with C(c) = B(c) + B(c+2), D = C(0) + C(1)
       const int row = lane;
       f32x4 be0[NHB], bo0[NHB], be2[NHB], bo2[NHB], be1[NHB], bo1[NHB], be3[NHB], bo3[NHB];
@@ -316,14 +347,13 @@ __global__ __launch_bounds__(kThreads, 2) void tile_kernel(
       for (int hb = 0; hb < NHB; ++hb) {
         const f32x4 de = (be0[hb] + be2[hb]) + (be1[hb] + be3[hb]);
         const f32x4 dd = (bo0[hb] + bo2[hb]) + (bo1[hb] + bo3[hb]);
-        const f32x4 sc = de + dd;  // heads 4hb .. 4hb+3 of row r
+        f32x4 sc = de + dd;  // heads 4hb .. 4hb+3 of row r
         if (BN == 256 || r < BN) reinterpret_cast<f32x4*>(s_sc + r * GH)[hb] = sc;
-        // rows past len hold copies of row len-1, so they leave the max unchanged
+        // rows past len read as zero: they take no part in the max
+        if (r >= len) sc = f32x4{-__builtin_inff(), -__builtin_inff(), -__builtin_inff(), -__builtin_inff()};
 #pragma unroll
         for (int i = 0; i < 4; ++i) lmax[4 * hb + i] = sc[i];
       }
-    } else {
-      if (t + 1 < t_end) load_k(t + 1);
     }
 
     // ---- B: tile max per head (A.3) ------------------------------------------
@@ -514,11 +544,10 @@ __global__ __launch_bounds__(kThreads, 2) void tile_kernel(
           uint32_t vw[8];
 #pragma unroll
           for (int q = 0; q < 8; ++q) {
-            const int i = base + q;
-            const bool ok = i < lcnt[k];
-            const int rr = ok ? s_lrow[g * LCAP + i] : n0;
-            cf[q] = ok ? s_lcw[g * LCAP + i] : 0.0f;
-            vw[q] = *reinterpret_cast<const uint32_t*>(Vg + static_cast<size_t>(rr) * row_stride);
+            const int i = min(base + q, lcnt[k] - 1);
+            const int rr = __builtin_amdgcn_readfirstlane(s_lrow[g * LCAP + i]);
+            cf[q] = s_lcw[g * LCAP + i];
+            vw[q] = *reinterpret_cast<const uint32_t*>(Vg + static_cast<size_t>(rr) * row_bytes + v_lane_off);
           }
 #pragma unroll
           for (int q = 0; q < 8; ++q) {
@@ -746,6 +775,20 @@ static void chunk_plan(int B, int KVH, int T_c, int* cs, int* cpg) {
   const int c = static_cast<int>((T_c + want - 1) / want);
   *cs = c;
   *cpg = (T_c + c - 1) / c;
+}
+
+// The device exponential on an array (test hook, declared in santa_internal.h).
+__global__ void expf_kernel(const float* __restrict__ x, float* __restrict__ y, size_t n) {
+  for (size_t i = blockIdx.x * static_cast<size_t>(blockDim.x) + threadIdx.x; i < n;
+       i += static_cast<size_t>(gridDim.x) * blockDim.x)
+    y[i] = santa_expf(x[i]);
+}
+hipError_t launch_expf(const float* x, float* y, size_t n, hipStream_t stream) {
+  if (n == 0) return hipSuccess;
+  const size_t blocks = (n + kThreads - 1) / kThreads;
+  hipLaunchKernelGGL(expf_kernel, dim3(static_cast<unsigned>(blocks < 65536 ? blocks : 65536)), dim3(kThreads), 0,
+                     stream, x, y, n);
+  return hipGetLastError();
 }
 
 // santa_prop pass 1 on the tile kernel (declared in santa_internal.h).

@@ -23,6 +23,8 @@ namespace flash {
 hipError_t launch_prop_pass1(const void* q, const void* K, int dtype, int B, int H, int KVH, int L, int L_storage,
                              int block_n, int path, float* m_tiles, float* ell_tiles, uint16_t* u_stash,
                              hipStream_t stream);
+// y[i] = santa_expf(x[i]) on the device (test hook for the exponential).
+hipError_t launch_expf(const float* x, float* y, size_t n, hipStream_t stream);
 // Chunks of cs tiles per workgroup, cpg chunks per (b, kv) group, sized to
 // about one resident round of 256-thread workgroups on the current device.
 void plan_chunks(int B, int KVH, int T_c, int* cs, int* cpg);

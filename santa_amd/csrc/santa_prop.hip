@@ -216,7 +216,7 @@ __global__ __launch_bounds__(kThreads) void pass2_kernel(const uint16_t* __restr
   const int t_end = min(T_c, t_begin + cs);
   const int tid = static_cast<int>(threadIdx.x);
   const int lane = tid & 63;
-  const int wave = tid >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform for the compiler
   const int jrow = lane >> 4;
   const int qq = lane & 15;
 
@@ -225,7 +225,11 @@ __global__ __launch_bounds__(kThreads) void pass2_kernel(const uint16_t* __restr
   __shared__ int s_lrow[GH * BN];
 
   const size_t row_stride = static_cast<size_t>(KVH) * kD;
-  const uint16_t* Vg = V + static_cast<size_t>(b) * L_storage * row_stride + static_cast<size_t>(kv) * kD + 2 * lane;
+  const uint32_t row_bytes = static_cast<uint32_t>(KVH) * kD * 2u;
+  // wave-uniform 64-bit base + 32-bit lane offset (scalar-base loads)
+  const char* Vg = reinterpret_cast<const char*>(V + static_cast<size_t>(b) * L_storage * row_stride +
+                                                 static_cast<size_t>(kv) * kD);
+  const uint32_t v_lane_off = 4u * static_cast<uint32_t>(lane);
   const uint16_t* ub = u_stash + static_cast<size_t>(b) * L_storage * H;
 
   float acc0[HPW], acc1[HPW];
@@ -312,11 +316,10 @@ __global__ __launch_bounds__(kThreads) void pass2_kernel(const uint16_t* __restr
         uint32_t vw[8];
 #pragma unroll
         for (int q = 0; q < 8; ++q) {
-          const int i = base + q;
-          const bool ok = i < cnt;
-          const int rr = ok ? s_lrow[g * BN + i] : n0;
-          cf[q] = ok ? s_lcw[g * BN + i] : 0.0f;
-          vw[q] = *reinterpret_cast<const uint32_t*>(Vg + static_cast<size_t>(rr) * row_stride);
+          const int i = min(base + q, cnt - 1);
+          const int rr = __builtin_amdgcn_readfirstlane(s_lrow[g * BN + i]);
+          cf[q] = s_lcw[g * BN + i];
+          vw[q] = *reinterpret_cast<const uint32_t*>(Vg + static_cast<size_t>(rr) * row_bytes + v_lane_off);
         }
 #pragma unroll
         for (int q = 0; q < 8; ++q) {

@@ -14,6 +14,7 @@ from ._C import (  # noqa: F401
     _debug_tiles,
     _decode_reference_order,
     _decode_tiles_only,
+    _device_expf,
     _library_version,
     _workspace_bytes,
     decode_systematic_batched,
