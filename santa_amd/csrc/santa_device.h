@@ -40,10 +40,10 @@ __device__ __forceinline__ float h16_to_f32(uint16_t h) {
 // f32 -> bf16 / f16, round to nearest even (the reference's __float2bfloat16 /
 // __float2half_rn, flash/santa_cuda_kernel.cu:53-55).
 __device__ __forceinline__ uint16_t f32_to_bf16_rne(float f) {
-  uint32_t u = __float_as_uint(f);
-  if ((u & 0x7fffffffu) > 0x7f800000u) return static_cast<uint16_t>((u >> 16) | 0x0040u);
-  u += 0x7fffu + ((u >> 16) & 1u);
-  return static_cast<uint16_t>(u >> 16);
+  const uint32_t u = __float_as_uint(f);
+  const uint32_t rne = (u + 0x7fffu + ((u >> 16) & 1u)) >> 16;
+  const uint32_t qnan = (u >> 16) | 0x0040u;
+  return static_cast<uint16_t>(((u & 0x7fffffffu) > 0x7f800000u) ? qnan : rne);
 }
 // f32 -> f16 in integer arithmetic.  A plain (_Float16) cast lets the
 // backend fold a preceding f32 multiply into v_fma_mixlo_f16, which rounds
@@ -136,11 +136,27 @@ enum : int {
   kDppQuadXor1 = 0xB1,      // quad_perm [1,0,3,2]
   kDppQuadXor2 = 0x4E,      // quad_perm [2,3,0,1]
   kDppRowHalfMirror = 0x141, // lane i <-> 7-i within each 8 lanes
-  kDppRowMirror = 0x140      // lane i <-> 15-i within each 16 lanes
+  kDppRowMirror = 0x140,     // lane i <-> 15-i within each 16 lanes
+  kDppRowBcast15 = 0x142,    // lane 15 of each row to the next row
+  kDppRowBcast31 = 0x143     // lane 31 to rows 2 and 3
 };
 template <int CTRL>
 __device__ __forceinline__ float dpp(float v) {
   return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+
+// v from lane (i + N) of the same 16-lane row, 0 where that lane is outside it.
+template <int N>
+__device__ __forceinline__ float dpp_shl_zero(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x100 + N, 0xF, 0xF, true));
+}
+
+// dpp<CTRL>(v) + 0.0f: the same value (scores and sums are never -0.0 here)
+// but a floating-point result, so a following fmaxf needs no NaN
+// canonicalisation of its operands and compiles to one v_max_f32.
+template <int CTRL>
+__device__ __forceinline__ float dppf(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false)) + 0.0f;
 }
 
 // v from lane (i - N) of the same 16-lane row, 0 where that lane is outside it.
@@ -149,18 +165,45 @@ __device__ __forceinline__ float dpp_shr_zero(float v) {
   return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x110 + N, 0xF, 0xF, true));
 }
 
-// Max over the 64 lanes of a wave (exact in any order): DPP inside each
-// 16-lane row, then the four row maxima.
-__device__ __forceinline__ float wave_max_dpp(float v) {
-  v = fmaxf(v, dpp<kDppQuadXor1>(v));
-  v = fmaxf(v, dpp<kDppQuadXor2>(v));
-  v = fmaxf(v, dpp<kDppRowHalfMirror>(v));
-  v = fmaxf(v, dpp<kDppRowMirror>(v));
-  const float m0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));
-  const float m1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 16));
-  const float m2 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32));
-  const float m3 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 48));
-  return fmaxf(fmaxf(m0, m1), fmaxf(m2, m3));
+// Order keys: a monotone bijection float <-> int32 (flip the magnitude bits
+// of negative values), so a float maximum is an integer maximum -- which
+// needs no NaN canonicalisation and fuses with DPP.  Exact for every
+// non-NaN input (-0.0 orders below +0.0).
+__device__ __forceinline__ int order_key(float f) {
+  const int b = __float_as_int(f);
+  return b ^ static_cast<int>(static_cast<unsigned>(b >> 31) >> 1);
+}
+__device__ __forceinline__ float from_order_key(int k) {
+  return __int_as_float(k ^ static_cast<int>(static_cast<unsigned>(k >> 31) >> 1));
+}
+
+// Maximum of order keys over the 64 lanes of a wave, valid in lane 63:
+// DPP inside each 16-lane row, then the row broadcasts 15 and 31 (rows left
+// out by a broadcast see INT_MIN, the identity).
+__device__ __forceinline__ int wave_max_key_lane63(int k) {
+  k = max(k, __builtin_amdgcn_update_dpp(0, k, kDppQuadXor1, 0xF, 0xF, false));
+  k = max(k, __builtin_amdgcn_update_dpp(0, k, kDppQuadXor2, 0xF, 0xF, false));
+  k = max(k, __builtin_amdgcn_update_dpp(0, k, kDppRowHalfMirror, 0xF, 0xF, false));
+  k = max(k, __builtin_amdgcn_update_dpp(0, k, kDppRowMirror, 0xF, 0xF, false));
+  k = max(k, __builtin_amdgcn_update_dpp(-2147483647 - 1, k, kDppRowBcast15, 0xA, 0xF, false));
+  k = max(k, __builtin_amdgcn_update_dpp(-2147483647 - 1, k, kDppRowBcast31, 0xC, 0xF, false));
+  return k;
+}
+
+// Max over the 64 lanes of a wave (exact in any order), valid in lane 63:
+// DPP inside each 16-lane row, then the row broadcasts 15 and 31.  v must be
+// the result of floating-point arithmetic (or a constant).
+__device__ __forceinline__ float wave_max_lane63(float v) {
+  v = fmaxf(v, dppf<kDppQuadXor1>(v));
+  v = fmaxf(v, dppf<kDppQuadXor2>(v));
+  v = fmaxf(v, dppf<kDppRowHalfMirror>(v));
+  v = fmaxf(v, dppf<kDppRowMirror>(v));
+  // rows 1, 3 take lane 15 / 47; then rows 2, 3 take lane 31
+  v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(v), __float_as_int(v), kDppRowBcast15, 0xA,
+                                                          0xF, false)) + 0.0f);
+  v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(v), __float_as_int(v), kDppRowBcast31, 0xC,
+                                                          0xF, false)) + 0.0f);
+  return v;
 }
 
 // ------------------------------------------------------ systematic counts
@@ -196,13 +239,43 @@ __device__ __forceinline__ void systematic_counts(const float (&x0)[NP], const f
     r0[p] = r0[p] + dpp_shr_zero<8>(r0[p]);
     r1[p] = r1[p] + dpp_shr_zero<8>(r1[p]);
   }
-  float carry = 0.0f;
+  float pre0[NP], pre1[NP], car[NP];
 #pragma unroll
   for (int p = 0; p < NP; ++p) {
-    const float pre0 = r0[p] - x0[p];
-    const float pre1 = r1[p] - x1[p];
-    const float tot0 = pre0 + x0[p];
-    const float tot1 = pre1 + x1[p];
+    pre0[p] = r0[p] - x0[p];
+    pre1[p] = r1[p] - x1[p];
+  }
+  float carry = 0.0f;
+  if (len >= 32 * NCH) {
+    // full tile: every chunk ends at its row's lane 15, odd element
+#pragma unroll
+    for (int p = 0; p < NP; ++p) {
+      const float tot1 = pre1[p] + x1[p];
+      float cj[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        cj[j] = carry;
+        if (4 * p + j < NCH) carry = carry + __int_as_float(__builtin_amdgcn_readlane(__float_as_int(tot1), 16 * j + 15));
+      }
+      car[p] = (jrow == 0) ? cj[0] : (jrow == 1) ? cj[1] : (jrow == 2) ? cj[2] : cj[3];
+    }
+#pragma unroll
+    for (int p = 0; p < NP; ++p) {
+      const float pg0 = car[p] + pre0[p];
+      const float pg1 = car[p] + pre1[p];
+      c0[p] = count_from_floors(a0, pg0, pg0 + x0[p]);
+      c1[p] = count_from_floors(a0, pg1, pg1 + x1[p]);
+      if (32 * (4 * p + jrow) >= 32 * NCH) {  // rows past BN (BN < 128)
+        c0[p] = 0;
+        c1[p] = 0;
+      }
+    }
+    return;
+  }
+#pragma unroll
+  for (int p = 0; p < NP; ++p) {
+    const float tot0 = pre0[p] + x0[p];
+    const float tot1 = pre1[p] + x1[p];
     float cj[4];
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
@@ -216,10 +289,13 @@ __device__ __forceinline__ void systematic_counts(const float (&x0)[NP], const f
         carry = carry + tot;
       }
     }
-    const float car = (jrow == 0) ? cj[0] : (jrow == 1) ? cj[1] : (jrow == 2) ? cj[2] : cj[3];
+    car[p] = (jrow == 0) ? cj[0] : (jrow == 1) ? cj[1] : (jrow == 2) ? cj[2] : cj[3];
+  }
+#pragma unroll
+  for (int p = 0; p < NP; ++p) {
     const int row = 32 * (4 * p + jrow) + 2 * qq;
-    const float pg0 = car + pre0;
-    const float pg1 = car + pre1;
+    const float pg0 = car[p] + pre0[p];
+    const float pg1 = car[p] + pre1[p];
     c0[p] = (row < len) ? count_from_floors(a0, pg0, pg0 + x0[p]) : 0;
     c1[p] = (row + 1 < len) ? count_from_floors(a0, pg1, pg1 + x1[p]) : 0;
   }

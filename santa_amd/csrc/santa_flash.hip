@@ -139,6 +139,12 @@ __device__ __forceinline__ int union_rows(const uint64_t* s_mask, int lane) {
   return e;
 }
 
+// Tile max of head g from the four waves' order-key maxima.
+template <int GH>
+__device__ __forceinline__ float tile_max_of(const int* s_wmax, int g) {
+  return from_order_key(max(max(s_wmax[g], s_wmax[GH + g]), max(s_wmax[2 * GH + g], s_wmax[3 * GH + g])));
+}
+
 template <bool BF16, int GH, int BN, int MODE>
 __global__ __launch_bounds__(kThreads, 2) void tile_kernel(
     const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K, const uint16_t* __restrict__ V, int H, int KVH,
@@ -174,7 +180,7 @@ __global__ __launch_bounds__(kThreads, 2) void tile_kernel(
 
   __shared__ float s_sc[BN * GH];          // scores, [row][head]
   __shared__ uint16_t s_ub[GH * BN];       // 16-bit u, [head][row]
-  __shared__ float s_wmax[4 * GH];
+  __shared__ int s_wmax[4 * GH];           // wave maxima as order keys
   __shared__ float s_W[NWS * GH];
   __shared__ uint64_t s_mask[GH * NPAIR * 2];
 
@@ -359,8 +365,8 @@ __global__ __launch_bounds__(kThreads, 2) void tile_kernel(
     // ---- B: tile max per head (A.3) ------------------------------------------
 #pragma unroll
     for (int g = 0; g < GH; ++g) {
-      const float mx = wave_max_dpp(lmax[g]);
-      if (lane == 0) s_wmax[wave * GH + g] = mx;
+      const int mk = wave_max_key_lane63(order_key(lmax[g]));
+      if (lane == 63) s_wmax[wave * GH + g] = mk;
     }
     __syncthreads();  // (1) scores and wave maxima visible
     if constexpr (MODE == kOnline) {
@@ -375,9 +381,7 @@ __global__ __launch_bounds__(kThreads, 2) void tile_kernel(
       if (tid < NSLAB * GH) {
         const int g = tid % GH;
         const int w = tid / GH;
-        float mg = s_wmax[g];
-#pragma unroll
-        for (int ww = 1; ww < 4; ++ww) mg = fmaxf(mg, s_wmax[ww * GH + g]);
+        const float mg = tile_max_of<GH>(s_wmax, g);
         float part_ell = 0.0f;
 #pragma unroll
         for (int j = 0; j < 16; ++j) {
@@ -391,31 +395,30 @@ __global__ __launch_bounds__(kThreads, 2) void tile_kernel(
         s_W[w * GH + g] = part_ell;
       }
     } else if (tid < NT_REF) {
-      // Thread tid plays the reference's thread tid: items idx = tid + NT_REF k.
+      // Thread tid plays the reference's thread tid: items idx = tid + NT_REF k,
+      // valid while idx < len * GH (a prefix in k).  Invalid items add +0.
       const int g = tid % GH;
-      float mg = s_wmax[g];
-#pragma unroll
-      for (int w = 1; w < 4; ++w) mg = fmaxf(mg, s_wmax[w * GH + g]);
+      const float mg = tile_max_of<GH>(s_wmax, g);
       float sv[KC];
 #pragma unroll
-      for (int k = 0; k < KC; ++k) {
-        const int idx = tid + NT_REF * k;
-        sv[k] = (idx < len * GH) ? s_sc[idx] : 0.0f;
-      }
+      for (int k = 0; k < KC; ++k) sv[k] = s_sc[tid + NT_REF * k];
       float acc = 0.0f;
 #pragma unroll
       for (int k = 0; k < KC; ++k) {
         const int idx = tid + NT_REF * k;
-        if (idx < len * GH) {
-          const float u = santa_expf(sv[k] - mg);
-          acc += u;
-          s_ub[g * BN + idx / GH] = f32_to_h16<BF16>(u);
-        }
+        const float u = santa_expf(sv[k] - mg);
+        acc += (idx < len * GH) ? u : 0.0f;
+        s_ub[g * BN + idx / GH] = f32_to_h16<BF16>(u);
       }
-      // the reference's 32-lane tree for lane g of each warp: pairs at lane
-      // distance 16, 8, ... GH; the remaining levels only add +0.
-#pragma unroll
-      for (int m = 16; m >= GH; m >>= 1) acc = acc + __shfl_xor(acc, m, 32);
+      // the reference's 32-lane __shfl_down tree for lane g: pairs at lane
+      // distance 16, 8, ... GH (the remaining levels only add +0).  Distance
+      // 16 crosses 16-lane rows (permlane16 swap); 8 and 4 stay inside.
+      {
+        const auto sw = __builtin_amdgcn_permlane16_swap(__float_as_uint(acc), __float_as_uint(acc), false, false);
+        acc = acc + __uint_as_float(sw[1]);  // lanes of rows 0 and 2 (the ones used)
+      }
+      if constexpr (GH <= 8) acc = acc + dpp_shl_zero<8>(acc);
+      if constexpr (GH <= 4) acc = acc + dpp_shl_zero<4>(acc);
       if ((tid & 31) < GH) s_W[(tid >> 5) * GH + (tid & 31)] = acc;
     }
     __syncthreads();  // (2) 16-bit u and warp masses visible
@@ -425,9 +428,7 @@ __global__ __launch_bounds__(kThreads, 2) void tile_kernel(
 #pragma unroll
       for (int k = 0; k < HPW; ++k) {
         const int g = wave + 4 * k;
-        float mg = s_wmax[g];
-#pragma unroll
-        for (int w = 1; w < 4; ++w) mg = fmaxf(mg, s_wmax[w * GH + g]);
+        const float mg = tile_max_of<GH>(s_wmax, g);
         float ell = 0.0f;
 #pragma unroll
         for (int w = 0; w < NWS; ++w) ell += s_W[w * GH + g];
@@ -461,9 +462,7 @@ __global__ __launch_bounds__(kThreads, 2) void tile_kernel(
     for (int k = 0; k < HPW; ++k) {
       const int g = wave + 4 * k;
       const int h = h0 + g;
-      float mg = s_wmax[g];
-#pragma unroll
-      for (int w = 1; w < 4; ++w) mg = fmaxf(mg, s_wmax[w * GH + g]);
+      const float mg = tile_max_of<GH>(s_wmax, g);
       float ell = 0.0f;
 #pragma unroll
       for (int w = 0; w < NW_REF; ++w) ell += s_W[w * GH + g];
