@@ -166,10 +166,13 @@ __global__ __launch_bounds__(kThreads, 2) void tile_kernel(
   constexpr int LCAP = (MODE == kOnline) ? kListCap : (PASS1 ? 1 : BN);  // sampled rows buffered per head
 
   const int wg = static_cast<int>(blockIdx.x);
-  const int bk = wg / cpg;  // b * KVH + kv
-  const int chunk = wg - bk * cpg;
-  const int kv = bk % KVH;
-  const int b = bk / KVH;
+  // wg = (b * cpg + chunk) * KVH + kv: the KV heads of one chunk of tokens are
+  // neighbours in launch order, so they run together and read whole token rows
+  // (KVH x 256 B) of the NHD cache at about the same time.
+  const int kv = wg % KVH;
+  const int chunk = (wg / KVH) % cpg;
+  const int b = wg / (KVH * cpg);
+  const int bk = b * KVH + kv;
   const int h0 = kv * GH;
   const int t_begin = chunk * cs;
   const int t_end = min(T_c, t_begin + cs);
@@ -682,12 +685,14 @@ __global__ __launch_bounds__(kD) void merge_kernel(const float* __restrict__ par
   const int g = h % GH;
   const int bk = b * KVH + kv;
   const int d = static_cast<int>(threadIdx.x);
-  const float* pb = part + (static_cast<size_t>(bk) * cpg * GH + g) * kPartStride;
+  // chunk c of (b, kv) was workgroup (b * cpg + c) * KVH + kv
+  const float* pb = part + ((static_cast<size_t>(b) * cpg * KVH + kv) * GH + g) * kPartStride;
+  const size_t cstride = static_cast<size_t>(KVH) * GH * kPartStride;
   float ms = -__builtin_inff();
-  for (int c = 0; c < cpg; ++c) ms = fmaxf(ms, pb[static_cast<size_t>(c) * GH * kPartStride]);
+  for (int c = 0; c < cpg; ++c) ms = fmaxf(ms, pb[c * cstride]);
   float Z = 0.0f, num = 0.0f;
   for (int c = 0; c < cpg; ++c) {
-    const float* pc = pb + static_cast<size_t>(c) * GH * kPartStride;
+    const float* pc = pb + c * cstride;
     const float w = santa_expf(pc[0] - ms);
     Z = fmaf(w, pc[1], Z);
     num = fmaf(w, pc[2 + d], num);
@@ -697,7 +702,7 @@ __global__ __launch_bounds__(kD) void merge_kernel(const float* __restrict__ par
   if (d == 0 && m_star) m_star[bh] = ms;
   if (vrows && g == 0 && d == 0) {
     int e = 0;
-    for (int c = 0; c < cpg; ++c) e += part_emit[static_cast<size_t>(bk) * cpg + c];
+    for (int c = 0; c < cpg; ++c) e += part_emit[(static_cast<size_t>(b) * cpg + c) * KVH + kv];
     vrows[bk] = e;
   }
 }

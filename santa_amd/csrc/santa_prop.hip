@@ -207,10 +207,13 @@ __global__ __launch_bounds__(kThreads) void pass2_kernel(const uint16_t* __restr
   constexpr int NM = 2 * NPAIR;  // 64-bit row masks per head and tile
 
   const int wg = static_cast<int>(blockIdx.x);
-  const int bk = wg / cpg;
-  const int chunk = wg - bk * cpg;
-  const int kv = bk % KVH;
-  const int b = bk / KVH;
+  // wg = (b * cpg + chunk) * KVH + kv: the KV heads of one chunk of tokens are
+  // neighbours in launch order, so they run together and read whole token rows
+  // (KVH x 256 B) of the NHD cache at about the same time.
+  const int kv = wg % KVH;
+  const int chunk = (wg / KVH) % cpg;
+  const int b = wg / (KVH * cpg);
+  const int bk = b * KVH + kv;
   const int h0 = kv * GH;
   const int t_begin = chunk * cs;
   const int t_end = min(T_c, t_begin + cs);
@@ -361,13 +364,14 @@ __global__ __launch_bounds__(kD) void finalize_kernel(const float* __restrict__ 
   const int g = h % GH;
   const int bk = b * KVH + kv;
   const int d = static_cast<int>(threadIdx.x);
-  const float* pb = part + (static_cast<size_t>(bk) * cpg * GH + g) * kD + d;
+  // chunk c of (b, kv) was workgroup (b * cpg + c) * KVH + kv
+  const float* pb = part + ((static_cast<size_t>(b) * cpg * KVH + kv) * GH + g) * kD + d;
   float s = 0.0f;
-  for (int c = 0; c < cpg; ++c) s += pb[static_cast<size_t>(c) * GH * kD];
+  for (int c = 0; c < cpg; ++c) s += pb[static_cast<size_t>(c) * KVH * GH * kD];
   out[static_cast<size_t>(bh) * kD + d] = f32_to_h16<BF16>(s * scale_out);
   if (vrows && g == 0 && d == 0) {
     int e = 0;
-    for (int c = 0; c < cpg; ++c) e += part_emit[static_cast<size_t>(bk) * cpg + c];
+    for (int c = 0; c < cpg; ++c) e += part_emit[(static_cast<size_t>(b) * cpg + c) * KVH + kv];
     vrows[bk] = e;
   }
 }
