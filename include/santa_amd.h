@@ -148,6 +148,21 @@ int santa_prop_decode(const void* q, const void* K, const void* V, int dtype, in
                       int block_n, int pass1_path, int S, uint64_t seed, void* out, float* m_star, int* vrows,
                       void* workspace, size_t workspace_bytes, hipStream_t stream);
 
+/* Batched, ragged santa_prop (no counterpart in the reference, whose adapter
+ * loops over sequences, tutorial_code/attention_backends.py:491-500): B
+ * sequences of a [B, L_storage, KVH, D] cache, sequence b decoded exactly as
+ * santa_prop_decode on its first seq_lens[b] tokens with budget seq_S[b]
+ * (RNG key h, as in the per-sequence calls).  seq_lens, seq_S: device int
+ * arrays [B]; max_len = max seq_lens; total_tiles = sum over b of
+ * ceil(seq_lens[b] / block_n); every sequence uses the same block_n and
+ * pass-1 path.  out [B,H,D], m_star [B,H], vrows [B,KVH] (may be NULL). */
+size_t santa_prop_batched_workspace_size(int B, int H, int KVH, int D, int L_storage, int max_tiles,
+                                         long long total_tiles);
+int santa_prop_decode_batched(const void* q, const void* K, const void* V, int dtype, int B, int H, int KVH, int D,
+                              int L_storage, const int* seq_lens, const int* seq_S, int max_len, long long total_tiles,
+                              int block_n, int pass1_path, uint64_t seed, void* out, float* m_star, int* vrows,
+                              void* workspace, size_t workspace_bytes, hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -8,9 +8,11 @@
 #include <c10/core/DeviceGuard.h>
 #include <c10/hip/HIPStream.h>
 
+#include <algorithm>
 #include <cstdint>
 #include <cstdlib>
 #include <tuple>
+#include <vector>
 
 #include "santa_amd.h"
 
@@ -124,12 +126,123 @@ std::vector<at::Tensor> debug_pass(at::Tensor q_h, at::Tensor K_g, at::Tensor V_
   return {m_tiles, ell_tiles, m_star, S_tiles, invdelta, a0, stash, counts, out, vrows};
 }
 
+// A Python int (same value for every sequence) or a length-B sequence / 1-D
+// tensor of ints.
+std::vector<int64_t> per_sequence(const py::object& v, int64_t B, const char* name) {
+  std::vector<int64_t> out;
+  if (py::isinstance<py::int_>(v)) {
+    out.assign(static_cast<size_t>(B), v.cast<int64_t>());
+    return out;
+  }
+  if (THPVariable_Check(v.ptr())) {
+    const at::Tensor t = v.cast<at::Tensor>().to(at::kCPU).to(at::kLong).contiguous();
+    TORCH_CHECK(t.dim() == 1 && t.numel() == B, name, " must be an int or have one entry per sequence (", B, ")");
+    const int64_t* p = t.data_ptr<int64_t>();
+    out.assign(p, p + B);
+    return out;
+  }
+  out = v.cast<std::vector<int64_t>>();
+  TORCH_CHECK(static_cast<int64_t>(out.size()) == B, name, " must be an int or have one entry per sequence (", B, ")");
+  return out;
+}
+
+// Batched (and ragged) santa_prop: q_h [B,H,D], K_g/V_g [B,L_storage,KVH,D];
+// S and valid_len are ints or per-sequence lists / tensors.  Sequence b is
+// decoded exactly as decode_systematic_scalar on K_g[b, :valid_len[b]] with
+// budget S[b].  Returns (out [B,H,D], m_star [B,H], vrows [B,KVH] or [0]).
+std::tuple<at::Tensor, at::Tensor, at::Tensor> decode_batched(at::Tensor q_h, at::Tensor K_g, at::Tensor V_g,
+                                                              py::object S, uint64_t seed, int64_t block_n,
+                                                              bool want_vrows, py::object valid_len) {
+  TORCH_CHECK(q_h.is_cuda(), "q_h must be CUDA");
+  TORCH_CHECK(K_g.is_cuda() && V_g.is_cuda(), "K_g and V_g must be CUDA");
+  TORCH_CHECK((q_h.scalar_type() == at::kBFloat16 || q_h.scalar_type() == at::kHalf), "q_h must be bf16 or f16");
+  TORCH_CHECK((K_g.scalar_type() == at::kBFloat16 || K_g.scalar_type() == at::kHalf) &&
+                  K_g.scalar_type() == V_g.scalar_type(),
+              "K_g/V_g must be bf16 or f16 and match");
+  TORCH_CHECK(q_h.scalar_type() == K_g.scalar_type(), "q_h dtype must match K_g/V_g");
+  TORCH_CHECK(q_h.dim() == 3 && K_g.dim() == 4 && V_g.dim() == 4,
+              "Batched path expects q_h [B,H,D], K_g/V_g [B,L,KVH,D]");
+  TORCH_CHECK(q_h.device() == K_g.device() && q_h.device() == V_g.device(), "device mismatch");
+  TORCH_CHECK(K_g.sizes() == V_g.sizes(), "K_g and V_g must have the same shape");
+  TORCH_CHECK(q_h.size(0) == K_g.size(0), "Batch mismatch between q_h and K_g/V_g");
+  TORCH_CHECK(q_h.size(2) == K_g.size(3), "D mismatch (q_h.size(2) vs K_g.size(3))");
+  TORCH_CHECK(K_g.size(2) > 0 && q_h.size(1) % K_g.size(2) == 0,
+              "H must be divisible by KVH (expected KVH == K_g.size(2) for NHD)");
+  TORCH_CHECK(K_g.is_contiguous() && V_g.is_contiguous(), "K_g/V_g must be contiguous with layout [B, L, KVH, D] (NHD)");
+  const int B = static_cast<int>(q_h.size(0)), H = static_cast<int>(q_h.size(1)), D = static_cast<int>(q_h.size(2));
+  const int L_st = static_cast<int>(K_g.size(1)), KVH = static_cast<int>(K_g.size(2));
+  const std::vector<int64_t> Ss = per_sequence(S, B, "S");
+  std::vector<int64_t> lens = per_sequence(valid_len, B, "valid_len");
+  const char* env = std::getenv("SANTA_PASS1");
+  std::vector<int> bn(B), tc(B), path(B);
+  for (int b = 0; b < B; ++b) {
+    if (lens[b] <= 0) lens[b] = L_st;
+    TORCH_CHECK(lens[b] <= L_st, "valid_len exceeds storage length: valid_len=", lens[b], " storage=", L_st);
+    const int rc = santa_prop_plan(static_cast<int>(lens[b]), H, KVH, D, block_n, env, &bn[b], &tc[b], &path[b]);
+    TORCH_CHECK(rc == SANTA_OK, santa_last_error());
+  }
+  c10::DeviceGuard guard(q_h.device());
+  const at::Tensor q = aligned_q(q_h);
+  const int dtype = (q.scalar_type() == at::kBFloat16) ? SANTA_BF16 : SANTA_F16;
+  TORCH_CHECK(reinterpret_cast<uintptr_t>(K_g.data_ptr()) % 16 == 0 && reinterpret_cast<uintptr_t>(V_g.data_ptr()) % 4 == 0,
+              "K_g/V_g storage must be 16-byte aligned");
+  auto optsF = q.options().dtype(at::kFloat);
+  auto optsI = q.options().dtype(at::kInt);
+  at::Tensor out = at::empty({B, H, D}, q.options());
+  at::Tensor m_star = at::empty({B, H}, optsF);
+  at::Tensor vrows = want_vrows ? at::empty({B, KVH}, optsI) : at::empty({0}, optsI);
+  hipStream_t st = current_stream(q);
+  bool uniform = true;
+  for (int b = 1; b < B; ++b) uniform = uniform && bn[b] == bn[0] && path[b] == path[0];
+  if (uniform) {
+    long long total = 0;
+    int max_len = 0, max_tiles = 0;
+    std::vector<int32_t> host(2 * static_cast<size_t>(B));
+    for (int b = 0; b < B; ++b) {
+      total += tc[b];
+      max_len = std::max(max_len, static_cast<int>(lens[b]));
+      max_tiles = std::max(max_tiles, tc[b]);
+      host[b] = static_cast<int32_t>(lens[b]);
+      host[B + b] = static_cast<int32_t>(Ss[b]);
+    }
+    at::Tensor meta = at::from_blob(host.data(), {2 * B}, at::TensorOptions().dtype(at::kInt)).to(q.device());
+    const size_t ws_bytes = santa_prop_batched_workspace_size(B, H, KVH, D, L_st, max_tiles, total);
+    at::Tensor ws = at::empty({static_cast<int64_t>(ws_bytes)}, q.options().dtype(at::kByte));
+    const int rc = santa_prop_decode_batched(q.data_ptr(), K_g.data_ptr(), V_g.data_ptr(), dtype, B, H, KVH, D, L_st,
+                                             meta.data_ptr<int>(), meta.data_ptr<int>() + B, max_len, total, bn[0],
+                                             path[0], seed, out.data_ptr(), m_star.data_ptr<float>(),
+                                             want_vrows ? vrows.data_ptr<int>() : nullptr, ws.data_ptr(), ws_bytes, st);
+    TORCH_CHECK(rc == SANTA_OK, santa_last_error());
+    return std::make_tuple(out, m_star, vrows);
+  }
+  // sequences on different block sizes / pass-1 paths: one launch sequence each
+  const size_t row = static_cast<size_t>(KVH) * D * K_g.element_size();
+  for (int b = 0; b < B; ++b) {
+    const size_t ws_bytes = santa_prop_workspace_size(H, KVH, D, static_cast<int>(lens[b]), tc[b]);
+    at::Tensor ws = at::empty({static_cast<int64_t>(ws_bytes)}, q.options().dtype(at::kByte));
+    const char* Kb = static_cast<const char*>(K_g.data_ptr()) + static_cast<size_t>(b) * L_st * row;
+    const char* Vb = static_cast<const char*>(V_g.data_ptr()) + static_cast<size_t>(b) * L_st * row;
+    const int rc = santa_prop_decode(static_cast<const char*>(q.data_ptr()) + static_cast<size_t>(b) * H * D * q.element_size(),
+                                     Kb, Vb, dtype, H, KVH, D, static_cast<int>(lens[b]), bn[b], path[b],
+                                     static_cast<int>(Ss[b]), seed,
+                                     static_cast<char*>(out.data_ptr()) + static_cast<size_t>(b) * H * D * out.element_size(),
+                                     m_star.data_ptr<float>() + static_cast<size_t>(b) * H,
+                                     want_vrows ? vrows.data_ptr<int>() + static_cast<size_t>(b) * KVH : nullptr,
+                                     ws.data_ptr(), ws_bytes, st);
+    TORCH_CHECK(rc == SANTA_OK, santa_last_error());
+  }
+  return std::make_tuple(out, m_star, vrows);
+}
+
 }  // namespace
 
 PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
   m.doc() = "S^2ANTA-Prop sampled-attention decode for MI355X (gfx950)";
   m.def("decode_systematic_scalar", &decode_systematic_scalar, py::arg("q_h"), py::arg("K_g"), py::arg("V_g"),
         py::arg("S"), py::arg("seed") = 42ULL, py::arg("block_n") = 0, py::arg("want_vrows") = false);
+  m.def("decode_systematic_batched", &decode_batched, py::arg("q_h"), py::arg("K_g"), py::arg("V_g"), py::arg("S"),
+        py::arg("seed") = 42ULL, py::arg("block_n") = 0, py::arg("want_vrows") = false,
+        py::arg("valid_len") = py::int_(-1));
   m.def("_debug_pass", &debug_pass, py::arg("q_h"), py::arg("K_g"), py::arg("V_g"), py::arg("S"),
         py::arg("seed") = 42ULL, py::arg("block_n") = 0);
   m.def("_library_version", []() { return std::string(santa_version()); });

@@ -130,6 +130,61 @@ __device__ __forceinline__ int count_from_floors(float a0, float pg, float cum) 
   return c > 32767 ? 32767 : c;
 }
 
+// ---------------------------------------------------------------- grids
+// Position of workgroup wg in a persistent chunked grid.  Uniform form: every
+// sequence has T_c tiles in cpg chunks of cs tiles, wg = (b * cpg + chunk) *
+// KVH + kv.  Ragged form (seq_lens != nullptr): sequence b has
+// T_b = ceil(seq_lens[b] / BN) tiles in ceil(T_b / cs) chunks, and its
+// workgroups follow those of sequences 0 .. b-1 (kv fastest); workgroups past
+// the last sequence get an empty tile range (b = -1).
+// Length of sequence b of a ragged batch, clamped to [1, max_rows] so that a
+// malformed length can only give wrong numbers, never an access outside the
+// [B, L_storage] cache or the [B, H, T_c] tile arrays.
+__device__ __forceinline__ int ragged_len(const int* seq_lens, int b, int max_rows) {
+  return min(max(seq_lens[b], 1), max_rows);
+}
+
+struct GridPos {
+  int b, kv, chunk, len, n_tiles, wg_base;
+};
+__device__ __forceinline__ GridPos grid_pos(int wg, const int* seq_lens, int B, int KVH, int BN, int L_valid, int T_c,
+                                            int cs, int cpg) {
+  GridPos p;
+  if (!seq_lens) {
+    p.kv = wg % KVH;
+    p.chunk = (wg / KVH) % cpg;
+    p.b = wg / (KVH * cpg);
+    p.len = L_valid;
+    p.n_tiles = T_c;
+    p.wg_base = p.b * cpg * KVH;
+    return p;
+  }
+  int base = 0;
+  p.b = -1;
+  p.kv = 0;
+  p.chunk = 0;
+  p.len = 0;
+  p.n_tiles = 0;
+  p.wg_base = 0;
+  for (int bb = 0; bb < B; ++bb) {
+    const int len = ragged_len(seq_lens, bb, L_valid);
+    const int tiles = (len + BN - 1) / BN;
+    const int n = KVH * ((tiles + cs - 1) / cs);
+    if (wg < base + n) {
+      const int local = wg - base;
+      p.b = bb;
+      p.kv = local % KVH;
+      p.chunk = local / KVH;
+      p.len = len;
+      p.n_tiles = tiles;
+      p.wg_base = base;
+      break;
+    }
+    base += n;
+  }
+  return p;
+}
+
 // ---------------------------------------------------------------- DPP
 // gfx9 DPP controls used by the 8-lane score tree.
 enum : int {

@@ -151,7 +151,7 @@ __global__ __launch_bounds__(kThreads, 2) void tile_kernel(
     int L_valid, int L_storage, int T_c, int cs, int cpg, float q_scale, int S_pt, uint64_t seed,
     float* __restrict__ m_tiles, float* __restrict__ ell_tiles, float* __restrict__ out_tiles,
     int* __restrict__ emit_cnt, int16_t* __restrict__ dbg_counts, float* __restrict__ part,
-    int* __restrict__ part_emit, uint16_t* __restrict__ u_stash) {
+    int* __restrict__ part_emit, uint16_t* __restrict__ u_stash, const int* __restrict__ seq_lens, int B) {
   static_assert(BN == 32 || BN == 64 || BN == 256, "block_n");
   static_assert(GH == 4 || GH == 8, "group size");
   constexpr int NT_REF = (BN == 256) ? 256 : 128;  // reference block size (launchers :521,:559)
@@ -166,16 +166,19 @@ __global__ __launch_bounds__(kThreads, 2) void tile_kernel(
   constexpr int LCAP = (MODE == kOnline) ? kListCap : (PASS1 ? 1 : BN);  // sampled rows buffered per head
 
   const int wg = static_cast<int>(blockIdx.x);
-  // wg = (b * cpg + chunk) * KVH + kv: the KV heads of one chunk of tokens are
-  // neighbours in launch order, so they run together and read whole token rows
-  // (KVH x 256 B) of the NHD cache at about the same time.
-  const int kv = wg % KVH;
-  const int chunk = (wg / KVH) % cpg;
-  const int b = wg / (KVH * cpg);
+  // The KV heads of one chunk of tokens are neighbours in launch order, so
+  // they run together and read whole token rows (KVH x 256 B) of the NHD
+  // cache at about the same time.  T_c is the tile stride of the per-tile
+  // outputs (the longest sequence's tile count in the ragged form).
+  const GridPos gp = grid_pos(wg, seq_lens, B, KVH, BN, L_valid, T_c, cs, cpg);
+  const int kv = gp.kv;
+  const int chunk = gp.chunk;
+  const int b = gp.b < 0 ? 0 : gp.b;
   const int bk = b * KVH + kv;
   const int h0 = kv * GH;
+  L_valid = gp.len;  // this sequence's valid length from here on
   const int t_begin = chunk * cs;
-  const int t_end = min(T_c, t_begin + cs);
+  const int t_end = (gp.b < 0) ? t_begin : min(gp.n_tiles, t_begin + cs);
 
   const int tid = static_cast<int>(threadIdx.x);
   const int lane = tid & 63;
@@ -720,17 +723,21 @@ struct Args {
   int* part_emit;
   int cs, cpg;
   uint16_t* u_stash;
+  const int* seq_lens;  // ragged form (prop pass 1) or nullptr
+  int n_wg;             // grid size of the ragged form
 };
 
 template <bool BF16, int GH, int BN, int MODE>
 static hipError_t launch_t(const Args& a, hipStream_t stream) {
   const float q_scale = 1.0f / sqrtf(static_cast<float>(kD));
-  const unsigned grid = static_cast<unsigned>(a.B) * static_cast<unsigned>(a.KVH) * static_cast<unsigned>(a.cpg);
+  const unsigned grid = a.seq_lens ? static_cast<unsigned>(a.n_wg)
+                                   : static_cast<unsigned>(a.B) * static_cast<unsigned>(a.KVH) * static_cast<unsigned>(a.cpg);
+  if (grid == 0) return hipSuccess;
   hipLaunchKernelGGL((tile_kernel<BF16, GH, BN, MODE>), dim3(grid), dim3(kThreads), 0, stream,
                      static_cast<const uint16_t*>(a.q), static_cast<const uint16_t*>(a.K),
                      static_cast<const uint16_t*>(a.V), a.H, a.KVH, a.L_valid, a.L_storage, a.T_c, a.cs, a.cpg,
                      q_scale, a.S_pt, a.seed, a.m_tiles, a.ell_tiles, a.out_tiles, a.emit_cnt, a.counts, a.part,
-                     a.part_emit, a.u_stash);
+                     a.part_emit, a.u_stash, a.seq_lens, a.B);
   return hipGetLastError();
 }
 
@@ -798,10 +805,17 @@ hipError_t launch_expf(const float* x, float* y, size_t n, hipStream_t stream) {
 // santa_prop pass 1 on the tile kernel (declared in santa_internal.h).
 hipError_t launch_prop_pass1(const void* q, const void* K, int dtype, int B, int H, int KVH, int L, int L_storage,
                              int block_n, int path, float* m_tiles, float* ell_tiles, uint16_t* u_stash,
-                             hipStream_t stream) {
+                             const int* seq_lens, int cs, int n_wg, hipStream_t stream) {
   Args a{q, K, nullptr, B, H, KVH, L, L_storage, (L + block_n - 1) / block_n, 0, 0, m_tiles, ell_tiles, nullptr,
-         nullptr, nullptr, nullptr, nullptr, 0, 0, u_stash};
-  chunk_plan(B, KVH, a.T_c, &a.cs, &a.cpg);
+         nullptr, nullptr, nullptr, nullptr, 0, 0, u_stash, seq_lens};
+  if (seq_lens) {
+    // ragged: L is the longest sequence; n_wg workgroups of cs tiles
+    a.cs = cs;
+    a.cpg = 0;
+    a.n_wg = n_wg;
+  } else {
+    chunk_plan(B, KVH, a.T_c, &a.cs, &a.cpg);
+  }
   const int GH = H / KVH;
   if (path == 0) {
     return (dtype == SANTA_BF16) ? launch_t<true, 4, 256, kPass1Vec>(a, stream)
@@ -816,6 +830,17 @@ hipError_t launch_prop_pass1(const void* q, const void* K, int dtype, int B, int
 
 // Tile chunking shared with santa_prop's pass 2.
 void plan_chunks(int B, int KVH, int T_c, int* cs, int* cpg) { chunk_plan(B, KVH, T_c, cs, cpg); }
+
+// Ragged batches: about one resident round over all (kv, tile) items; each
+// sequence adds at most one partial chunk per KV head.
+void plan_ragged(int B, int KVH, long long total_tiles, int* cs, int* n_wg) {
+  const long long items = total_tiles * KVH;
+  long long want = resident_workgroups();
+  long long c = (items + want - 1) / want;
+  if (c < 1) c = 1;
+  *cs = static_cast<int>(c);
+  *n_wg = static_cast<int>(KVH * ((total_tiles + c - 1) / c + B));
+}
 
 }  // namespace flash
 }  // namespace santa

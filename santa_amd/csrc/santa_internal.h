@@ -20,9 +20,15 @@ namespace flash {
 // santa_prop pass 1 on the flash tile kernel: per-tile m, ell [B, H, T_c] and
 // the 16-bit u stash [B, L_storage, H].  path 0 = vec numerics (GH 4,
 // block_n 256), 1 = general numerics.  Shapes are checked by the caller.
+// Ragged form: seq_lens (device, [B]) holds each sequence's length, L the
+// longest (it sets the tile stride of m/ell), cs tiles per chunk and n_wg
+// workgroups (any workgroup past the last sequence exits at once).
 hipError_t launch_prop_pass1(const void* q, const void* K, int dtype, int B, int H, int KVH, int L, int L_storage,
                              int block_n, int path, float* m_tiles, float* ell_tiles, uint16_t* u_stash,
-                             hipStream_t stream);
+                             const int* seq_lens, int cs, int n_wg, hipStream_t stream);
+// Chunking of a ragged batch with total_tiles tiles: cs tiles per chunk and
+// an upper bound n_wg on the workgroups of the ragged grid.
+void plan_ragged(int B, int KVH, long long total_tiles, int* cs, int* n_wg);
 // y[i] = santa_expf(x[i]) on the device (test hook for the exponential).
 hipError_t launch_expf(const float* x, float* y, size_t n, hipStream_t stream);
 // Chunks of cs tiles per workgroup, cpg chunks per (b, kv) group, sized to

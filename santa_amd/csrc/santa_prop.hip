@@ -44,7 +44,9 @@ __global__ __launch_bounds__(kBudgetThreads) void budgets_kernel(const float* __
                                                                  int S, uint64_t seed, float* __restrict__ m_star,
                                                                  int* __restrict__ S_tiles,
                                                                  float* __restrict__ invdelta,
-                                                                 float* __restrict__ a0_tile) {
+                                                                 float* __restrict__ a0_tile,
+                                                                 const int* __restrict__ seq_lens,
+                                                                 const int* __restrict__ seq_S, int BN) {
   extern __shared__ float smem[];
   float* frac = smem;
   int* idx = reinterpret_cast<int*>(smem + T_c);
@@ -55,7 +57,10 @@ __global__ __launch_bounds__(kBudgetThreads) void budgets_kernel(const float* __
   const int bh = static_cast<int>(blockIdx.x);
   const int h = bh % H;
   const int tid = static_cast<int>(threadIdx.x);
-  const size_t off = static_cast<size_t>(bh) * T_c;
+  const size_t off = static_cast<size_t>(bh) * T_c;  // T_c: tile stride of the [B, H, T_c] arrays
+  // ragged batches: this sequence's tile count and budget
+  if (seq_lens) T_c = (ragged_len(seq_lens, bh / H, T_c * BN) + BN - 1) / BN;
+  if (seq_S) S = seq_S[bh / H];
   const float* mt = m_tiles + off;
   const float* lt = ell_tiles + off;
 
@@ -200,23 +205,24 @@ __global__ __launch_bounds__(kThreads) void pass2_kernel(const uint16_t* __restr
                                                          const float* __restrict__ invdelta,
                                                          const float* __restrict__ a0_tile,
                                                          int16_t* __restrict__ dbg_counts, float* __restrict__ part,
-                                                         int* __restrict__ part_emit, int want_emit) {
+                                                         int* __restrict__ part_emit, int want_emit,
+                                                         const int* __restrict__ seq_lens, int B) {
   constexpr int NCH = BN / 32;
   constexpr int NPAIR = (NCH + 3) / 4;
   constexpr int HPW = GH / 4;
   constexpr int NM = 2 * NPAIR;  // 64-bit row masks per head and tile
 
   const int wg = static_cast<int>(blockIdx.x);
-  // wg = (b * cpg + chunk) * KVH + kv: the KV heads of one chunk of tokens are
-  // neighbours in launch order, so they run together and read whole token rows
-  // (KVH x 256 B) of the NHD cache at about the same time.
-  const int kv = wg % KVH;
-  const int chunk = (wg / KVH) % cpg;
-  const int b = wg / (KVH * cpg);
-  const int bk = b * KVH + kv;
+  // The KV heads of one chunk of tokens are neighbours in launch order;
+  // T_c is the tile stride of the [B, H, T_c] budget arrays.
+  const GridPos gp = grid_pos(wg, seq_lens, B, KVH, BN, L, T_c, cs, cpg);
+  const int kv = gp.kv;
+  const int chunk = gp.chunk;
+  const int b = gp.b < 0 ? 0 : gp.b;
   const int h0 = kv * GH;
+  L = gp.len;  // this sequence's length from here on
   const int t_begin = chunk * cs;
-  const int t_end = min(T_c, t_begin + cs);
+  const int t_end = (gp.b < 0) ? t_begin : min(gp.n_tiles, t_begin + cs);
   const int tid = static_cast<int>(threadIdx.x);
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform for the compiler
@@ -356,7 +362,9 @@ template <bool BF16, int GH>
 __global__ __launch_bounds__(kD) void finalize_kernel(const float* __restrict__ part,
                                                       const int* __restrict__ part_emit, int H, int KVH, int cpg,
                                                       float scale_out, uint16_t* __restrict__ out,
-                                                      int* __restrict__ vrows) {
+                                                      int* __restrict__ vrows, const int* __restrict__ seq_lens,
+                                                      const int* __restrict__ seq_S, int BN, int cs,
+                                                      int max_rows, int n_wg) {
   const int bh = static_cast<int>(blockIdx.x);
   const int b = bh / H;
   const int h = bh % H;
@@ -364,55 +372,84 @@ __global__ __launch_bounds__(kD) void finalize_kernel(const float* __restrict__ 
   const int g = h % GH;
   const int bk = b * KVH + kv;
   const int d = static_cast<int>(threadIdx.x);
-  // chunk c of (b, kv) was workgroup (b * cpg + c) * KVH + kv
-  const float* pb = part + ((static_cast<size_t>(b) * cpg * KVH + kv) * GH + g) * kD + d;
+  // chunk c of (b, kv) was workgroup base_b + c * KVH + kv
+  int base = b * cpg * KVH;
+  int nch = cpg;
+  if (seq_lens) {
+    base = 0;
+    for (int bb = 0; bb < b; ++bb) base += KVH * (((ragged_len(seq_lens, bb, max_rows) + BN - 1) / BN + cs - 1) / cs);
+    nch = ((ragged_len(seq_lens, b, max_rows) + BN - 1) / BN + cs - 1) / cs;
+    // only the n_wg launched workgroups wrote partials
+    nch = max(0, min(nch, (n_wg - base - kv + KVH - 1) / KVH));
+  }
+  if (seq_S) scale_out = (seq_S[b] > 0) ? (1.0f / static_cast<float>(seq_S[b])) : 0.0f;
+  const float* pb = part + ((static_cast<size_t>(base) + kv) * GH + g) * kD + d;
   float s = 0.0f;
-  for (int c = 0; c < cpg; ++c) s += pb[static_cast<size_t>(c) * KVH * GH * kD];
+  for (int c = 0; c < nch; ++c) s += pb[static_cast<size_t>(c) * KVH * GH * kD];
   out[static_cast<size_t>(bh) * kD + d] = f32_to_h16<BF16>(s * scale_out);
   if (vrows && g == 0 && d == 0) {
     int e = 0;
-    for (int c = 0; c < cpg; ++c) e += part_emit[(static_cast<size_t>(b) * cpg + c) * KVH + kv];
+    for (int c = 0; c < nch; ++c) e += part_emit[static_cast<size_t>(base) + c * KVH + kv];
     vrows[bk] = e;
   }
 }
 
+// Grid: B * KVH * cpg workgroups (uniform) or n_wg (ragged, seq_lens set).
+struct Pass2Grid {
+  const int* seq_lens;
+  int n_wg;
+};
+
 template <bool BF16, int GH, int BN>
 static hipError_t launch_pass2_t(const uint16_t* V, const uint16_t* u_stash, int B, int H, int KVH, int L,
                                  int L_storage, int T_c, int cs, int cpg, const float* invdelta, const float* a0,
-                                 int16_t* counts, float* part, int* part_emit, int want_emit, hipStream_t stream) {
-  const unsigned grid = static_cast<unsigned>(B) * static_cast<unsigned>(KVH) * static_cast<unsigned>(cpg);
+                                 int16_t* counts, float* part, int* part_emit, int want_emit, Pass2Grid rg,
+                                 hipStream_t stream) {
+  const unsigned grid = rg.seq_lens ? static_cast<unsigned>(rg.n_wg)
+                                    : static_cast<unsigned>(B) * static_cast<unsigned>(KVH) * static_cast<unsigned>(cpg);
+  if (grid == 0) return hipSuccess;
   hipLaunchKernelGGL((pass2_kernel<BF16, GH, BN>), dim3(grid), dim3(kThreads), 0, stream, V, u_stash, H, KVH, L,
-                     L_storage, T_c, cs, cpg, invdelta, a0, counts, part, part_emit, want_emit);
+                     L_storage, T_c, cs, cpg, invdelta, a0, counts, part, part_emit, want_emit, rg.seq_lens, B);
   return hipGetLastError();
 }
 
 template <bool BF16, int GH>
 static hipError_t launch_pass2_bn(int bn, const uint16_t* V, const uint16_t* u_stash, int B, int H, int KVH, int L,
                                   int L_storage, int T_c, int cs, int cpg, const float* invdelta, const float* a0,
-                                  int16_t* counts, float* part, int* part_emit, int want_emit, hipStream_t stream) {
+                                  int16_t* counts, float* part, int* part_emit, int want_emit, Pass2Grid rg,
+                                  hipStream_t stream) {
   switch (bn) {
     case 32:
       return launch_pass2_t<BF16, GH, 32>(V, u_stash, B, H, KVH, L, L_storage, T_c, cs, cpg, invdelta, a0, counts,
-                                          part, part_emit, want_emit, stream);
+                                          part, part_emit, want_emit, rg, stream);
     case 64:
       return launch_pass2_t<BF16, GH, 64>(V, u_stash, B, H, KVH, L, L_storage, T_c, cs, cpg, invdelta, a0, counts,
-                                          part, part_emit, want_emit, stream);
+                                          part, part_emit, want_emit, rg, stream);
     default:
       return launch_pass2_t<BF16, GH, 256>(V, u_stash, B, H, KVH, L, L_storage, T_c, cs, cpg, invdelta, a0, counts,
-                                           part, part_emit, want_emit, stream);
+                                           part, part_emit, want_emit, rg, stream);
   }
 }
 
 // Workspace of one decode call (offsets 256-B aligned).
+// T_c is the tile stride of the [B, H, T_c] arrays (the longest sequence's
+// tile count); total_tiles >= 0 selects the ragged grid over that many tiles.
 struct PropWs {
   size_t m, ell, st, inv, a0, stash, part, emit, total;
-  int cs, cpg;
+  int cs, cpg, n_wg;
 };
-static PropWs prop_ws_layout(int B, int H, int KVH, int L_storage, int T_c) {
+static PropWs prop_ws_layout(int B, int H, int KVH, int L_storage, int T_c, long long total_tiles = -1) {
   PropWs w{};
-  flash::plan_chunks(B, KVH, T_c, &w.cs, &w.cpg);
+  size_t chunks;
+  if (total_tiles >= 0) {
+    flash::plan_ragged(B, KVH, total_tiles, &w.cs, &w.n_wg);
+    w.cpg = 0;
+    chunks = static_cast<size_t>(w.n_wg);
+  } else {
+    flash::plan_chunks(B, KVH, T_c, &w.cs, &w.cpg);
+    chunks = static_cast<size_t>(B) * KVH * w.cpg;
+  }
   const size_t bht = static_cast<size_t>(B) * H * T_c;
-  const size_t chunks = static_cast<size_t>(B) * KVH * w.cpg;
   size_t off = 0;
   w.m = off;
   off = align_up(off + bht * sizeof(float));
@@ -510,17 +547,18 @@ extern "C" int santa_prop_pass1(const void* q, const void* K, int dtype, int H, 
                      H / KVH, D, block_n);
   if (!q || !K || !m_tiles || !ell_tiles || !u_stash) return set_error(SANTA_ERR_INVALID, "null pointer argument");
   const hipError_t e = flash::launch_prop_pass1(q, K, dtype, 1, H, KVH, L, L, block_n, pass1_path, m_tiles, ell_tiles,
-                                                static_cast<uint16_t*>(u_stash), stream);
+                                                static_cast<uint16_t*>(u_stash), nullptr, 0, 0, stream);
   if (e != hipSuccess) return set_error(SANTA_ERR_HIP, "pass-1 launch failed: %s", hipGetErrorString(e));
   return clear_error();
 }
 
 static int prop_budgets_launch(const float* m_tiles, const float* ell_tiles, int BH, int H, int T_c, int S,
                                uint64_t seed, float* m_star, int* S_tiles, float* invdelta, float* a0,
-                               hipStream_t stream) {
+                               hipStream_t stream, const int* seq_lens = nullptr, const int* seq_S = nullptr,
+                               int block_n = 0) {
   const size_t shmem = static_cast<size_t>(T_c) * (2 * sizeof(float) + sizeof(int));
   hipLaunchKernelGGL(prop::budgets_kernel, dim3(BH), dim3(prop::kBudgetThreads), shmem, stream, m_tiles, ell_tiles, H,
-                     T_c, S, seed, m_star, S_tiles, invdelta, a0);
+                     T_c, S, seed, m_star, S_tiles, invdelta, a0, seq_lens, seq_S, block_n);
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess) return set_error(SANTA_ERR_HIP, "budget launch failed: %s", hipGetErrorString(e));
   return SANTA_OK;
@@ -542,7 +580,8 @@ extern "C" int santa_prop_tile_budgets(const float* m_tiles, const float* ell_ti
 static int prop_pass2_launch(const void* V, const uint16_t* u_stash, int dtype, int B, int H, int KVH, int L,
                              int L_storage, int block_n, int T_c, int S, const float* invdelta, const float* a0,
                              int16_t* counts, void* out, int* vrows, const prop::PropWs& w, char* base,
-                             hipStream_t stream) {
+                             hipStream_t stream, const int* seq_lens = nullptr, const int* seq_S = nullptr) {
+  const prop::Pass2Grid rg{seq_lens, w.n_wg};
   float* part = reinterpret_cast<float*>(base + w.part);
   int* pe = reinterpret_cast<int*>(base + w.emit);
   const int GH = H / KVH;
@@ -551,14 +590,14 @@ static int prop_pass2_launch(const void* V, const uint16_t* u_stash, int dtype, 
   const int want_emit = vrows ? 1 : 0;
   if (dtype == SANTA_BF16)
     e = (GH == 4) ? prop::launch_pass2_bn<true, 4>(block_n, Vh, u_stash, B, H, KVH, L, L_storage, T_c, w.cs, w.cpg,
-                                                   invdelta, a0, counts, part, pe, want_emit, stream)
+                                                   invdelta, a0, counts, part, pe, want_emit, rg, stream)
                   : prop::launch_pass2_bn<true, 8>(block_n, Vh, u_stash, B, H, KVH, L, L_storage, T_c, w.cs, w.cpg,
-                                                   invdelta, a0, counts, part, pe, want_emit, stream);
+                                                   invdelta, a0, counts, part, pe, want_emit, rg, stream);
   else
     e = (GH == 4) ? prop::launch_pass2_bn<false, 4>(block_n, Vh, u_stash, B, H, KVH, L, L_storage, T_c, w.cs, w.cpg,
-                                                    invdelta, a0, counts, part, pe, want_emit, stream)
+                                                    invdelta, a0, counts, part, pe, want_emit, rg, stream)
                   : prop::launch_pass2_bn<false, 8>(block_n, Vh, u_stash, B, H, KVH, L, L_storage, T_c, w.cs, w.cpg,
-                                                    invdelta, a0, counts, part, pe, want_emit, stream);
+                                                    invdelta, a0, counts, part, pe, want_emit, rg, stream);
   if (e != hipSuccess) return set_error(SANTA_ERR_HIP, "pass-2 launch failed: %s", hipGetErrorString(e));
   const float scale_out = (S > 0) ? (1.0f / static_cast<float>(S)) : 0.0f;
   const unsigned grid = static_cast<unsigned>(B) * static_cast<unsigned>(H);
@@ -566,17 +605,17 @@ static int prop_pass2_launch(const void* V, const uint16_t* u_stash, int dtype, 
   if (dtype == SANTA_BF16) {
     if (GH == 4)
       hipLaunchKernelGGL((prop::finalize_kernel<true, 4>), dim3(grid), dim3(prop::kD), 0, stream, part, pe, H, KVH,
-                         w.cpg, scale_out, o, vrows);
+                         w.cpg, scale_out, o, vrows, seq_lens, seq_S, block_n, w.cs, L, w.n_wg);
     else
       hipLaunchKernelGGL((prop::finalize_kernel<true, 8>), dim3(grid), dim3(prop::kD), 0, stream, part, pe, H, KVH,
-                         w.cpg, scale_out, o, vrows);
+                         w.cpg, scale_out, o, vrows, seq_lens, seq_S, block_n, w.cs, L, w.n_wg);
   } else {
     if (GH == 4)
       hipLaunchKernelGGL((prop::finalize_kernel<false, 4>), dim3(grid), dim3(prop::kD), 0, stream, part, pe, H, KVH,
-                         w.cpg, scale_out, o, vrows);
+                         w.cpg, scale_out, o, vrows, seq_lens, seq_S, block_n, w.cs, L, w.n_wg);
     else
       hipLaunchKernelGGL((prop::finalize_kernel<false, 8>), dim3(grid), dim3(prop::kD), 0, stream, part, pe, H, KVH,
-                         w.cpg, scale_out, o, vrows);
+                         w.cpg, scale_out, o, vrows, seq_lens, seq_S, block_n, w.cs, L, w.n_wg);
   }
   e = hipGetLastError();
   if (e != hipSuccess) return set_error(SANTA_ERR_HIP, "finalize launch failed: %s", hipGetErrorString(e));
@@ -630,12 +669,59 @@ extern "C" int santa_prop_decode(const void* q, const void* K, const void* V, in
   float* a0 = reinterpret_cast<float*>(base + w.a0);
   uint16_t* stash = reinterpret_cast<uint16_t*>(base + w.stash);
   hipError_t e = flash::launch_prop_pass1(q, K, dtype, 1, H, KVH, L, L, block_n, pass1_path, m_tiles, ell_tiles,
-                                          stash, stream);
+                                          stash, nullptr, 0, 0, stream);
   if (e != hipSuccess) return set_error(SANTA_ERR_HIP, "pass-1 launch failed: %s", hipGetErrorString(e));
   if ((st = prop_budgets_launch(m_tiles, ell_tiles, H, H, T_c, S, seed, m_star, S_tiles, inv, a0, stream)) != SANTA_OK)
     return st;
   if ((st = prop_pass2_launch(V, stash, dtype, 1, H, KVH, L, L, block_n, T_c, S, inv, a0, nullptr, out, vrows, w, base,
                               stream)) != SANTA_OK)
+    return st;
+  return clear_error();
+}
+
+extern "C" size_t santa_prop_batched_workspace_size(int B, int H, int KVH, int D, int L_storage, int max_tiles,
+                                                    long long total_tiles) {
+  (void)D;
+  if (B <= 0 || H <= 0 || KVH <= 0 || H % KVH != 0 || L_storage <= 0 || max_tiles <= 0 || total_tiles < 0) return 0;
+  return prop::prop_ws_layout(B, H, KVH, L_storage, max_tiles, total_tiles).total;
+}
+
+extern "C" int santa_prop_decode_batched(const void* q, const void* K, const void* V, int dtype, int B, int H, int KVH,
+                                         int D, int L_storage, const int* seq_lens, const int* seq_S, int max_len,
+                                         long long total_tiles, int block_n, int pass1_path, uint64_t seed, void* out,
+                                         float* m_star, int* vrows, void* workspace, size_t workspace_bytes,
+                                         hipStream_t stream) {
+  int st = prop::check_common(dtype, H, KVH, D);
+  if (st != SANTA_OK) return st;
+  if (B <= 0) return set_error(SANTA_ERR_INVALID, "empty batch");
+  if (max_len <= 0 || max_len > L_storage)
+    return set_error(SANTA_ERR_INVALID, "max_len must be in [1, L_storage]: max_len=%d L_storage=%d", max_len, L_storage);
+  const int T_c = (max_len + block_n - 1) / block_n;
+  if ((st = prop::check_bn(block_n, T_c)) != SANTA_OK) return st;
+  if (total_tiles < 0 || total_tiles > static_cast<long long>(B) * T_c)
+    return set_error(SANTA_ERR_INVALID, "total_tiles out of range");
+  if (pass1_path == 0 && !(H / KVH == 4 && block_n == 256))
+    return set_error(SANTA_ERR_INVALID, "SANTA_PASS1=vec requires GH=4, D=128, block_n=256. Got GH=%d D=%d block_n=%d",
+                     H / KVH, D, block_n);
+  if (!q || !K || !V || !out || !seq_lens || !seq_S) return set_error(SANTA_ERR_INVALID, "null pointer argument");
+  const prop::PropWs w = prop::prop_ws_layout(B, H, KVH, L_storage, T_c, total_tiles);
+  if (!workspace || workspace_bytes < w.total)
+    return set_error(SANTA_ERR_WORKSPACE, "workspace too small: need %zu bytes, got %zu", w.total, workspace_bytes);
+  char* base = static_cast<char*>(workspace);
+  float* m_tiles = reinterpret_cast<float*>(base + w.m);
+  float* ell_tiles = reinterpret_cast<float*>(base + w.ell);
+  int* S_tiles = reinterpret_cast<int*>(base + w.st);
+  float* inv = reinterpret_cast<float*>(base + w.inv);
+  float* a0 = reinterpret_cast<float*>(base + w.a0);
+  uint16_t* stash = reinterpret_cast<uint16_t*>(base + w.stash);
+  hipError_t e = flash::launch_prop_pass1(q, K, dtype, B, H, KVH, max_len, L_storage, block_n, pass1_path, m_tiles,
+                                          ell_tiles, stash, seq_lens, w.cs, w.n_wg, stream);
+  if (e != hipSuccess) return set_error(SANTA_ERR_HIP, "pass-1 launch failed: %s", hipGetErrorString(e));
+  if ((st = prop_budgets_launch(m_tiles, ell_tiles, B * H, H, T_c, 0, seed, m_star, S_tiles, inv, a0, stream, seq_lens,
+                                seq_S, block_n)) != SANTA_OK)
+    return st;
+  if ((st = prop_pass2_launch(V, stash, dtype, B, H, KVH, max_len, L_storage, block_n, T_c, 0, inv, a0, nullptr, out,
+                              vrows, w, base, stream, seq_lens, seq_S)) != SANTA_OK)
     return st;
   return clear_error();
 }

@@ -4,8 +4,14 @@ reference's `santa_prop_batch_cuda` extension module
 
     decode_systematic_scalar(q_h, K_g, V_g, S, seed=42, block_n=0,
                              want_vrows=False) -> (out, m_star, vrows)
+    decode_systematic_batched(q_h, K_g, V_g, S, seed=42, block_n=0,
+                              want_vrows=False, valid_len=-1) -> (out, m_star, vrows)
 
-Single sequence: q_h [H, D], K_g / V_g [L, KVH, D].  The environment variable
+Single sequence: q_h [H, D], K_g / V_g [L, KVH, D].  Batched (an addition
+over the reference, whose adapter loops over sequences): q_h [B, H, D],
+K_g / V_g [B, L_storage, KVH, D]; S and valid_len are ints or one value per
+sequence, and sequence b is decoded exactly as the scalar call on
+K_g[b, :valid_len[b]] with budget S[b].  The environment variable
 SANTA_PASS1 (auto / gqa / vec) selects the pass-1 numerics on every call, as
 in the reference.
 
@@ -13,4 +19,4 @@ torch is imported first so that the native module binds to torch's HIP runtime.
 """
 import torch  # noqa: F401  (must precede the native module)
 
-from ._C import _debug_pass, _library_version, decode_systematic_scalar  # noqa: F401
+from ._C import _debug_pass, _library_version, decode_systematic_batched, decode_systematic_scalar  # noqa: F401

@@ -1,0 +1,133 @@
+"""GPU parity of the batched, ragged santa_prop entry point.
+
+Sequence b of a batched call must be decoded exactly as the per-sequence
+call on K[b, :valid_len[b]] with budget S[b]: m* bit-exact and vrows exact
+against that call (whose every intermediate is bit-exact to the CPU oracle,
+tests/test_prop_gpu.py) and against the oracle itself on the smaller cases.
+The output sums the same count-weighted rows in another chunking, so it is
+checked to the north-star bf16 tolerance (max abs <= 2e-2, mean rel <= 1e-3)
+against the per-sequence output and against a torch fp32 restatement of the
+estimator given the per-sequence counts.
+
+Every case prints its name, shape and seed before touching the GPU.
+"""
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from helpers import SEED, bits16, gen_qkv, h16_to_f32, tol_check
+from test_prop_gpu import prop_estimator_given_counts
+
+pytestmark = pytest.mark.gpu
+
+
+def _run(H, KVH, lens, Ss, block_n, env, monkeypatch, seed, L_st=None, oracle_check=False, as_tensor=False):
+    import santa_prop_batch_cuda as m
+
+    if env is None:
+        monkeypatch.delenv("SANTA_PASS1", raising=False)
+    else:
+        monkeypatch.setenv("SANTA_PASS1", env)
+    B = len(lens)
+    L_st = L_st or max(lens)
+    print(f"\n[case] prop batched H={H} KVH={KVH} L_storage={L_st} lens={lens} S={Ss} block_n={block_n} "
+          f"env={env} seed={seed}", flush=True)
+    q, K, V = gen_qkv(B, H, KVH, L_st, seed=seed + B, lowrank=0.5)
+    dev = torch.device("cuda:0")
+    qd, Kd, Vd = q.to(dev), K.to(dev), V.to(dev)
+    vl = torch.tensor(lens, dtype=torch.int32) if as_tensor else list(lens)
+    out, ms, vr = m.decode_systematic_batched(qd, Kd, Vd, list(Ss), seed=seed, block_n=block_n, want_vrows=True,
+                                              valid_len=vl)
+    out2, ms2, vr2 = m.decode_systematic_batched(qd, Kd, Vd, list(Ss), seed=seed, block_n=block_n, valid_len=vl)
+    torch.cuda.synchronize()
+    assert out.shape == (B, H, 128) and ms.shape == (B, H) and vr.shape == (B, KVH) and vr2.numel() == 0
+    np.testing.assert_array_equal(bits16(out), bits16(out2), err_msg="repeat call")
+    np.testing.assert_array_equal(ms.cpu().numpy().view(np.uint32), ms2.cpu().numpy().view(np.uint32))
+    for b, (Lb, Sb) in enumerate(zip(lens, Ss)):
+        qb = qd[b].contiguous()
+        Kb, Vb = Kd[b, :Lb].contiguous(), Vd[b, :Lb].contiguous()
+        ref, ms_r, vr_r = m.decode_systematic_scalar(qb, Kb, Vb, Sb, seed=seed, block_n=block_n, want_vrows=True)
+        dbg = m._debug_pass(qb, Kb, Vb, Sb, seed=seed, block_n=block_n)
+        torch.cuda.synchronize()
+        np.testing.assert_array_equal(ms[b].cpu().numpy().view(np.uint32), ms_r.cpu().numpy().view(np.uint32),
+                                      err_msg=f"m_star b={b}")
+        np.testing.assert_array_equal(vr[b].cpu().numpy(), vr_r.cpu().numpy(), err_msg=f"vrows b={b}")
+        got = h16_to_f32(bits16(out[b]))
+        ok, mabs, mrel = tol_check(got, h16_to_f32(bits16(ref)))
+        assert ok, (f"b={b} vs per-sequence", mabs, mrel)
+        est = prop_estimator_given_counts(dbg[7].cpu(), V[b, :Lb], Sb).to(q.dtype).float().numpy()
+        ok, mabs, mrel = tol_check(got, est)
+        assert ok, (f"b={b} vs torch estimator", mabs, mrel)
+        if Sb <= 0:
+            assert not got.any(), f"b={b}: S <= 0 must give a zero output"
+        if oracle_check:
+            exp = oracle.prop_decode(q[b], K[b, :Lb].contiguous(), V[b, :Lb].contiguous(), Sb, seed=seed,
+                                     block_n=block_n, is_bf16=True, debug=True)
+            np.testing.assert_array_equal(ms[b].cpu().numpy().view(np.uint32), exp["m_star"].view(np.uint32))
+            np.testing.assert_array_equal(vr[b].cpu().numpy(), exp["vrows"])
+            ok, mabs, mrel = tol_check(got, h16_to_f32(exp["out16"]))
+            assert ok, (f"b={b} vs oracle", mabs, mrel)
+
+
+@pytest.mark.parametrize(
+    "H,KVH,lens,Ss,block_n,env",
+    [
+        # ragged, one block size (256) for every sequence: the single ragged grid
+        (32, 8, [12000, 3100, 7777, 4096, 11999], [256, 64, 300, 1, 0], 0, None),
+        (32, 8, [12000, 3100, 7777, 4096, 11999], [256, 64, 300, 1, 0], 0, "vec"),
+        (32, 8, [12000, 3100, 7777, 4096, 11999], [256, 64, 300, 1, 0], 0, "gqa"),
+        # forced small tiles, GH=8, lengths down to one token
+        (16, 2, [1, 33, 500, 1000], [7, 40, 256, 1000], 32, None),
+        (16, 2, [64, 65, 130, 2000], [3, 64, 129, 500], 64, None),
+        # block sizes differ between sequences: one launch sequence each
+        (32, 8, [1000, 8000, 2000], [256, 256, 256], 0, None),
+    ],
+)
+def test_prop_batched_parity(H, KVH, lens, Ss, block_n, env, monkeypatch):
+    _run(H, KVH, lens, Ss, block_n, env, monkeypatch, SEED)
+
+
+def test_prop_batched_against_oracle(monkeypatch):
+    _run(32, 8, [4000, 3500, 4096], [256, 100, 17], 256, None, monkeypatch, SEED + 3, L_st=4096,
+         oracle_check=True, as_tensor=True)
+
+
+def test_prop_batched_uniform_int_arguments(monkeypatch):
+    import santa_prop_batch_cuda as m
+
+    monkeypatch.delenv("SANTA_PASS1", raising=False)
+    print("\n[case] prop batched int S / int valid_len B=3 L=5000 valid_len=4500", flush=True)
+    q, K, V = gen_qkv(3, 32, 8, 5000, seed=SEED + 9)
+    dev = torch.device("cuda:0")
+    qd, Kd, Vd = q.to(dev), K.to(dev), V.to(dev)
+    a = m.decode_systematic_batched(qd, Kd, Vd, 256, seed=SEED, valid_len=4500, want_vrows=True)
+    b = m.decode_systematic_batched(qd, Kd, Vd, [256] * 3, seed=SEED, valid_len=[4500] * 3, want_vrows=True)
+    c = m.decode_systematic_batched(qd, Kd[:, :4500].contiguous(), Vd[:, :4500].contiguous(), 256, seed=SEED,
+                                    want_vrows=True)
+    torch.cuda.synchronize()
+    for x, y in ((a, b), (a, c)):
+        np.testing.assert_array_equal(bits16(x[0]), bits16(y[0]))
+        np.testing.assert_array_equal(x[1].cpu().numpy(), y[1].cpu().numpy())
+        np.testing.assert_array_equal(x[2].cpu().numpy(), y[2].cpu().numpy())
+
+
+def test_prop_batched_errors(monkeypatch):
+    import santa_prop_batch_cuda as m
+
+    monkeypatch.delenv("SANTA_PASS1", raising=False)
+    print("\n[case] prop batched argument errors", flush=True)
+    dev = torch.device("cuda:0")
+    q, K, V = gen_qkv(2, 32, 8, 512)
+    qd, Kd, Vd = q.to(dev), K.to(dev), V.to(dev)
+    with pytest.raises(RuntimeError, match="one entry per sequence"):
+        m.decode_systematic_batched(qd, Kd, Vd, [10, 20, 30])
+    with pytest.raises(RuntimeError, match="one entry per sequence"):
+        m.decode_systematic_batched(qd, Kd, Vd, 10, valid_len=[100])
+    with pytest.raises(RuntimeError, match="valid_len exceeds storage length"):
+        m.decode_systematic_batched(qd, Kd, Vd, 10, valid_len=[100, 513])
+    with pytest.raises(RuntimeError, match="Batch mismatch"):
+        m.decode_systematic_batched(qd[:1], Kd, Vd, 10)
+    with pytest.raises(RuntimeError, match=r"\[B, L, KVH, D\]"):
+        nc = Kd.transpose(0, 1).contiguous().transpose(0, 1)
+        m.decode_systematic_batched(qd, nc, nc, 10)
