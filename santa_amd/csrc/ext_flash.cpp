@@ -147,6 +147,29 @@ std::tuple<at::Tensor, at::Tensor, at::Tensor, at::Tensor, at::Tensor> debug_til
   return std::make_tuple(m_tiles, ell_tiles, counts, out_tiles, emit);
 }
 
+// Test-only: the block_n = 256 production tile pass (the wave kernel) with
+// its per-tile statistics written out.  Returns (m_tiles [B,H,T_c],
+// ell_tiles, counts [B,H,T_c,256] i16).
+std::tuple<at::Tensor, at::Tensor, at::Tensor> debug_wave(at::Tensor q_h, at::Tensor K_g, at::Tensor V_g, int64_t S,
+                                                          uint64_t seed, int64_t valid_len) {
+  const Plan p = plan_call(q_h, K_g, V_g, S, 256, valid_len);
+  c10::DeviceGuard guard(q_h.device());
+  const at::Tensor q = aligned_q(q_h);
+  const ShapeInfo& in = p.info;
+  auto optsF = q.options().dtype(at::kFloat);
+  at::Tensor m_tiles = at::empty({in.B, in.H, p.T_c}, optsF);
+  at::Tensor ell_tiles = at::empty({in.B, in.H, p.T_c}, optsF);
+  at::Tensor counts = at::empty({in.B, in.H, p.T_c, 256}, q.options().dtype(at::kShort));
+  const size_t ws_bytes = santa_flash_workspace_size(in.B, in.H, in.KVH, in.D, p.T_c);
+  at::Tensor ws = at::empty({static_cast<int64_t>(ws_bytes)}, q.options().dtype(at::kByte));
+  const hipError_t e = santa::flash::launch_wave_debug(q.data_ptr(), K_g.data_ptr(), V_g.data_ptr(), p.dtype, in.B,
+                                                       in.H, in.KVH, p.L, in.L_storage, p.S_pt, seed, ws.data_ptr(),
+                                                       m_tiles.data_ptr<float>(), ell_tiles.data_ptr<float>(),
+                                                       counts.data_ptr<int16_t>(), current_stream(q));
+  TORCH_CHECK(e == hipSuccess, "wave kernel launch failed: ", hipGetErrorString(e));
+  return std::make_tuple(m_tiles, ell_tiles, counts);
+}
+
 // Test-only: the reference-structured launch pair (per-tile partials, then
 // the finalize with the reference's merge association).  Returns the same
 // tuple as decode_systematic_scalar.
@@ -225,6 +248,8 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
         py::arg("valid_len") = -1);
   m.def("_debug_tiles", &debug_tiles, py::arg("q_h"), py::arg("K_g"), py::arg("V_g"), py::arg("S"),
         py::arg("seed") = 42ULL, py::arg("block_n") = 0, py::arg("valid_len") = -1);
+  m.def("_debug_wave", &debug_wave, py::arg("q_h"), py::arg("K_g"), py::arg("V_g"), py::arg("S"),
+        py::arg("seed") = 42ULL, py::arg("valid_len") = -1);
   m.def("_decode_reference_order", &decode_reference_order, py::arg("q_h"), py::arg("K_g"), py::arg("V_g"),
         py::arg("S"), py::arg("seed") = 42ULL, py::arg("block_n") = 0, py::arg("want_vrows") = false,
         py::arg("valid_len") = -1);

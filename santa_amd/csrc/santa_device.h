@@ -121,6 +121,36 @@ __device__ __forceinline__ float santa_expf(float x) {
   return (x != x) ? x : res;
 }
 
+// santa_expf for x <= 0 that is not NaN (the softmax weights exp(s - m)):
+// the same value with the upper clamp and the NaN select left out.
+__device__ __forceinline__ float santa_expf_nonpos(float x) {
+  const float xc = fmaxf(x, -104.0f);
+  const float n = __builtin_rintf(xc * 1.44269502162933349609375f);
+  float r = fmaf(n, -0.693145751953125f, xc);
+  r = fmaf(n, -1.428606765330187045e-06f, r);
+  float p = 1.984126984126984e-4f;
+  p = fmaf(p, r, 1.3888888888888889e-3f);
+  p = fmaf(p, r, 8.3333333333333333e-3f);
+  p = fmaf(p, r, 4.1666666666666667e-2f);
+  p = fmaf(p, r, 1.6666666666666667e-1f);
+  p = fmaf(p, r, 0.5f);
+  p = fmaf(p, r, 1.0f);
+  p = fmaf(p, r, 1.0f);
+  return __builtin_amdgcn_ldexpf(p, static_cast<int>(n));
+}
+
+// f32 -> 16-bit (RNE) -> f32 for a finite, non-negative value: for bf16 the
+// rounding is done in place on the bit pattern (no NaN case to handle).
+template <bool BF16>
+__device__ __forceinline__ float round16_nonneg(float f) {
+  if constexpr (BF16) {
+    const uint32_t u = __float_as_uint(f);
+    return __uint_as_float((u + 0x7fffu + ((u >> 16) & 1u)) & 0xffff0000u);
+  } else {
+    return h16_to_f32<false>(f32_to_f16_rne(f));
+  }
+}
+
 // float -> int as the reference's (int)(f_curr - f_prev) sees it for the
 // finite, small differences that occur; NaN maps to 0 (then clamped).
 __device__ __forceinline__ int count_from_floors(float a0, float pg, float cum) {

@@ -601,6 +601,372 @@ __global__ __launch_bounds__(kThreads, 2) void tile_kernel(
   }
 }
 
+// ------------------------------------------------------------- wave kernel
+// santa_flash tiles of block_n = 256, online mode, with each wave64 owning
+// whole tiles: wave w of a workgroup takes tiles t_begin + w, t_begin + w + 4,
+// ... of the chunk, so the four waves never wait for one another until the
+// chunk ends.  A tile is scored in four 64-row sub-blocks (hh, e) = (0,0),
+// (0,1), (1,0), (1,1); lane 16j+q of sub-block (hh, e) owns row
+// 128hh + 32j + 2q + e.  That is the two-rows-per-lane layout of
+// systematic_counts (register pair hh, element e), so scores, u, the 16-bit
+// u, x and the counts never leave registers; only the sub-block staging of K
+// (the row-per-lane transpose for the MFMA operand) and the sampled-row
+// lists use LDS.  Each sub-block load takes 4 rows of stride 2 (16 lanes x
+// 16 B per row, still 256 contiguous bytes per row); the loads of the next
+// sub-block are issued before the current one is scored.
+//
+// Statistics are bit-identical to tile_kernel's (the reference's): the tile
+// max is exact in any order, and ell keeps the reference thread / 32-lane
+// tree / warp association (flash/santa_cuda_kernel.cu:243-273), rebuilt from
+// this layout with cross-row swaps and DPP.  The output merge differs only
+// in rounding: a sampled row's coefficient c * ell_t * exp(m_t - M) is formed
+// when the row is listed, relative to the wave's running max M, and listed
+// coefficients are rescaled in place when M grows.  The four waves' partials
+// are merged in wave order at the end of the chunk.
+constexpr int kWaveListCap = 64;  // listed rows per head (one per lane)
+
+template <int N>
+__device__ __forceinline__ float xrow16(float v) {  // rows 0<->1, 2<->3
+  const auto s = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(s[1]);
+}
+__device__ __forceinline__ float xhalf32(float v) {  // lanes i <-> i + 32
+  const auto s = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(s[1]);
+}
+
+// ell of one head from its u values (u[hh][e] at this lane; 0 past len),
+// with the reference's association for block_n = 256 (256 reference
+// threads; thread tau = GH * rho + g sums rows rho + (256 / GH) k in order k,
+// then per 32-thread warp a shfl_down tree of distances 16, 8, ... GH, then
+// the warps in order).
+template <int GH>
+__device__ __forceinline__ float wave_ell(const float (&u)[2][2]) {
+  float A[2];
+  if constexpr (GH == 4) {
+    // rows rho' + 64 k: k = 0..3 -> (hh 0, row block j), (hh 0, j + 2),
+    // (hh 1, j), (hh 1, j + 2); valid in lanes 0..31
+#pragma unroll
+    for (int e = 0; e < 2; ++e) {
+      float a = u[0][e] + xhalf32(u[0][e]);
+      a = a + u[1][e];
+      A[e] = a + xhalf32(u[1][e]);
+    }
+    // warp w = lanes 4w .. 4w+3: ((A0 + A4) + (A2 + A6)) + ((A1 + A5) + (A3 + A7)),
+    // A_m = A[m % 2] at lane 4w + m / 2
+#pragma unroll
+    for (int e = 0; e < 2; ++e) {
+      A[e] = A[e] + dpp_shl_zero<2>(A[e]);
+      A[e] = A[e] + dpp_shl_zero<1>(A[e]);
+    }
+    const float W = A[0] + A[1];
+    float ell = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(W), 0));
+#pragma unroll
+    for (int w = 1; w < 8; ++w) ell = ell + __int_as_float(__builtin_amdgcn_readlane(__float_as_int(W), 4 * w));
+    return ell;
+  } else {
+    // rows rho'' + 32 k: k = 0..7 -> (hh 0, j = 0..3), (hh 1, j = 0..3); lanes 0..15
+#pragma unroll
+    for (int e = 0; e < 2; ++e) {
+      float a = 0.0f;
+#pragma unroll
+      for (int hh = 0; hh < 2; ++hh) {
+        const float v = u[hh][e];
+        const float v16 = xrow16<0>(v);
+        a = (hh == 0) ? v : a + v;
+        a = a + v16;
+        a = a + xhalf32(v);
+        a = a + xhalf32(v16);
+      }
+      A[e] = a;
+    }
+    // warp w = lanes 2w, 2w+1: (A0 + A2) + (A1 + A3), A_m = A[m % 2] at lane 2w + m / 2
+#pragma unroll
+    for (int e = 0; e < 2; ++e) A[e] = A[e] + dpp_shl_zero<1>(A[e]);
+    const float W = A[0] + A[1];
+    float ell = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(W), 0));
+#pragma unroll
+    for (int w = 1; w < 8; ++w) ell = ell + __int_as_float(__builtin_amdgcn_readlane(__float_as_int(W), 2 * w));
+    return ell;
+  }
+}
+
+template <bool BF16, int GH, bool DBG>
+__global__ __launch_bounds__(kThreads, 2) void wave_kernel(
+    const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K, const uint16_t* __restrict__ V, int H, int KVH,
+    int L_valid, int L_storage, int T_c, int cs, int cpg, float q_scale, int S_pt, uint64_t seed,
+    float* __restrict__ part, int* __restrict__ part_emit, float* __restrict__ dbg_m, float* __restrict__ dbg_ell,
+    int16_t* __restrict__ dbg_counts) {
+  constexpr int BN = 256;
+  constexpr int NHB = GH / 4;
+  constexpr int LCAP = kWaveListCap;
+  const int wg = static_cast<int>(blockIdx.x);
+  const GridPos gp = grid_pos(wg, nullptr, 1, KVH, BN, L_valid, T_c, cs, cpg);
+  const int kv = gp.kv;
+  const int b = gp.b;
+  const int h0 = kv * GH;
+  const int t_begin = gp.chunk * cs;
+  const int t_end = min(T_c, t_begin + cs);
+  const int tid = static_cast<int>(threadIdx.x);
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+
+  __shared__ u32x4 s_k[4 * 64 * 16];  // per wave: 64 rows x 256 B staging; the chunk merge reuses it
+  __shared__ int s_lrow[4 * GH * LCAP];
+  __shared__ float s_lcw[4 * GH * LCAP];
+  u32x4* const wk = s_k + wave * 64 * 16;
+  int* const lrow = s_lrow + wave * GH * LCAP;
+  float* const lcw = s_lcw + wave * GH * LCAP;
+
+  const size_t row_stride = static_cast<size_t>(KVH) * kD;
+  const uint32_t row_bytes = static_cast<uint32_t>(KVH) * kD * 2u;
+  const char* Kg = reinterpret_cast<const char*>(K + static_cast<size_t>(b) * L_storage * row_stride +
+                                                 static_cast<size_t>(kv) * kD);
+  const char* Vg = reinterpret_cast<const char*>(V + static_cast<size_t>(b) * L_storage * row_stride +
+                                                 static_cast<size_t>(kv) * kD);
+  const uint32_t v_lane_off = 4u * static_cast<uint32_t>(lane);
+
+  float qa[NHB][8];
+#pragma unroll
+  for (int hb = 0; hb < NHB; ++hb) {
+    const uint16_t* qh = Q + (static_cast<size_t>(b) * H + h0 + 4 * hb + (lane & 3)) * kD + (lane >> 2);
+#pragma unroll
+    for (int m = 0; m < 8; ++m) qa[hb][m] = h16_to_f32<BF16>(qh[16 * m]) * q_scale;
+  }
+
+  float runM[GH], runZ[GH], num0[GH], num1[GH];
+  int lcnt[GH];
+#pragma unroll
+  for (int g = 0; g < GH; ++g) {
+    runM[g] = -__builtin_inff();
+    runZ[g] = 0.0f;
+    num0[g] = 0.0f;
+    num1[g] = 0.0f;
+    lcnt[g] = 0;
+  }
+  int emit_total = 0;
+
+  // the listed rows of head g, in list order, into the numerator
+  auto flush = [&](int g) {
+    const int n = lcnt[g];
+    if (n == 0) return;
+    const int rowv = (lane < n) ? lrow[g * LCAP + lane] : 0;
+    const float coefv = (lane < n) ? lcw[g * LCAP + lane] : 0.0f;
+    for (int q0 = 0; q0 < n; q0 += 16) {
+      float coef[16];
+      uint32_t vw[16];
+#pragma unroll
+      for (int q = 0; q < 16; ++q) {
+        const int j = min(q0 + q, n - 1);
+        const int row = __builtin_amdgcn_readlane(rowv, j);
+        coef[q] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(coefv), j));
+        vw[q] = *reinterpret_cast<const uint32_t*>(Vg + static_cast<size_t>(row) * row_bytes + v_lane_off);
+      }
+#pragma unroll
+      for (int q = 0; q < 16; ++q) {
+        if (q0 + q < n) {
+          num0[g] = fmaf(coef[q], lo16_to_f32<BF16>(vw[q]), num0[g]);
+          num1[g] = fmaf(coef[q], hi16_to_f32<BF16>(vw[q]), num1[g]);
+        }
+      }
+    }
+    lcnt[g] = 0;
+  };
+
+  // Sub-block sb = 2 hh + e of tile t: 16 loads of 4 rows (stride 2), one
+  // descriptor each; rows at or past the tile's end (and every row of a tile
+  // at or past t_end) read as zero and cost no traffic.
+  u32x4 kw[16];
+  const int k_lane_off = static_cast<int>((lane >> 4) * 2u * row_bytes + 16u * (lane & 15));
+  auto load_k = [&](int t, int sb) {
+    const int len = (t < t_end) ? min(BN, L_valid - t * BN) : 0;
+    const int r0 = 128 * (sb >> 1) + (sb & 1);
+    const char* kt = Kg + static_cast<size_t>(t * BN + r0) * row_bytes;
+#pragma unroll
+    for (int c = 0; c < 16; ++c) {
+      const int nvalid = __builtin_amdgcn_readfirstlane(min(max(len - r0 - 8 * c, 0), 8));
+      const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+          const_cast<char*>(kt + static_cast<size_t>(8 * c) * row_bytes), static_cast<short>(0),
+          nvalid * static_cast<int>(row_bytes), kBufferWord3);
+      kw[c] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rs, k_lane_off, 0, kBufferNontemporal));
+    }
+  };
+  load_k(t_begin + wave, 0);
+
+  const int jrow = lane >> 4;
+  const int qq = lane & 15;
+  const uint64_t below = (1ull << lane) - 1ull;
+  for (int t = t_begin + wave; t < t_end; t += 4) {
+    const int n0 = t * BN;
+    const int len = min(BN, L_valid - n0);
+
+    // ---- scores of the four sub-blocks -------------------------------------
+    f32x4 sc[2][2][NHB];
+#pragma unroll
+    for (int sb = 0; sb < 4; ++sb) {
+#pragma unroll
+      for (int c = 0; c < 16; ++c) {
+        const int r = 4 * c + (lane >> 4);
+        wk[r * 16 + ((lane & 15) ^ (r & 15))] = kw[c];
+      }
+      load_k(sb == 3 ? t + 4 : t, (sb + 1) & 3);
+      __builtin_amdgcn_wave_barrier();
+      const int row = lane;
+      f32x4 be0[NHB], bo0[NHB], be2[NHB], bo2[NHB], be1[NHB], bo1[NHB], be3[NHB], bo3[NHB];
+      score_group<BF16, NHB, 0>(wk, row, qa, be0, bo0);
+      score_group<BF16, NHB, 2>(wk, row, qa, be2, bo2);
+      score_group<BF16, NHB, 1>(wk, row, qa, be1, bo1);
+      score_group<BF16, NHB, 3>(wk, row, qa, be3, bo3);
+#pragma unroll
+      for (int hb = 0; hb < NHB; ++hb) {
+        const f32x4 de = (be0[hb] + be2[hb]) + (be1[hb] + be3[hb]);
+        const f32x4 dd = (bo0[hb] + bo2[hb]) + (bo1[hb] + bo3[hb]);
+        sc[sb >> 1][sb & 1][hb] = de + dd;
+      }
+    }
+
+    // ---- tile max per head (exact in any order) --------------------------------
+    bool valid[2][2];
+#pragma unroll
+    for (int hh = 0; hh < 2; ++hh)
+#pragma unroll
+      for (int e = 0; e < 2; ++e) valid[hh][e] = 128 * hh + 32 * jrow + 2 * qq + e < len;
+    float mg[GH];
+#pragma unroll
+    for (int g = 0; g < GH; ++g) {
+      int k = -2147483647 - 1;
+#pragma unroll
+      for (int hh = 0; hh < 2; ++hh)
+#pragma unroll
+        for (int e = 0; e < 2; ++e)
+          if (valid[hh][e]) k = max(k, order_key(sc[hh][e][g >> 2][g & 3]));
+      k = wave_max_key_lane63(k);
+      mg[g] = from_order_key(__builtin_amdgcn_readlane(k, 63));
+    }
+
+    // ---- per head: u, ell, counts, sampled rows ----------------------------------
+    uint64_t uni[2][2] = {{0, 0}, {0, 0}};
+#pragma unroll
+    for (int g = 0; g < GH; ++g) {
+      const int h = h0 + g;
+      float u[2][2], ub[2][2];
+#pragma unroll
+      for (int hh = 0; hh < 2; ++hh)
+#pragma unroll
+        for (int e = 0; e < 2; ++e) {
+          // s - m <= 0 for the rows that take part (inputs are finite)
+          u[hh][e] = valid[hh][e] ? santa_expf_nonpos(sc[hh][e][g >> 2][g & 3] - mg[g]) : 0.0f;
+          ub[hh][e] = round16_nonneg<BF16>(u[hh][e]);
+        }
+      const float ell = wave_ell<GH>(u);
+      const float invdel = (S_pt > 0 && ell > 1e-20f) ? (static_cast<float>(S_pt) / ell) : 0.0f;
+      const float a0 = u01(seed, b * H + h, t);
+      float x0[2], x1[2];
+#pragma unroll
+      for (int hh = 0; hh < 2; ++hh) {
+        x0[hh] = (valid[hh][0] && invdel > 0.0f) ? ub[hh][0] * invdel : 0.0f;
+        x1[hh] = (valid[hh][1] && invdel > 0.0f) ? ub[hh][1] * invdel : 0.0f;
+      }
+      int cnt[2][2];
+      systematic_counts<8>(x0, x1, len, a0, lane, cnt[0], cnt[1]);
+      // cnt[0] / cnt[1] are the e = 0 / e = 1 rows of register pairs hh = 0, 1
+      if constexpr (DBG) {
+        const size_t mt = (static_cast<size_t>(b) * H + h) * T_c + t;
+        if (lane == 0) {
+          dbg_m[mt] = mg[g];
+          dbg_ell[mt] = ell;
+        }
+#pragma unroll
+        for (int hh = 0; hh < 2; ++hh) {
+          int16_t* dc = dbg_counts + mt * BN + 128 * hh + 32 * jrow + 2 * qq;
+          dc[0] = static_cast<int16_t>(cnt[0][hh]);
+          dc[1] = static_cast<int16_t>(cnt[1][hh]);
+        }
+      }
+
+      // running max and mass; listed coefficients follow the running max
+      float f;
+      if (mg[g] > runM[g]) {
+        const float r = santa_expf(runM[g] - mg[g]);
+        runZ[g] = fmaf(runZ[g], r, ell);
+        num0[g] *= r;
+        num1[g] *= r;
+        if (lane < lcnt[g]) lcw[g * LCAP + lane] *= r;
+        runM[g] = mg[g];
+        f = ell;
+      } else {
+        const float w = santa_expf(mg[g] - runM[g]);
+        runZ[g] = fmaf(w, ell, runZ[g]);
+        f = ell * w;
+      }
+#pragma unroll
+      for (int hh = 0; hh < 2; ++hh)
+#pragma unroll
+        for (int e = 0; e < 2; ++e) {
+          const int c = cnt[e][hh];
+          const uint64_t nz = __ballot(c != 0);
+          uni[hh][e] |= nz;
+          const int nn = __popcll(nz);
+          if (nn) {
+            if (lcnt[g] + nn > LCAP) flush(g);
+            const int pos = lcnt[g] + __popcll(nz & below);
+            if (c != 0) {
+              lrow[g * LCAP + pos] = n0 + 128 * hh + 32 * jrow + 2 * qq + e;
+              lcw[g * LCAP + pos] = static_cast<float>(c) * f;
+            }
+            lcnt[g] += nn;
+          }
+        }
+    }
+    emit_total += __popcll(uni[0][0]) + __popcll(uni[0][1]) + __popcll(uni[1][0]) + __popcll(uni[1][1]);
+  }
+#pragma unroll
+  for (int g = 0; g < GH; ++g) flush(g);
+
+  // ---- the four waves' partials, merged in wave order -----------------------------
+  __syncthreads();  // every wave is done with its staging area
+  float* sp = reinterpret_cast<float*>(s_k);  // [wave][g][kPartStride], then the wave emit counts
+  int* s_emit = reinterpret_cast<int*>(sp + 4 * GH * kPartStride);
+#pragma unroll
+  for (int g = 0; g < GH; ++g) {
+    float* p = sp + (wave * GH + g) * kPartStride;
+    if (lane == 0) {
+      p[0] = runM[g];
+      p[1] = runZ[g];
+    }
+    p[2 + 2 * lane] = num0[g];
+    p[3 + 2 * lane] = num1[g];
+  }
+  if (lane == 0) s_emit[wave] = emit_total;
+  __syncthreads();
+#pragma unroll
+  for (int k = 0; k < NHB; ++k) {
+    const int g = wave + 4 * k;
+    float M = -__builtin_inff();
+#pragma unroll
+    for (int w = 0; w < 4; ++w) M = fmaxf(M, sp[(w * GH + g) * kPartStride]);
+    float Z = 0.0f, n0v = 0.0f, n1v = 0.0f;
+    if (M != -__builtin_inff()) {
+#pragma unroll
+      for (int w = 0; w < 4; ++w) {
+        const float* p = sp + (w * GH + g) * kPartStride;
+        const float r = santa_expf(p[0] - M);
+        Z = fmaf(p[1], r, Z);
+        n0v = fmaf(p[2 + 2 * lane], r, n0v);
+        n1v = fmaf(p[3 + 2 * lane], r, n1v);
+      }
+    }
+    float* pp = part + (static_cast<size_t>(wg) * GH + g) * kPartStride;
+    if (lane == 0) {
+      pp[0] = M;
+      pp[1] = Z;
+    }
+    pp[2 + 2 * lane] = n0v;
+    pp[3 + 2 * lane] = n1v;
+  }
+  if (tid == 0) part_emit[wg] = (s_emit[0] + s_emit[1]) + (s_emit[2] + s_emit[3]);
+}
+
 // Split-KV merge of per-tile partials (flash/santa_cuda_kernel.cu:386-470):
 // one workgroup per (b, h); max and Z trees with the reference's pairing
 // (strides 128 .. 1), numerator accumulated over tiles in ascending order
@@ -751,6 +1117,36 @@ static hipError_t launch_bn(int bn, const Args& a, hipStream_t stream) {
     default:
       return launch_t<BF16, GH, 256, MODE>(a, stream);
   }
+}
+
+template <bool BF16, int GH>
+static hipError_t launch_wave_t(const Args& a, float* dbg_m, float* dbg_ell, int16_t* dbg_counts,
+                                hipStream_t stream) {
+  const float q_scale = 1.0f / sqrtf(static_cast<float>(kD));
+  const unsigned grid = static_cast<unsigned>(a.B) * static_cast<unsigned>(a.KVH) * static_cast<unsigned>(a.cpg);
+  if (grid == 0) return hipSuccess;
+  if (dbg_counts)
+    hipLaunchKernelGGL((wave_kernel<BF16, GH, true>), dim3(grid), dim3(kThreads), 0, stream,
+                       static_cast<const uint16_t*>(a.q), static_cast<const uint16_t*>(a.K),
+                       static_cast<const uint16_t*>(a.V), a.H, a.KVH, a.L_valid, a.L_storage, a.T_c, a.cs, a.cpg,
+                       q_scale, a.S_pt, a.seed, a.part, a.part_emit, dbg_m, dbg_ell, dbg_counts);
+  else
+    hipLaunchKernelGGL((wave_kernel<BF16, GH, false>), dim3(grid), dim3(kThreads), 0, stream,
+                       static_cast<const uint16_t*>(a.q), static_cast<const uint16_t*>(a.K),
+                       static_cast<const uint16_t*>(a.V), a.H, a.KVH, a.L_valid, a.L_storage, a.T_c, a.cs, a.cpg,
+                       q_scale, a.S_pt, a.seed, a.part, a.part_emit, nullptr, nullptr, nullptr);
+  return hipGetLastError();
+}
+
+// The online tile pass of block_n = 256 on the wave kernel (debug outputs
+// may be null).
+static hipError_t launch_wave(int dtype, int GH, const Args& a, float* dbg_m, float* dbg_ell, int16_t* dbg_counts,
+                              hipStream_t stream) {
+  if (dtype == SANTA_BF16)
+    return (GH == 4) ? launch_wave_t<true, 4>(a, dbg_m, dbg_ell, dbg_counts, stream)
+                     : launch_wave_t<true, 8>(a, dbg_m, dbg_ell, dbg_counts, stream);
+  return (GH == 4) ? launch_wave_t<false, 4>(a, dbg_m, dbg_ell, dbg_counts, stream)
+                   : launch_wave_t<false, 8>(a, dbg_m, dbg_ell, dbg_counts, stream);
 }
 
 template <int MODE>
@@ -952,6 +1348,22 @@ FlashWs flash_ws_layout(int B, int H, int KVH, int T_c) {
 }
 }  // namespace
 
+namespace santa {
+namespace flash {
+// Declared in santa_internal.h.
+hipError_t launch_wave_debug(const void* q, const void* K, const void* V, int dtype, int B, int H, int KVH,
+                             int L_valid, int L_storage, int S_pt, uint64_t seed, void* workspace, float* m_tiles,
+                             float* ell_tiles, int16_t* counts, hipStream_t stream) {
+  const int T_c = (L_valid + 255) / 256;
+  const FlashWs w = flash_ws_layout(B, H, KVH, T_c);
+  char* base = static_cast<char*>(workspace);
+  Args a{q, K, V, B, H, KVH, L_valid, L_storage, T_c, S_pt, seed, nullptr, nullptr, nullptr, nullptr, nullptr,
+         reinterpret_cast<float*>(base + w.part), reinterpret_cast<int*>(base + w.emit), w.cs, w.cpg, nullptr};
+  return launch_wave(dtype, H / KVH, a, m_tiles, ell_tiles, counts, stream);
+}
+}  // namespace flash
+}  // namespace santa
+
 extern "C" size_t santa_flash_workspace_size(int B, int H, int KVH, int D, int T_c) {
   (void)D;
   if (B <= 0 || H <= 0 || KVH <= 0 || T_c <= 0 || H % KVH != 0) return 0;
@@ -978,7 +1390,9 @@ extern "C" int santa_flash_decode_tiles(const void* q, const void* K, const void
   flash::Args a{q, K, V, B, H, KVH, L_valid, L_storage, T_c, S_per_tile, seed, nullptr, nullptr, nullptr, nullptr,
                 nullptr, reinterpret_cast<float*>(base + w.part), reinterpret_cast<int*>(base + w.emit), w.cs, w.cpg,
                 nullptr};
-  const hipError_t e = flash::launch_tiles<flash::kOnline>(dtype, H / KVH, block_n, a, stream);
+  const hipError_t e = (block_n == 256 && H / KVH == 4)
+                           ? flash::launch_wave(dtype, H / KVH, a, nullptr, nullptr, nullptr, stream)
+                           : flash::launch_tiles<flash::kOnline>(dtype, H / KVH, block_n, a, stream);
   if (e != hipSuccess) return set_error(SANTA_ERR_HIP, "tile launch failed: %s", hipGetErrorString(e));
   return clear_error();
 }

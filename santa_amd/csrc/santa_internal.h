@@ -29,6 +29,12 @@ hipError_t launch_prop_pass1(const void* q, const void* K, int dtype, int B, int
 // Chunking of a ragged batch with total_tiles tiles: cs tiles per chunk and
 // an upper bound n_wg on the workgroups of the ragged grid.
 void plan_ragged(int B, int KVH, long long total_tiles, int* cs, int* n_wg);
+// The block_n = 256 online tile pass (the wave kernel) with its per-tile
+// statistics m, ell [B, H, T_c] and counts [B, H, T_c, 256] written out
+// (test hook; the chunk partials go to the santa_flash_decode workspace).
+hipError_t launch_wave_debug(const void* q, const void* K, const void* V, int dtype, int B, int H, int KVH,
+                             int L_valid, int L_storage, int S_pt, uint64_t seed, void* workspace, float* m_tiles,
+                             float* ell_tiles, int16_t* counts, hipStream_t stream);
 // y[i] = santa_expf(x[i]) on the device (test hook for the exponential).
 hipError_t launch_expf(const float* x, float* y, size_t n, hipStream_t stream);
 // Chunks of cs tiles per workgroup, cpg chunks per (b, kv) group, sized to

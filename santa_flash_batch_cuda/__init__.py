@@ -12,6 +12,7 @@ import torch  # noqa: F401  (must precede the native module)
 
 from ._C import (  # noqa: F401
     _debug_tiles,
+    _debug_wave,
     _decode_reference_order,
     _decode_tiles_only,
     _device_expf,

@@ -157,3 +157,47 @@ def test_device_expf_matches_oracle():
     assert np.array_equal(np.isnan(y_gpu), nan)
     bad = np.nonzero(y_gpu[~nan].view(np.uint32) != y_ref[~nan].view(np.uint32))[0]
     assert bad.size == 0, (x[~nan][bad[:5]], y_gpu[~nan][bad[:5]], y_ref[~nan][bad[:5]])
+
+
+@pytest.mark.parametrize(
+    "B,H,KVH,L,S,valid_len,dtype",
+    [
+        (1, 32, 8, 4096, 32, -1, torch.bfloat16),      # cfg1
+        (2, 32, 8, 5000, 256, -1, torch.bfloat16),     # ragged last tile
+        (3, 32, 8, 4096, 100, 3001, torch.bfloat16),   # valid_len < storage
+        (1, 32, 8, 700, 7, -1, torch.bfloat16),        # one ragged tile
+        (1, 32, 8, 1, 5, -1, torch.bfloat16),          # one token
+        (1, 32, 8, 257, 9, -1, torch.bfloat16),        # one row in the second tile
+        (2, 64, 8, 3000, 512, -1, torch.bfloat16),     # GH=8
+        (1, 32, 8, 2048, 100000, -1, torch.bfloat16),  # lists overflow inside a tile
+        (2, 32, 8, 32768, 256, -1, torch.bfloat16),    # several tiles per wave, cfg2 rows
+        (2, 32, 8, 6000, 300, -1, torch.float16),
+    ],
+)
+def test_wave_kernel_statistics(B, H, KVH, L, S, valid_len, dtype):
+    """The block_n=256 production kernel: tile max, tile mass and every count
+    bit-exact to the oracle, read back through its debug outputs."""
+    _announce(f"wave kernel B={B} H={H} KVH={KVH} L={L} S={S} valid_len={valid_len} {dtype}")
+    m = _mod()
+    q, K, V = gen_qkv(B, H, KVH, L, seed=SEED + 7 * B + L, dtype=dtype, lowrank=0.5)
+    dev = torch.device("cuda:0")
+    qd, Kd, Vd = q.to(dev), K.to(dev), V.to(dev)
+    mt, lt, cnt = m._debug_wave(qd, Kd, Vd, S, seed=SEED, valid_len=valid_len)
+    out, ms, vr = m.decode_systematic_batched(qd, Kd, Vd, S, seed=SEED, block_n=256, want_vrows=True,
+                                              valid_len=valid_len)
+    torch.cuda.synchronize()
+    is_bf16 = dtype == torch.bfloat16
+    exp = oracle.flash_decode(q, K, V, S, seed=SEED, block_n=256, valid_len=valid_len, is_bf16=is_bf16, debug=True)
+    np.testing.assert_array_equal(mt.cpu().numpy().view(np.uint32), exp["m_tiles"].view(np.uint32), err_msg="m_tiles")
+    np.testing.assert_array_equal(lt.cpu().numpy().view(np.uint32), exp["ell_tiles"].view(np.uint32),
+                                  err_msg="ell_tiles")
+    c_gpu = cnt.cpu().numpy()
+    assert np.array_equal(c_gpu, exp["counts"]), f"counts differ at {np.argwhere(c_gpu != exp['counts'])[:8]}"
+    np.testing.assert_array_equal(ms.cpu().numpy().view(np.uint32), exp["m_star"].view(np.uint32), err_msg="m_star")
+    np.testing.assert_array_equal(vr.cpu().numpy(), exp["vrows"], err_msg="vrows")
+    got = h16_to_f32(bits16(out), is_bf16)
+    ok, mabs, mrel = tol_check(got, h16_to_f32(exp["out16"], is_bf16))
+    assert ok, ("vs oracle", mabs, mrel)
+    ref = estimator_given_counts(mt, lt, cnt, Vd, S, valid_len if valid_len > 0 else L)
+    ok, mabs, mrel = tol_check(got, ref.to(dtype).float().numpy())
+    assert ok, ("vs torch estimator", mabs, mrel)
