@@ -123,6 +123,50 @@ __device__ __forceinline__ void score_group(const u32x4* wk, int row, const floa
   }
 }
 
+// Materializes v here: an empty asm that reads and writes it, so the
+// compiler cannot sink the arithmetic that produces v to its later uses
+// (which would keep every partial of a tile's scores live at once).
+__device__ __forceinline__ void pin(f32x4& v) { asm volatile("" : "+v"(v)); }
+
+// score_chunk / score_group for one head block (q registers qv[8]).
+template <bool BF16, int C>
+__device__ __forceinline__ void score_chunk1(const u32x4* wk, int row, const float (&qv)[8], f32x4& pe, f32x4& po) {
+  const u32x4 kc = wk[row * 16 + (C ^ (row & 15))];
+  const float k0 = lo16_to_f32<BF16>(kc.x), k1 = hi16_to_f32<BF16>(kc.x);
+  const float k2 = lo16_to_f32<BF16>(kc.y), k3 = hi16_to_f32<BF16>(kc.y);
+  const float k4 = lo16_to_f32<BF16>(kc.z), k5 = hi16_to_f32<BF16>(kc.z);
+  const float k6 = lo16_to_f32<BF16>(kc.w), k7 = hi16_to_f32<BF16>(kc.w);
+  constexpr int M = C / 2;
+  constexpr int J = 8 * (C % 2);
+  const f32x4 z = {0.0f, 0.0f, 0.0f, 0.0f};
+  const float q = qv[M];
+  f32x4 de = mfma_bcast<J + 0>(q, k0, z);
+  f32x4 dd = mfma_bcast<J + 4>(q, k4, z);
+  de = mfma_bcast<J + 1>(q, k1, de);
+  dd = mfma_bcast<J + 5>(q, k5, dd);
+  de = mfma_bcast<J + 2>(q, k2, de);
+  dd = mfma_bcast<J + 6>(q, k6, dd);
+  de = mfma_bcast<J + 3>(q, k3, de);
+  dd = mfma_bcast<J + 7>(q, k7, dd);
+  pe = de;
+  po = dd;
+}
+template <bool BF16, int C>
+__device__ __forceinline__ void score_group1(const u32x4* wk, int row, const float (&qv)[8], f32x4& be, f32x4& bo) {
+  // a scheduling fence after each chunk pair keeps only two chunks'
+  // accumulators live
+  f32x4 e0, o0, e8, o8, e4, o4, e12, o12;
+  score_chunk1<BF16, C>(wk, row, qv, e0, o0);
+  score_chunk1<BF16, C + 8>(wk, row, qv, e8, o8);
+  const f32x4 ae = e0 + e8, ao = o0 + o8;
+  __builtin_amdgcn_sched_barrier(0);
+  score_chunk1<BF16, C + 4>(wk, row, qv, e4, o4);
+  score_chunk1<BF16, C + 12>(wk, row, qv, e12, o12);
+  be = ae + (e4 + e12);
+  bo = ao + (o4 + o12);
+  __builtin_amdgcn_sched_barrier(0);
+}
+
 // Number of rows of a tile sampled by any head of the group: the union of
 // the per-head nonzero-count masks (one 64-row block per lane < NBLK).
 template <int GH, int NBLK>
@@ -809,19 +853,34 @@ __global__ __launch_bounds__(kThreads, 2) void wave_kernel(
         const int r = 4 * c + (lane >> 4);
         wk[r * 16 + ((lane & 15) ^ (r & 15))] = kw[c];
       }
-      load_k(sb == 3 ? t + 4 : t, (sb + 1) & 3);
+      // GH = 8: the next tile's first sub-block is loaded after the tail (whose
+      // registers would not fit beside it; the 8-head tail is VALU-bound)
+      if (GH == 4 || sb < 3) load_k(sb == 3 ? t + 4 : t, (sb + 1) & 3);
       __builtin_amdgcn_wave_barrier();
       const int row = lane;
-      f32x4 be0[NHB], bo0[NHB], be2[NHB], bo2[NHB], be1[NHB], bo1[NHB], be3[NHB], bo3[NHB];
-      score_group<BF16, NHB, 0>(wk, row, qa, be0, bo0);
-      score_group<BF16, NHB, 2>(wk, row, qa, be2, bo2);
-      score_group<BF16, NHB, 1>(wk, row, qa, be1, bo1);
-      score_group<BF16, NHB, 3>(wk, row, qa, be3, bo3);
+      if constexpr (NHB == 1) {
+        f32x4 be0[NHB], bo0[NHB], be2[NHB], bo2[NHB], be1[NHB], bo1[NHB], be3[NHB], bo3[NHB];
+        score_group<BF16, NHB, 0>(wk, row, qa, be0, bo0);
+        score_group<BF16, NHB, 2>(wk, row, qa, be2, bo2);
+        score_group<BF16, NHB, 1>(wk, row, qa, be1, bo1);
+        score_group<BF16, NHB, 3>(wk, row, qa, be3, bo3);
+        const f32x4 de = (be0[0] + be2[0]) + (be1[0] + be3[0]);
+        const f32x4 dd = (bo0[0] + bo2[0]) + (bo1[0] + bo3[0]);
+        sc[sb >> 1][sb & 1][0] = de + dd;
+        pin(sc[sb >> 1][sb & 1][0]);
+      } else {
+        // one head block at a time: the staged rows are read once per block
+        // rather than holding every block's accumulators
 #pragma unroll
-      for (int hb = 0; hb < NHB; ++hb) {
-        const f32x4 de = (be0[hb] + be2[hb]) + (be1[hb] + be3[hb]);
-        const f32x4 dd = (bo0[hb] + bo2[hb]) + (bo1[hb] + bo3[hb]);
-        sc[sb >> 1][sb & 1][hb] = de + dd;
+        for (int hb = 0; hb < NHB; ++hb) {
+          f32x4 be0, bo0, be2, bo2, be1, bo1, be3, bo3;
+          score_group1<BF16, 0>(wk, row, qa[hb], be0, bo0);
+          score_group1<BF16, 2>(wk, row, qa[hb], be2, bo2);
+          score_group1<BF16, 1>(wk, row, qa[hb], be1, bo1);
+          score_group1<BF16, 3>(wk, row, qa[hb], be3, bo3);
+          sc[sb >> 1][sb & 1][hb] = ((be0 + be2) + (be1 + be3)) + ((bo0 + bo2) + (bo1 + bo3));
+          pin(sc[sb >> 1][sb & 1][hb]);
+        }
       }
     }
 
@@ -919,6 +978,7 @@ __global__ __launch_bounds__(kThreads, 2) void wave_kernel(
         }
     }
     emit_total += __popcll(uni[0][0]) + __popcll(uni[0][1]) + __popcll(uni[1][0]) + __popcll(uni[1][1]);
+    if constexpr (GH == 8) load_k(t + 4, 0);
   }
 #pragma unroll
   for (int g = 0; g < GH; ++g) flush(g);
@@ -1390,9 +1450,8 @@ extern "C" int santa_flash_decode_tiles(const void* q, const void* K, const void
   flash::Args a{q, K, V, B, H, KVH, L_valid, L_storage, T_c, S_per_tile, seed, nullptr, nullptr, nullptr, nullptr,
                 nullptr, reinterpret_cast<float*>(base + w.part), reinterpret_cast<int*>(base + w.emit), w.cs, w.cpg,
                 nullptr};
-  const hipError_t e = (block_n == 256 && H / KVH == 4)
-                           ? flash::launch_wave(dtype, H / KVH, a, nullptr, nullptr, nullptr, stream)
-                           : flash::launch_tiles<flash::kOnline>(dtype, H / KVH, block_n, a, stream);
+  const hipError_t e = (block_n == 256) ? flash::launch_wave(dtype, H / KVH, a, nullptr, nullptr, nullptr, stream)
+                                         : flash::launch_tiles<flash::kOnline>(dtype, H / KVH, block_n, a, stream);
   if (e != hipSuccess) return set_error(SANTA_ERR_HIP, "tile launch failed: %s", hipGetErrorString(e));
   return clear_error();
 }
