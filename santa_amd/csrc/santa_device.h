@@ -153,11 +153,11 @@ __device__ __forceinline__ float round16_nonneg(float f) {
 
 // float -> int as the reference's (int)(f_curr - f_prev) sees it for the
 // finite, small differences that occur; NaN maps to 0 (then clamped).
+// Clamping the float difference to [0, 32767] before the conversion is the
+// same as clamping the integer (and fmaxf maps NaN to 0).
 __device__ __forceinline__ int count_from_floors(float a0, float pg, float cum) {
   const float d = floorf(a0 + cum) - floorf(a0 + pg);
-  int c = (d != d) ? 0 : static_cast<int>(fminf(fmaxf(d, -2147483648.0f), 2147483520.0f));
-  c = c < 0 ? 0 : c;
-  return c > 32767 ? 32767 : c;
+  return static_cast<int>(fminf(fmaxf(d, 0.0f), 32767.0f));
 }
 
 // ---------------------------------------------------------------- grids

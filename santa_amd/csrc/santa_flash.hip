@@ -828,6 +828,7 @@ __global__ __launch_bounds__(kThreads, 2) void wave_kernel(
     const char* kt = Kg + static_cast<size_t>(t * BN + r0) * row_bytes;
 #pragma unroll
     for (int c = 0; c < 16; ++c) {
+      // wave-uniform; readfirstlane keeps the descriptor in SGPRs
       const int nvalid = __builtin_amdgcn_readfirstlane(min(max(len - r0 - 8 * c, 0), 8));
       const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
           const_cast<char*>(kt + static_cast<size_t>(8 * c) * row_bytes), static_cast<short>(0),
@@ -920,11 +921,13 @@ __global__ __launch_bounds__(kThreads, 2) void wave_kernel(
       const float ell = wave_ell<GH>(u);
       const float invdel = (S_pt > 0 && ell > 1e-20f) ? (static_cast<float>(S_pt) / ell) : 0.0f;
       const float a0 = u01(seed, b * H + h, t);
+      // u (so the 16-bit u) is 0 past len and invdel is finite and >= 0, so
+      // x = ub * invdel is the reference's 0 there without a select
       float x0[2], x1[2];
 #pragma unroll
       for (int hh = 0; hh < 2; ++hh) {
-        x0[hh] = (valid[hh][0] && invdel > 0.0f) ? ub[hh][0] * invdel : 0.0f;
-        x1[hh] = (valid[hh][1] && invdel > 0.0f) ? ub[hh][1] * invdel : 0.0f;
+        x0[hh] = ub[hh][0] * invdel;
+        x1[hh] = ub[hh][1] * invdel;
       }
       int cnt[2][2];
       systematic_counts<8>(x0, x1, len, a0, lane, cnt[0], cnt[1]);
