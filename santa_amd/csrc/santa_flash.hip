@@ -1120,14 +1120,40 @@ __global__ __launch_bounds__(kD) void merge_kernel(const float* __restrict__ par
   // chunk c of (b, kv) was workgroup (b * cpg + c) * KVH + kv
   const float* pb = part + ((static_cast<size_t>(b) * cpg * KVH + kv) * GH + g) * kPartStride;
   const size_t cstride = static_cast<size_t>(KVH) * GH * kPartStride;
+  // The partials are read in batches of up to 16 chunks with every load of
+  // a batch issued before the first use (one memory round trip per batch,
+  // usually the only one); max and sums keep the ascending chunk order.
+  constexpr int kBatch = 16;
   float ms = -__builtin_inff();
-  for (int c = 0; c < cpg; ++c) ms = fmaxf(ms, pb[c * cstride]);
   float Z = 0.0f, num = 0.0f;
-  for (int c = 0; c < cpg; ++c) {
-    const float* pc = pb + c * cstride;
-    const float w = santa_expf(pc[0] - ms);
-    Z = fmaf(w, pc[1], Z);
-    num = fmaf(w, pc[2 + d], num);
+  if (cpg <= kBatch) {
+    float mc[kBatch], zc[kBatch], nc[kBatch];
+#pragma unroll
+    for (int c = 0; c < kBatch; ++c) {
+      const float* pc = pb + static_cast<size_t>(c < cpg ? c : 0) * cstride;
+      mc[c] = pc[0];
+      zc[c] = pc[1];
+      nc[c] = pc[2 + d];
+    }
+#pragma unroll
+    for (int c = 0; c < kBatch; ++c)
+      if (c < cpg) ms = fmaxf(ms, mc[c]);
+#pragma unroll
+    for (int c = 0; c < kBatch; ++c) {
+      if (c < cpg) {
+        const float w = santa_expf(mc[c] - ms);
+        Z = fmaf(w, zc[c], Z);
+        num = fmaf(w, nc[c], num);
+      }
+    }
+  } else {
+    for (int c = 0; c < cpg; ++c) ms = fmaxf(ms, pb[c * cstride]);
+    for (int c = 0; c < cpg; ++c) {
+      const float* pc = pb + c * cstride;
+      const float w = santa_expf(pc[0] - ms);
+      Z = fmaf(w, pc[1], Z);
+      num = fmaf(w, pc[2 + d], num);
+    }
   }
   const float inv_norm = (S_pt > 0 && Z > 0.0f) ? (1.0f / (Z * static_cast<float>(S_pt))) : 0.0f;
   out[static_cast<size_t>(bh) * kD + d] = f32_to_h16<BF16>(num * inv_norm);
