@@ -45,7 +45,7 @@ def parse_args():
     return ap.parse_args()
 
 
-PMC_SUMMARY = os.path.join(REPO, "profiles", "flash_tile_kernel_cfg2_pmc.md")
+PMC_SUMMARY = os.path.join(REPO, "profiles", "flash_wave_kernel_cfg2_pmc.md")
 
 
 def measured_traffic():
