@@ -112,6 +112,22 @@ int santa_flash_decode_tiles(const void* q, const void* K, const void* V, int dt
 int santa_flash_decode_merge(const void* workspace, size_t workspace_bytes, int dtype, int B, int H, int KVH, int D,
                              int T_c, int S_per_tile, void* out, float* m_star, int* vrows, hipStream_t stream);
 
+/* Ragged flash (no counterpart in the reference, whose batched call takes
+ * one valid_len for every sequence, flash/santa_cuda.cpp:188): sequence b of
+ * a [B, L_storage, KVH, D] cache is decoded on its first seq_lens[b] tokens
+ * with S_per_tile = S > 0 ? max(1, S / ceil(seq_lens[b] / block_n)) : 0 and
+ * RNG key b*H + h -- exactly what the uniform call does when every length
+ * equals seq_lens[b].  seq_lens: device int array [B]; max_len = max
+ * seq_lens (<= L_storage) and total_tiles = sum over b of
+ * ceil(seq_lens[b] / block_n), from the host; one block_n (32, 64 or 256)
+ * for every sequence.  out [B,H,D], m_star [B,H], vrows [B,KVH] (may be
+ * NULL).  Lengths are clamped on the device to [1, max_len]. */
+size_t santa_flash_ragged_workspace_size(int B, int H, int KVH, int D, long long total_tiles);
+int santa_flash_decode_ragged(const void* q, const void* K, const void* V, int dtype, int B, int H, int KVH, int D,
+                              int L_storage, const int* seq_lens, int max_len, long long total_tiles, int block_n,
+                              int64_t S, uint64_t seed, void* out, float* m_star, int* vrows, void* workspace,
+                              size_t workspace_bytes, hipStream_t stream);
+
 /* -------------------------------------------------------------- prop */
 
 /* Host planning.  block_n <= 0 selects 256 when pass1_env is "vec"/"gqa_vec",

@@ -8,7 +8,9 @@
 #include <c10/hip/HIPStream.h>
 
 #include <cstdint>
+#include <algorithm>
 #include <tuple>
+#include <vector>
 
 #include "santa_amd.h"
 #include "santa_internal.h"
@@ -100,10 +102,37 @@ hipStream_t current_stream(const at::Tensor& t) {
   return c10::hip::getCurrentHIPStream(t.device().index()).stream();
 }
 
+std::tuple<at::Tensor, at::Tensor, at::Tensor> decode_ragged(at::Tensor q_h, at::Tensor K_g, at::Tensor V_g,
+                                                             int64_t S, uint64_t seed, int64_t block_n,
+                                                             bool want_vrows, std::vector<int64_t> lens);
+
+// valid_len: an int (the reference's form), or -- an addition over the
+// reference -- one length per sequence (list or 1-D tensor) for the batched
+// form.
 std::tuple<at::Tensor, at::Tensor, at::Tensor> decode_systematic_scalar(at::Tensor q_h, at::Tensor K_g,
                                                                         at::Tensor V_g, int64_t S, uint64_t seed,
                                                                         int64_t block_n, bool want_vrows,
-                                                                        int64_t valid_len) {
+                                                                        py::object valid_len_obj) {
+  int64_t valid_len = -1;
+  if (py::isinstance<py::int_>(valid_len_obj)) {
+    valid_len = valid_len_obj.cast<int64_t>();
+  } else {
+    std::vector<int64_t> lens;
+    if (THPVariable_Check(valid_len_obj.ptr())) {
+      const at::Tensor t = valid_len_obj.cast<at::Tensor>().to(at::kCPU).to(at::kLong).contiguous();
+      TORCH_CHECK(t.dim() == 1, "valid_len must be an int or a 1-D list of per-sequence lengths");
+      lens.assign(t.data_ptr<int64_t>(), t.data_ptr<int64_t>() + t.numel());
+    } else {
+      lens = valid_len_obj.cast<std::vector<int64_t>>();
+    }
+    TORCH_CHECK(q_h.dim() == 3, "per-sequence valid_len needs the batched form q_h [B,H,D]");
+    TORCH_CHECK(static_cast<int64_t>(lens.size()) == q_h.size(0),
+                "valid_len must be an int or have one entry per sequence (", q_h.size(0), ")");
+    bool uniform = true;
+    for (size_t i = 1; i < lens.size(); ++i) uniform = uniform && lens[i] == lens[0];
+    if (!uniform) return decode_ragged(q_h, K_g, V_g, S, seed, block_n, want_vrows, lens);
+    valid_len = lens.empty() ? -1 : lens[0];
+  }
   const Plan p = plan_call(q_h, K_g, V_g, S, block_n, valid_len);
   c10::DeviceGuard guard(q_h.device());
   const at::Tensor q = aligned_q(q_h);
@@ -120,6 +149,46 @@ std::tuple<at::Tensor, at::Tensor, at::Tensor> decode_systematic_scalar(at::Tens
                                     p.L, in.L_storage, p.bn, p.S_pt, seed, out.data_ptr(),
                                     m_star.data_ptr<float>(), want_vrows ? vrows.data_ptr<int>() : nullptr,
                                     ws.data_ptr(), ws_bytes, current_stream(q));
+  TORCH_CHECK(rc == SANTA_OK, santa_last_error());
+  return std::make_tuple(out, m_star, vrows);
+}
+
+// Ragged batch: block_n planned from the longest sequence (or given), one
+// launch pair over all sequences (santa_flash_decode_ragged).
+std::tuple<at::Tensor, at::Tensor, at::Tensor> decode_ragged(at::Tensor q_h, at::Tensor K_g, at::Tensor V_g,
+                                                             int64_t S, uint64_t seed, int64_t block_n,
+                                                             bool want_vrows, std::vector<int64_t> lens) {
+  const ShapeInfo in = check_inputs_q_kv(q_h, K_g, V_g);
+  int64_t max_len = 0;
+  for (int64_t& l : lens) {
+    if (l <= 0) l = in.L_storage;
+    TORCH_CHECK(l <= in.L_storage, "valid_len exceeds storage length: valid_len=", l, " storage=", in.L_storage);
+    max_len = std::max(max_len, l);
+  }
+  // checks and block_n as for a uniform call at the longest length
+  const Plan p = plan_call(q_h, K_g, V_g, S, block_n, max_len);
+  c10::DeviceGuard guard(q_h.device());
+  const at::Tensor q = aligned_q(q_h);
+  long long total = 0;
+  std::vector<int32_t> host(lens.size());
+  for (size_t b = 0; b < lens.size(); ++b) {
+    host[b] = static_cast<int32_t>(lens[b]);
+    total += (lens[b] + p.bn - 1) / p.bn;
+  }
+  at::Tensor dlens = at::from_blob(host.data(), {static_cast<int64_t>(host.size())},
+                                   at::TensorOptions().dtype(at::kInt)).to(q.device());
+  auto optsF = q.options().dtype(at::kFloat);
+  auto optsI = q.options().dtype(at::kInt);
+  at::Tensor out = at::empty({in.B, in.H, in.D}, q.options());
+  at::Tensor m_star = at::empty({in.B, in.H}, optsF);
+  at::Tensor vrows = want_vrows ? at::empty({in.B, in.KVH}, optsI) : at::empty({0}, optsI);
+  const size_t ws_bytes = santa_flash_ragged_workspace_size(in.B, in.H, in.KVH, in.D, total);
+  at::Tensor ws = at::empty({static_cast<int64_t>(ws_bytes)}, q.options().dtype(at::kByte));
+  const int rc = santa_flash_decode_ragged(q.data_ptr(), K_g.data_ptr(), V_g.data_ptr(), p.dtype, in.B, in.H, in.KVH,
+                                           in.D, in.L_storage, dlens.data_ptr<int>(), static_cast<int>(max_len), total,
+                                           p.bn, S, seed, out.data_ptr(), m_star.data_ptr<float>(),
+                                           want_vrows ? vrows.data_ptr<int>() : nullptr, ws.data_ptr(), ws_bytes,
+                                           current_stream(q));
   TORCH_CHECK(rc == SANTA_OK, santa_last_error());
   return std::make_tuple(out, m_star, vrows);
 }
@@ -242,10 +311,10 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
   m.doc() = "S^2ANTA-Flash sampled-attention decode for MI355X (gfx950)";
   m.def("decode_systematic_scalar", &decode_systematic_scalar, py::arg("q_h"), py::arg("K_g"), py::arg("V_g"),
         py::arg("S"), py::arg("seed") = 42ULL, py::arg("block_n") = 0, py::arg("want_vrows") = false,
-        py::arg("valid_len") = -1);
+        py::arg("valid_len") = py::int_(-1));
   m.def("decode_systematic_batched", &decode_systematic_scalar, py::arg("q_h"), py::arg("K_g"), py::arg("V_g"),
         py::arg("S"), py::arg("seed") = 42ULL, py::arg("block_n") = 0, py::arg("want_vrows") = false,
-        py::arg("valid_len") = -1);
+        py::arg("valid_len") = py::int_(-1));
   m.def("_debug_tiles", &debug_tiles, py::arg("q_h"), py::arg("K_g"), py::arg("V_g"), py::arg("S"),
         py::arg("seed") = 42ULL, py::arg("block_n") = 0, py::arg("valid_len") = -1);
   m.def("_debug_wave", &debug_wave, py::arg("q_h"), py::arg("K_g"), py::arg("V_g"), py::arg("S"),

@@ -195,7 +195,8 @@ __global__ __launch_bounds__(kThreads, 2) void tile_kernel(
     int L_valid, int L_storage, int T_c, int cs, int cpg, float q_scale, int S_pt, uint64_t seed,
     float* __restrict__ m_tiles, float* __restrict__ ell_tiles, float* __restrict__ out_tiles,
     int* __restrict__ emit_cnt, int16_t* __restrict__ dbg_counts, float* __restrict__ part,
-    int* __restrict__ part_emit, uint16_t* __restrict__ u_stash, const int* __restrict__ seq_lens, int B) {
+    int* __restrict__ part_emit, uint16_t* __restrict__ u_stash, const int* __restrict__ seq_lens, int B,
+    long long S_total) {
   static_assert(BN == 32 || BN == 64 || BN == 256, "block_n");
   static_assert(GH == 4 || GH == 8, "group size");
   constexpr int NT_REF = (BN == 256) ? 256 : 128;  // reference block size (launchers :521,:559)
@@ -223,6 +224,9 @@ __global__ __launch_bounds__(kThreads, 2) void tile_kernel(
   L_valid = gp.len;  // this sequence's valid length from here on
   const int t_begin = chunk * cs;
   const int t_end = (gp.b < 0) ? t_begin : min(gp.n_tiles, t_begin + cs);
+  // ragged flash: S_per_tile from this sequence's tile count (flash/santa_cuda.cpp:204-208)
+  if (seq_lens && MODE == kOnline)
+    S_pt = (S_total > 0) ? static_cast<int>(max(1LL, S_total / static_cast<long long>(max(gp.n_tiles, 1)))) : 0;
 
   const int tid = static_cast<int>(threadIdx.x);
   const int lane = tid & 63;
@@ -739,18 +743,24 @@ template <bool BF16, int GH, bool DBG>
 __global__ __launch_bounds__(kThreads, 2) void wave_kernel(
     const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K, const uint16_t* __restrict__ V, int H, int KVH,
     int L_valid, int L_storage, int T_c, int cs, int cpg, float q_scale, int S_pt, uint64_t seed,
-    float* __restrict__ part, int* __restrict__ part_emit, float* __restrict__ dbg_m, float* __restrict__ dbg_ell,
-    int16_t* __restrict__ dbg_counts) {
+    float* __restrict__ part, int* __restrict__ part_emit, const int* __restrict__ seq_lens, int B, long long S_total,
+    float* __restrict__ dbg_m, float* __restrict__ dbg_ell, int16_t* __restrict__ dbg_counts) {
   constexpr int BN = 256;
   constexpr int NHB = GH / 4;
   constexpr int LCAP = kWaveListCap;
   const int wg = static_cast<int>(blockIdx.x);
-  const GridPos gp = grid_pos(wg, nullptr, 1, KVH, BN, L_valid, T_c, cs, cpg);
+  // uniform grid, or the ragged one (seq_lens: per-sequence lengths, L_valid
+  // the longest; workgroups past the last sequence only write an empty
+  // partial)
+  const GridPos gp = grid_pos(wg, seq_lens, B, KVH, BN, L_valid, T_c, cs, cpg);
   const int kv = gp.kv;
-  const int b = gp.b;
+  const int b = gp.b < 0 ? 0 : gp.b;
   const int h0 = kv * GH;
+  L_valid = gp.len;
   const int t_begin = gp.chunk * cs;
-  const int t_end = min(T_c, t_begin + cs);
+  const int t_end = (gp.b < 0) ? t_begin : min(gp.n_tiles, t_begin + cs);
+  if (seq_lens)  // S_per_tile from this sequence's tile count (flash/santa_cuda.cpp:204-208)
+    S_pt = (S_total > 0) ? static_cast<int>(max(1LL, S_total / static_cast<long long>(max(gp.n_tiles, 1)))) : 0;
   const int tid = static_cast<int>(threadIdx.x);
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -1109,7 +1119,9 @@ __global__ __launch_bounds__(kThreads) void finalize_kernel(const float* __restr
 template <bool BF16, int GH>
 __global__ __launch_bounds__(kD) void merge_kernel(const float* __restrict__ part, const int* __restrict__ part_emit,
                                                    int H, int KVH, int cpg, int S_pt, uint16_t* __restrict__ out,
-                                                   float* __restrict__ m_star, int* __restrict__ vrows) {
+                                                   float* __restrict__ m_star, int* __restrict__ vrows,
+                                                   const int* __restrict__ seq_lens, int BN, int cs, int max_len,
+                                                   int n_wg, long long S_total) {
   const int bh = static_cast<int>(blockIdx.x);
   const int b = bh / H;
   const int h = bh % H;
@@ -1117,8 +1129,17 @@ __global__ __launch_bounds__(kD) void merge_kernel(const float* __restrict__ par
   const int g = h % GH;
   const int bk = b * KVH + kv;
   const int d = static_cast<int>(threadIdx.x);
-  // chunk c of (b, kv) was workgroup (b * cpg + c) * KVH + kv
-  const float* pb = part + ((static_cast<size_t>(b) * cpg * KVH + kv) * GH + g) * kPartStride;
+  // chunk c of (b, kv) was workgroup base_b + c * KVH + kv
+  int base = b * cpg * KVH;
+  if (seq_lens) {
+    base = 0;
+    for (int bb = 0; bb < b; ++bb) base += KVH * (((ragged_len(seq_lens, bb, max_len) + BN - 1) / BN + cs - 1) / cs);
+    const int tiles = (ragged_len(seq_lens, b, max_len) + BN - 1) / BN;
+    cpg = (tiles + cs - 1) / cs;
+    cpg = max(0, min(cpg, (n_wg - base - kv + KVH - 1) / KVH));  // only launched workgroups wrote partials
+    S_pt = (S_total > 0) ? static_cast<int>(max(1LL, S_total / static_cast<long long>(tiles))) : 0;
+  }
+  const float* pb = part + ((static_cast<size_t>(base) + kv) * GH + g) * kPartStride;
   const size_t cstride = static_cast<size_t>(KVH) * GH * kPartStride;
   // The partials are read in batches of up to 16 chunks with every load of
   // a batch issued before the first use (one memory round trip per batch,
@@ -1160,7 +1181,7 @@ __global__ __launch_bounds__(kD) void merge_kernel(const float* __restrict__ par
   if (d == 0 && m_star) m_star[bh] = ms;
   if (vrows && g == 0 && d == 0) {
     int e = 0;
-    for (int c = 0; c < cpg; ++c) e += part_emit[(static_cast<size_t>(b) * cpg + c) * KVH + kv];
+    for (int c = 0; c < cpg; ++c) e += part_emit[static_cast<size_t>(base) + c * KVH + kv];
     vrows[bk] = e;
   }
 }
@@ -1178,8 +1199,9 @@ struct Args {
   int* part_emit;
   int cs, cpg;
   uint16_t* u_stash;
-  const int* seq_lens;  // ragged form (prop pass 1) or nullptr
+  const int* seq_lens;  // ragged form (prop pass 1, ragged flash) or nullptr
   int n_wg;             // grid size of the ragged form
+  long long S_total;    // ragged flash: S, for each sequence's S_per_tile
 };
 
 template <bool BF16, int GH, int BN, int MODE>
@@ -1192,7 +1214,7 @@ static hipError_t launch_t(const Args& a, hipStream_t stream) {
                      static_cast<const uint16_t*>(a.q), static_cast<const uint16_t*>(a.K),
                      static_cast<const uint16_t*>(a.V), a.H, a.KVH, a.L_valid, a.L_storage, a.T_c, a.cs, a.cpg,
                      q_scale, a.S_pt, a.seed, a.m_tiles, a.ell_tiles, a.out_tiles, a.emit_cnt, a.counts, a.part,
-                     a.part_emit, a.u_stash, a.seq_lens, a.B);
+                     a.part_emit, a.u_stash, a.seq_lens, a.B, a.S_total);
   return hipGetLastError();
 }
 
@@ -1212,18 +1234,21 @@ template <bool BF16, int GH>
 static hipError_t launch_wave_t(const Args& a, float* dbg_m, float* dbg_ell, int16_t* dbg_counts,
                                 hipStream_t stream) {
   const float q_scale = 1.0f / sqrtf(static_cast<float>(kD));
-  const unsigned grid = static_cast<unsigned>(a.B) * static_cast<unsigned>(a.KVH) * static_cast<unsigned>(a.cpg);
+  const unsigned grid = a.seq_lens ? static_cast<unsigned>(a.n_wg)
+                                   : static_cast<unsigned>(a.B) * static_cast<unsigned>(a.KVH) * static_cast<unsigned>(a.cpg);
   if (grid == 0) return hipSuccess;
   if (dbg_counts)
     hipLaunchKernelGGL((wave_kernel<BF16, GH, true>), dim3(grid), dim3(kThreads), 0, stream,
                        static_cast<const uint16_t*>(a.q), static_cast<const uint16_t*>(a.K),
                        static_cast<const uint16_t*>(a.V), a.H, a.KVH, a.L_valid, a.L_storage, a.T_c, a.cs, a.cpg,
-                       q_scale, a.S_pt, a.seed, a.part, a.part_emit, dbg_m, dbg_ell, dbg_counts);
+                       q_scale, a.S_pt, a.seed, a.part, a.part_emit, a.seq_lens, a.B, a.S_total, dbg_m, dbg_ell,
+                       dbg_counts);
   else
     hipLaunchKernelGGL((wave_kernel<BF16, GH, false>), dim3(grid), dim3(kThreads), 0, stream,
                        static_cast<const uint16_t*>(a.q), static_cast<const uint16_t*>(a.K),
                        static_cast<const uint16_t*>(a.V), a.H, a.KVH, a.L_valid, a.L_storage, a.T_c, a.cs, a.cpg,
-                       q_scale, a.S_pt, a.seed, a.part, a.part_emit, nullptr, nullptr, nullptr);
+                       q_scale, a.S_pt, a.seed, a.part, a.part_emit, a.seq_lens, a.B, a.S_total, nullptr,
+                       nullptr, nullptr);
   return hipGetLastError();
 }
 
@@ -1236,6 +1261,32 @@ static hipError_t launch_wave(int dtype, int GH, const Args& a, float* dbg_m, fl
                      : launch_wave_t<true, 8>(a, dbg_m, dbg_ell, dbg_counts, stream);
   return (GH == 4) ? launch_wave_t<false, 4>(a, dbg_m, dbg_ell, dbg_counts, stream)
                    : launch_wave_t<false, 8>(a, dbg_m, dbg_ell, dbg_counts, stream);
+}
+
+// The chunk-partial merge, one workgroup per (b, h); seq_lens selects the
+// ragged chunk layout (then bn, cs, max_len, n_wg and S_total describe it).
+static hipError_t launch_merge(const float* part, const int* pe, int dtype, int B, int H, int KVH, int cpg, int S_pt,
+                               void* out, float* m_star, int* vrows, const int* seq_lens, int bn, int cs,
+                               int max_len, int n_wg, long long S_total, hipStream_t stream) {
+  const int GH = H / KVH;
+  const unsigned grid = static_cast<unsigned>(B) * static_cast<unsigned>(H);
+  uint16_t* o = static_cast<uint16_t*>(out);
+  if (dtype == SANTA_BF16) {
+    if (GH == 4)
+      hipLaunchKernelGGL((merge_kernel<true, 4>), dim3(grid), dim3(kD), 0, stream, part, pe, H, KVH, cpg, S_pt, o,
+                         m_star, vrows, seq_lens, bn, cs, max_len, n_wg, S_total);
+    else
+      hipLaunchKernelGGL((merge_kernel<true, 8>), dim3(grid), dim3(kD), 0, stream, part, pe, H, KVH, cpg, S_pt, o,
+                         m_star, vrows, seq_lens, bn, cs, max_len, n_wg, S_total);
+  } else {
+    if (GH == 4)
+      hipLaunchKernelGGL((merge_kernel<false, 4>), dim3(grid), dim3(kD), 0, stream, part, pe, H, KVH, cpg, S_pt, o,
+                         m_star, vrows, seq_lens, bn, cs, max_len, n_wg, S_total);
+    else
+      hipLaunchKernelGGL((merge_kernel<false, 8>), dim3(grid), dim3(kD), 0, stream, part, pe, H, KVH, cpg, S_pt, o,
+                         m_star, vrows, seq_lens, bn, cs, max_len, n_wg, S_total);
+  }
+  return hipGetLastError();
 }
 
 template <int MODE>
@@ -1498,25 +1549,8 @@ extern "C" int santa_flash_decode_merge(const void* workspace, size_t workspace_
   const char* base = static_cast<const char*>(workspace);
   const float* part = reinterpret_cast<const float*>(base + w.part);
   const int* pe = reinterpret_cast<const int*>(base + w.emit);
-  const int GH = H / KVH;
-  const unsigned grid = static_cast<unsigned>(B) * static_cast<unsigned>(H);
-  uint16_t* o = static_cast<uint16_t*>(out);
-  if (dtype == SANTA_BF16) {
-    if (GH == 4)
-      hipLaunchKernelGGL((flash::merge_kernel<true, 4>), dim3(grid), dim3(flash::kD), 0, stream, part, pe, H, KVH,
-                         w.cpg, S_per_tile, o, m_star, vrows);
-    else
-      hipLaunchKernelGGL((flash::merge_kernel<true, 8>), dim3(grid), dim3(flash::kD), 0, stream, part, pe, H, KVH,
-                         w.cpg, S_per_tile, o, m_star, vrows);
-  } else {
-    if (GH == 4)
-      hipLaunchKernelGGL((flash::merge_kernel<false, 4>), dim3(grid), dim3(flash::kD), 0, stream, part, pe, H, KVH,
-                         w.cpg, S_per_tile, o, m_star, vrows);
-    else
-      hipLaunchKernelGGL((flash::merge_kernel<false, 8>), dim3(grid), dim3(flash::kD), 0, stream, part, pe, H, KVH,
-                         w.cpg, S_per_tile, o, m_star, vrows);
-  }
-  const hipError_t e = hipGetLastError();
+  const hipError_t e = flash::launch_merge(part, pe, dtype, B, H, KVH, w.cpg, S_per_tile, out, m_star, vrows, nullptr,
+                                           0, 0, 0, 0, 0, stream);
   if (e != hipSuccess) return set_error(SANTA_ERR_HIP, "merge launch failed: %s", hipGetErrorString(e));
   return clear_error();
 }
@@ -1530,4 +1564,57 @@ extern "C" int santa_flash_decode(const void* q, const void* K, const void* V, i
   if (st != SANTA_OK) return st;
   return santa_flash_decode_merge(workspace, workspace_bytes, dtype, B, H, KVH, D, (L_valid + block_n - 1) / block_n,
                                   S_per_tile, out, m_star, vrows, stream);
+}
+
+// ------------------------------------------------------------ ragged flash
+namespace {
+struct RaggedWs {
+  size_t part, emit, total;
+  int cs, n_wg;
+};
+RaggedWs ragged_ws_layout(int B, int H, int KVH, long long total_tiles) {
+  RaggedWs w{};
+  flash::plan_ragged(B, KVH, total_tiles, &w.cs, &w.n_wg);
+  const size_t chunks = static_cast<size_t>(w.n_wg);
+  size_t off = 0;
+  w.part = off;
+  off = santa::align_up(off + chunks * (H / KVH) * flash::kPartStride * sizeof(float));
+  w.emit = off;
+  off = santa::align_up(off + chunks * sizeof(int));
+  w.total = off;
+  return w;
+}
+}  // namespace
+
+extern "C" size_t santa_flash_ragged_workspace_size(int B, int H, int KVH, int D, long long total_tiles) {
+  (void)D;
+  if (B <= 0 || H <= 0 || KVH <= 0 || H % KVH != 0 || total_tiles < 0) return 0;
+  return ragged_ws_layout(B, H, KVH, total_tiles).total;
+}
+
+extern "C" int santa_flash_decode_ragged(const void* q, const void* K, const void* V, int dtype, int B, int H, int KVH,
+                                         int D, int L_storage, const int* seq_lens, int max_len, long long total_tiles,
+                                         int block_n, int64_t S, uint64_t seed, void* out, float* m_star, int* vrows,
+                                         void* workspace, size_t workspace_bytes, hipStream_t stream) {
+  int st = check_flash_shape(dtype, B, H, KVH, D, max_len, L_storage, block_n);
+  if (st != SANTA_OK) return st;
+  if (!q || !K || !V || !out || !seq_lens) return set_error(SANTA_ERR_INVALID, "null pointer argument");
+  const int T_c = (max_len + block_n - 1) / block_n;
+  if (total_tiles < 0 || total_tiles > static_cast<long long>(B) * T_c)
+    return set_error(SANTA_ERR_INVALID, "total_tiles out of range");
+  const RaggedWs w = ragged_ws_layout(B, H, KVH, total_tiles);
+  if (!workspace || workspace_bytes < w.total)
+    return set_error(SANTA_ERR_WORKSPACE, "workspace too small: need %zu bytes, got %zu", w.total, workspace_bytes);
+  char* base = static_cast<char*>(workspace);
+  float* part = reinterpret_cast<float*>(base + w.part);
+  int* pe = reinterpret_cast<int*>(base + w.emit);
+  flash::Args a{q, K, V, B, H, KVH, max_len, L_storage, T_c, 0, seed, nullptr, nullptr, nullptr, nullptr, nullptr,
+                part, pe, w.cs, 0, nullptr, seq_lens, w.n_wg, static_cast<long long>(S)};
+  hipError_t e = (block_n == 256) ? flash::launch_wave(dtype, H / KVH, a, nullptr, nullptr, nullptr, stream)
+                                  : flash::launch_tiles<flash::kOnline>(dtype, H / KVH, block_n, a, stream);
+  if (e != hipSuccess) return set_error(SANTA_ERR_HIP, "tile launch failed: %s", hipGetErrorString(e));
+  e = flash::launch_merge(part, pe, dtype, B, H, KVH, 0, 0, out, m_star, vrows, seq_lens, block_n, w.cs, max_len,
+                          w.n_wg, static_cast<long long>(S), stream);
+  if (e != hipSuccess) return set_error(SANTA_ERR_HIP, "merge launch failed: %s", hipGetErrorString(e));
+  return clear_error();
 }

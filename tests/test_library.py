@@ -159,10 +159,12 @@ def test_extension_surfaces():
     import santa_flash_batch_cuda as flash
     import santa_prop_batch_cuda as prop
 
+    # valid_len keeps the reference's int form and default; it is typed
+    # `object` because the batched form also takes one length per sequence
     for fn in (flash.decode_systematic_scalar, flash.decode_systematic_batched):
         doc = fn.__doc__.splitlines()[0]
         assert re.search(r"\(q_h: .*, K_g: .*, V_g: .*, S: [\w.]*Int, seed: [\w.]*Int = 42, block_n: [\w.]*Int = 0, "
-                         r"want_vrows: bool = False, valid_len: [\w.]*Int = -1\)", doc), doc
+                         r"want_vrows: bool = False, valid_len: (?:[\w.]*Int|object) = -1\)", doc), doc
     doc = prop.decode_systematic_scalar.__doc__.splitlines()[0]
     assert re.search(r"\(q_h: .*, K_g: .*, V_g: .*, S: [\w.]*Int, seed: [\w.]*Int = 42, block_n: [\w.]*Int = 0, "
                      r"want_vrows: bool = False\)", doc), doc
