@@ -38,6 +38,9 @@ def parse_args():
     ap.add_argument("--S", type=int, default=256)
     ap.add_argument("--seed", type=int, default=1690)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--workload", choices=("cfg2", "cfg3", "cfg5"), default="cfg2",
+                    help="cfg2: the headline (flash, B=8, 32k); cfg3: batched ragged santa_prop (B=16, "
+                         "L_b in [8192, 131072], S_b = L_b // 64); cfg5: flash stress (B=32, 64q/8kv, 128k, S=512)")
     ap.add_argument("--cpu-sample-seqs", type=int, default=8, help="sequences timed for the CPU baseline")
     ap.add_argument("--copy-calibration-mib", type=int, default=0,
                     help="first run a plain device copy of this many MiB 5 times (a known-size kernel "
@@ -100,6 +103,137 @@ def cpu_baseline(q, K, V, S, seed, n_seq, min_wall_s=2.0, max_reps=20):
                       f"median of {len(times)} steps, {dt:.3f} s each; C oracle, OpenMP over tiles"}
 
 
+def device_inputs(B, L, H, KVH, D, seed, dev, keys="bias"):
+    """Synthetic q, K, V generated on the device (the larger workloads): N(0,1),
+    with K either plus the rank-4 key bias of the headline recipe ("bias") or
+    Student-t(3) with 16 planted needle rows per (b, kv) ("needles": K rows
+    set to a multiple of the group's mean query direction, scoring ~6 nats
+    above the rest)."""
+    import torch
+
+    g = torch.Generator(device=dev).manual_seed(seed)
+    q = torch.randn(B, H, D, generator=g, device=dev)
+    V = torch.randn(B, L, KVH, D, generator=g, device=dev, dtype=torch.bfloat16)
+    if keys == "bias":
+        K = torch.randn(B, L, KVH, D, generator=g, device=dev)
+        C = torch.randn(B, L, KVH, 4, generator=g, device=dev)
+        U = torch.randn(KVH, 4, D, generator=g, device=dev) / math.sqrt(D)
+        K = (K + 0.5 * math.sqrt(D) * torch.einsum("blkr,krd->blkd", C, U)).bfloat16()
+        del C
+    else:
+        K = torch.empty(B, L, KVH, D, device=dev, dtype=torch.bfloat16)
+        for b in range(B):  # Student-t(3) = N / sqrt(chi2_3 / 3), one sequence at a time
+            n = torch.randn(L, KVH, D, generator=g, device=dev)
+            chi = (torch.randn(3, L, KVH, D, generator=g, device=dev) ** 2).sum(0) / 3.0
+            K[b] = (n / chi.sqrt()).bfloat16()
+        GH = H // KVH
+        qm = q.view(B, KVH, GH, D).mean(2)
+        qhat = qm / qm.norm(dim=-1, keepdim=True)
+        alpha = (12.0 + 6.0) * math.sqrt(D) / qm.norm(dim=-1, keepdim=True)
+        pos = torch.randint(0, L, (B, KVH, 16), generator=g, device=dev)
+        for kv in range(KVH):
+            K[torch.arange(B, device=dev)[:, None], pos[:, kv], kv] = (alpha[:, kv] * qhat[:, kv]).bfloat16()[:, None]
+    return q.bfloat16(), K, V
+
+
+def run_cfg3(args, dev):
+    """Batched ragged santa_prop: B=16 sequences, L_b ~ U[8192, 131072] (seeded),
+    S_b = L_b // 64, one decode_systematic_batched call per step."""
+    import torch
+    import santa_prop_batch_cuda as prop
+
+    B, H, KVH, D, seed = 16, 32, 8, 128, args.seed
+    gl = torch.Generator().manual_seed(seed)
+    lens = torch.randint(8192, 131072 + 1, (B,), generator=gl).tolist()
+    Ss = [l // 64 for l in lens]
+    L = max(lens)
+    q, K, V = device_inputs(B, L, H, KVH, D, seed, dev)
+    torch.cuda.synchronize()
+    _, _, vrows = prop.decode_systematic_batched(q, K, V, Ss, seed=seed, want_vrows=True, valid_len=lens)
+    v_rows = int(vrows.sum().item())
+    bytes_alg = sum(lens) * KVH * D * 2 + v_rows * D * 2 + B * H * D * 2 * 2 + B * H * 4
+    for _ in range(args.warmup):
+        prop.decode_systematic_batched(q, K, V, Ss, seed=seed, valid_len=lens)
+    stream = torch.cuda.current_stream()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    e0.record(stream)
+    for _ in range(args.steps):
+        prop.decode_systematic_batched(q, K, V, Ss, seed=seed, valid_len=lens)
+    e1.record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    ms_step = e0.elapsed_time(e1) / args.steps
+    achieved = bytes_alg / (ms_step * 1e-3) / 1e9
+    return {
+        "metric": "sampled-attn decode µs/step + achieved HBM TB/s; tokens/s (cfg3: batched ragged santa_prop)",
+        "value": B / (ms_step * 1e-3), "unit": "tokens/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": ms_step, "us_per_step": ms_step * 1e3, "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "bf16", "data": "synthetic",
+        "config": {"workload": f"santa_prop batched ragged decode, 32q/8kv, d=128, B={B}, L_b seeded U[8192, 131072] "
+                               f"(sum {sum(lens)}), S_b = L_b // 64, seed {seed}, K/V ~ N(0,1) + rank-4 key bias 0.5",
+                   "global_batch": B, "seq_len": lens, "S": Ss, "parallelism": "single GPU"},
+        "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                     "frac": achieved / HBM_PEAK_GBPS, "traffic": None,
+                     "kernel": "whole prop step (pass 1 + budgets + pass 2 + finalize)", "kernel_us": ms_step * 1e3,
+                     "bytes_alg_per_launch": bytes_alg, "emitted_v_rows": v_rows},
+        "wall_s_timed": wall,
+    }
+
+
+def run_cfg5(args, dev):
+    """Flash stress: B=32, 64q/8kv (GH 8), L=131072, S=512, Student-t(3) keys with
+    planted needles."""
+    import torch
+    import santa_flash_batch_cuda as flash
+
+    B, L, H, KVH, D, S, seed = 32, 131072, 64, 8, 128, 512, args.seed
+    q, K, V = device_inputs(B, L, H, KVH, D, seed, dev, keys="needles")
+    torch.cuda.synchronize()
+    _, _, vrows = flash.decode_systematic_batched(q, K, V, S, seed=seed, want_vrows=True)
+    v_rows = int(vrows.sum().item())
+    bytes_alg = B * L * KVH * D * 2 + v_rows * D * 2 + B * H * D * 2 * 2 + B * H * 4
+    for _ in range(args.warmup):
+        flash.decode_systematic_batched(q, K, V, S, seed=seed)
+    stream = torch.cuda.current_stream()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    e0.record(stream)
+    for _ in range(args.steps):
+        flash.decode_systematic_batched(q, K, V, S, seed=seed)
+    e1.record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    ms_step = e0.elapsed_time(e1) / args.steps
+    T_c = (L + 255) // 256
+    ws = torch.empty(flash._workspace_bytes(B, H, KVH, D, T_c), dtype=torch.uint8, device=dev)
+    k0, k1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    k0.record(stream)
+    for _ in range(args.steps):
+        flash._decode_tiles_only(q, K, V, S, seed, 0, -1, ws)
+    k1.record(stream)
+    torch.cuda.synchronize()
+    ms_kernel = k0.elapsed_time(k1) / args.steps
+    achieved = bytes_alg / (ms_kernel * 1e-3) / 1e9
+    return {
+        "metric": "sampled-attn decode µs/step + achieved HBM TB/s; tokens/s (cfg5: flash stress)",
+        "value": B / (ms_step * 1e-3), "unit": "tokens/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": ms_step, "us_per_step": ms_step * 1e3, "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "bf16", "data": "synthetic",
+        "config": {"workload": f"santa_flash decode, 64q/8kv (GH 8), d=128, B={B}, {L} cached tokens, S={S}, "
+                               f"seed {seed}, Student-t(3) keys with 16 planted needles per KV head",
+                   "global_batch": B, "seq_len": L, "S": S, "parallelism": "single GPU"},
+        "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                     "frac": achieved / HBM_PEAK_GBPS, "traffic": None,
+                     "kernel": "santa::flash::wave_kernel (block_n 256, GH 8)", "kernel_us": ms_kernel * 1e3,
+                     "bytes_alg_per_launch": bytes_alg, "emitted_v_rows": v_rows,
+                     "step_achieved_GBps": bytes_alg / (ms_step * 1e-3) / 1e9},
+        "wall_s_timed": wall,
+    }
+
+
 def main():
     args = parse_args()
     if args.gpus != 1:
@@ -107,6 +241,12 @@ def main():
                           "n_gpus": args.gpus}))
         return 2
     import torch
+
+    if args.workload != "cfg2":
+        dev = torch.device("cuda:0")
+        line = run_cfg3(args, dev) if args.workload == "cfg3" else run_cfg5(args, dev)
+        print(json.dumps(line))
+        return 0
     import santa_flash_batch_cuda as flash
 
     dev = torch.device("cuda:0")
