@@ -739,12 +739,16 @@ __device__ __forceinline__ float wave_ell(const float (&u)[2][2]) {
   }
 }
 
-template <bool BF16, int GH, bool DBG>
+// P1: santa_prop pass 1 with the vec path's numerics (the flash tile
+// statistics): per tile and head m and ell into dbg_m / dbg_ell ([B, H, T_c])
+// and the 16-bit u into u_stash ([B, L_storage, H]); no sampling, no partials.
+template <bool BF16, int GH, bool DBG, bool P1 = false>
 __global__ __launch_bounds__(kThreads, 2) void wave_kernel(
     const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K, const uint16_t* __restrict__ V, int H, int KVH,
     int L_valid, int L_storage, int T_c, int cs, int cpg, float q_scale, int S_pt, uint64_t seed,
     float* __restrict__ part, int* __restrict__ part_emit, const int* __restrict__ seq_lens, int B, long long S_total,
-    float* __restrict__ dbg_m, float* __restrict__ dbg_ell, int16_t* __restrict__ dbg_counts) {
+    float* __restrict__ dbg_m, float* __restrict__ dbg_ell, int16_t* __restrict__ dbg_counts,
+    uint16_t* __restrict__ u_stash = nullptr) {
   constexpr int BN = 256;
   constexpr int NHB = GH / 4;
   constexpr int LCAP = kWaveListCap;
@@ -916,6 +920,7 @@ __global__ __launch_bounds__(kThreads, 2) void wave_kernel(
 
     // ---- per head: u, ell, counts, sampled rows ----------------------------------
     uint64_t uni[2][2] = {{0, 0}, {0, 0}};
+    uint32_t ubits[P1 ? GH : 1][2][2];  // pass 1: the 16-bit u of this lane's rows
 #pragma unroll
     for (int g = 0; g < GH; ++g) {
       const int h = h0 + g;
@@ -929,6 +934,19 @@ __global__ __launch_bounds__(kThreads, 2) void wave_kernel(
           ub[hh][e] = round16_nonneg<BF16>(u[hh][e]);
         }
       const float ell = wave_ell<GH>(u);
+      if constexpr (P1) {
+        const size_t mt = (static_cast<size_t>(b) * H + h) * T_c + t;
+        if (lane == 0) {
+          dbg_m[mt] = mg[g];
+          dbg_ell[mt] = ell;
+        }
+#pragma unroll
+        for (int hh = 0; hh < 2; ++hh)
+#pragma unroll
+          for (int e = 0; e < 2; ++e)
+            ubits[g][hh][e] = BF16 ? (__float_as_uint(ub[hh][e]) >> 16) : static_cast<uint32_t>(f32_to_h16<false>(u[hh][e]));
+        continue;
+      }
       const float invdel = (S_pt > 0 && ell > 1e-20f) ? (static_cast<float>(S_pt) / ell) : 0.0f;
       const float a0 = u01(seed, b * H + h, t);
       // u (so the 16-bit u) is 0 past len and invdel is finite and >= 0, so
@@ -990,9 +1008,31 @@ __global__ __launch_bounds__(kThreads, 2) void wave_kernel(
           }
         }
     }
+    if constexpr (P1) {
+      // the stash row [n, h0 .. h0+GH) of each valid row: one 8-B (GH 4) or
+      // 16-B (GH 8) store
+#pragma unroll
+      for (int hh = 0; hh < 2; ++hh)
+#pragma unroll
+        for (int e = 0; e < 2; ++e) {
+          if (valid[hh][e]) {
+            uint16_t* dst = u_stash + (static_cast<size_t>(b) * L_storage + n0 + 128 * hh + 32 * jrow + 2 * qq + e) * H + h0;
+            if constexpr (GH == 4) {
+              *reinterpret_cast<uint2*>(dst) = make_uint2(ubits[0][hh][e] | (ubits[1][hh][e] << 16),
+                                                          ubits[2][hh][e] | (ubits[3][hh][e] << 16));
+            } else {
+              *reinterpret_cast<uint4*>(dst) = make_uint4(ubits[0][hh][e] | (ubits[1][hh][e] << 16),
+                                                          ubits[2][hh][e] | (ubits[3][hh][e] << 16),
+                                                          ubits[4][hh][e] | (ubits[5][hh][e] << 16),
+                                                          ubits[6][hh][e] | (ubits[7][hh][e] << 16));
+            }
+          }
+        }
+    }
     emit_total += __popcll(uni[0][0]) + __popcll(uni[0][1]) + __popcll(uni[1][0]) + __popcll(uni[1][1]);
     if constexpr (GH == 8) load_k(t + 4, 0);
   }
+  if constexpr (P1) return;  // pass 1 writes no partials
 #pragma unroll
   for (int g = 0; g < GH; ++g) flush(g);
 
@@ -1354,8 +1394,22 @@ hipError_t launch_prop_pass1(const void* q, const void* K, int dtype, int B, int
   }
   const int GH = H / KVH;
   if (path == 0) {
-    return (dtype == SANTA_BF16) ? launch_t<true, 4, 256, kPass1Vec>(a, stream)
-                                 : launch_t<false, 4, 256, kPass1Vec>(a, stream);
+    // the vec path (GH 4, block_n 256) on the wave kernel
+    const float q_scale = 1.0f / sqrtf(static_cast<float>(kD));
+    const unsigned grid = a.seq_lens ? static_cast<unsigned>(a.n_wg)
+                                     : static_cast<unsigned>(a.B) * static_cast<unsigned>(a.KVH) * static_cast<unsigned>(a.cpg);
+    if (grid == 0) return hipSuccess;
+    if (dtype == SANTA_BF16)
+      hipLaunchKernelGGL((wave_kernel<true, 4, false, true>), dim3(grid), dim3(kThreads), 0, stream,
+                         static_cast<const uint16_t*>(a.q), static_cast<const uint16_t*>(a.K), nullptr, a.H, a.KVH,
+                         a.L_valid, a.L_storage, a.T_c, a.cs, a.cpg, q_scale, 0, 0ULL, nullptr, nullptr, a.seq_lens,
+                         a.B, 0LL, m_tiles, ell_tiles, nullptr, u_stash);
+    else
+      hipLaunchKernelGGL((wave_kernel<false, 4, false, true>), dim3(grid), dim3(kThreads), 0, stream,
+                         static_cast<const uint16_t*>(a.q), static_cast<const uint16_t*>(a.K), nullptr, a.H, a.KVH,
+                         a.L_valid, a.L_storage, a.T_c, a.cs, a.cpg, q_scale, 0, 0ULL, nullptr, nullptr, a.seq_lens,
+                         a.B, 0LL, m_tiles, ell_tiles, nullptr, u_stash);
+    return hipGetLastError();
   }
   if (dtype == SANTA_BF16)
     return (GH == 4) ? launch_bn<true, 4, kPass1Gen>(block_n, a, stream)
@@ -1367,11 +1421,15 @@ hipError_t launch_prop_pass1(const void* q, const void* K, int dtype, int B, int
 // Tile chunking shared with santa_prop's pass 2.
 void plan_chunks(int B, int KVH, int T_c, int* cs, int* cpg) { chunk_plan(B, KVH, T_c, cs, cpg); }
 
-// Ragged batches: about one resident round over all (kv, tile) items; each
-// sequence adds at most one partial chunk per KV head.
+// Ragged batches: one resident round over all (kv, tile) items.  Each
+// sequence adds at most one partial chunk per KV head, so B * KVH of the
+// resident slots are kept for those (else the grid would spill into a short
+// second round).
 void plan_ragged(int B, int KVH, long long total_tiles, int* cs, int* n_wg) {
   const long long items = total_tiles * KVH;
-  long long want = resident_workgroups();
+  const long long resident = resident_workgroups();
+  const long long slack = static_cast<long long>(B) * KVH;
+  const long long want = (resident > 2 * slack) ? resident - slack : (resident + 1) / 2;
   long long c = (items + want - 1) / want;
   if (c < 1) c = 1;
   *cs = static_cast<int>(c);
