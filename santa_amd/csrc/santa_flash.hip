@@ -748,7 +748,7 @@ __global__ __launch_bounds__(kThreads, 2) void wave_kernel(
     int L_valid, int L_storage, int T_c, int cs, int cpg, float q_scale, int S_pt, uint64_t seed,
     float* __restrict__ part, int* __restrict__ part_emit, const int* __restrict__ seq_lens, int B, long long S_total,
     float* __restrict__ dbg_m, float* __restrict__ dbg_ell, int16_t* __restrict__ dbg_counts,
-    uint16_t* __restrict__ u_stash = nullptr) {
+    uint16_t* __restrict__ u_stash = nullptr, int stash_ld = 0) {
   constexpr int BN = 256;
   constexpr int NHB = GH / 4;
   constexpr int LCAP = kWaveListCap;
@@ -1008,7 +1008,16 @@ __global__ __launch_bounds__(kThreads, 2) void wave_kernel(
           }
         }
     }
-    if constexpr (P1) {
+    if (P1 && stash_ld > 0) {
+      // head-major stash: per head and register pair, the lane's two rows as
+      // one 4-B store (whole tiles, 0 past len)
+#pragma unroll
+      for (int g = 0; g < GH; ++g)
+#pragma unroll
+        for (int hh = 0; hh < 2; ++hh)
+          *reinterpret_cast<uint32_t*>(u_stash + (static_cast<size_t>(b) * H + h0 + g) * stash_ld + n0 + 128 * hh +
+                                       32 * jrow + 2 * qq) = ubits[g][hh][0] | (ubits[g][hh][1] << 16);
+    } else if constexpr (P1) {
       // the stash row [n, h0 .. h0+GH) of each valid row: one 8-B (GH 4) or
       // 16-B (GH 8) store
 #pragma unroll
@@ -1381,7 +1390,7 @@ hipError_t launch_expf(const float* x, float* y, size_t n, hipStream_t stream) {
 // santa_prop pass 1 on the tile kernel (declared in santa_internal.h).
 hipError_t launch_prop_pass1(const void* q, const void* K, int dtype, int B, int H, int KVH, int L, int L_storage,
                              int block_n, int path, float* m_tiles, float* ell_tiles, uint16_t* u_stash,
-                             const int* seq_lens, int cs, int n_wg, hipStream_t stream) {
+                             const int* seq_lens, int cs, int n_wg, int stash_ld, hipStream_t stream) {
   Args a{q, K, nullptr, B, H, KVH, L, L_storage, (L + block_n - 1) / block_n, 0, 0, m_tiles, ell_tiles, nullptr,
          nullptr, nullptr, nullptr, nullptr, 0, 0, u_stash, seq_lens};
   if (seq_lens) {
@@ -1403,12 +1412,12 @@ hipError_t launch_prop_pass1(const void* q, const void* K, int dtype, int B, int
       hipLaunchKernelGGL((wave_kernel<true, 4, false, true>), dim3(grid), dim3(kThreads), 0, stream,
                          static_cast<const uint16_t*>(a.q), static_cast<const uint16_t*>(a.K), nullptr, a.H, a.KVH,
                          a.L_valid, a.L_storage, a.T_c, a.cs, a.cpg, q_scale, 0, 0ULL, nullptr, nullptr, a.seq_lens,
-                         a.B, 0LL, m_tiles, ell_tiles, nullptr, u_stash);
+                         a.B, 0LL, m_tiles, ell_tiles, nullptr, u_stash, stash_ld);
     else
       hipLaunchKernelGGL((wave_kernel<false, 4, false, true>), dim3(grid), dim3(kThreads), 0, stream,
                          static_cast<const uint16_t*>(a.q), static_cast<const uint16_t*>(a.K), nullptr, a.H, a.KVH,
                          a.L_valid, a.L_storage, a.T_c, a.cs, a.cpg, q_scale, 0, 0ULL, nullptr, nullptr, a.seq_lens,
-                         a.B, 0LL, m_tiles, ell_tiles, nullptr, u_stash);
+                         a.B, 0LL, m_tiles, ell_tiles, nullptr, u_stash, stash_ld);
     return hipGetLastError();
   }
   if (dtype == SANTA_BF16)

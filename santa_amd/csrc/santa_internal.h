@@ -23,9 +23,11 @@ namespace flash {
 // Ragged form: seq_lens (device, [B]) holds each sequence's length, L the
 // longest (it sets the tile stride of m/ell), cs tiles per chunk and n_wg
 // workgroups (any workgroup past the last sequence exits at once).
+// stash_ld > 0 (vec path only): the stash is head-major [B, H, stash_ld],
+// whole 256-row tiles, 0 past each sequence's length.
 hipError_t launch_prop_pass1(const void* q, const void* K, int dtype, int B, int H, int KVH, int L, int L_storage,
                              int block_n, int path, float* m_tiles, float* ell_tiles, uint16_t* u_stash,
-                             const int* seq_lens, int cs, int n_wg, hipStream_t stream);
+                             const int* seq_lens, int cs, int n_wg, int stash_ld, hipStream_t stream);
 // Chunking of a ragged batch with total_tiles tiles: cs tiles per chunk and
 // an upper bound n_wg on the workgroups of the ragged grid.
 void plan_ragged(int B, int KVH, long long total_tiles, int* cs, int* n_wg);

@@ -198,7 +198,10 @@ __device__ __forceinline__ int union_rows(const uint64_t* s_mask, int lane) {
 // LDS list, then the count-weighted V rows (fma per element) added to the
 // head's running sum.  The next tile's stash entries are loaded before the
 // current tile's V gather.
-template <bool BF16, int GH, int BN>
+// HM: the stash is head-major [B, H, stash_ld] (the fused decode's layout
+// for the vec path: a lane reads its row pair with one 4-B load); otherwise
+// the reference's [B, L_storage, H].
+template <bool BF16, int GH, int BN, bool HM>
 __global__ __launch_bounds__(kThreads) void pass2_kernel(const uint16_t* __restrict__ V,
                                                          const uint16_t* __restrict__ u_stash, int H, int KVH,
                                                          int L, int L_storage, int T_c, int cs, int cpg,
@@ -206,7 +209,7 @@ __global__ __launch_bounds__(kThreads) void pass2_kernel(const uint16_t* __restr
                                                          const float* __restrict__ a0_tile,
                                                          int16_t* __restrict__ dbg_counts, float* __restrict__ part,
                                                          int* __restrict__ part_emit, int want_emit,
-                                                         const int* __restrict__ seq_lens, int B) {
+                                                         const int* __restrict__ seq_lens, int B, int stash_ld) {
   constexpr int NCH = BN / 32;
   constexpr int NPAIR = (NCH + 3) / 4;
   constexpr int HPW = GH / 4;
@@ -239,7 +242,8 @@ __global__ __launch_bounds__(kThreads) void pass2_kernel(const uint16_t* __restr
   const char* Vg = reinterpret_cast<const char*>(V + static_cast<size_t>(b) * L_storage * row_stride +
                                                  static_cast<size_t>(kv) * kD);
   const uint32_t v_lane_off = 4u * static_cast<uint32_t>(lane);
-  const uint16_t* ub = u_stash + static_cast<size_t>(b) * L_storage * H;
+  const uint16_t* ub = u_stash + static_cast<size_t>(b) * (HM ? static_cast<size_t>(H) * stash_ld
+                                                              : static_cast<size_t>(L_storage) * H);
 
   float acc0[HPW], acc1[HPW];
 #pragma unroll
@@ -248,6 +252,34 @@ __global__ __launch_bounds__(kThreads) void pass2_kernel(const uint16_t* __restr
     acc1[k] = 0.0f;
   }
   int emit_total = 0;
+
+  // Count-weighted V rows of the listed samples, in list (ascending) order,
+  // one fma per element (prop/santa_cuda_kernel.cu:843-857); up to 32 row
+  // loads are in flight before the first is used.
+  int lc[HPW];
+#pragma unroll
+  for (int k = 0; k < HPW; ++k) lc[k] = 0;
+  auto flush = [&](int k, int g) {
+    for (int base = 0; base < lc[k]; base += 32) {
+      float cf[32];
+      uint32_t vw[32];
+#pragma unroll
+      for (int q = 0; q < 32; ++q) {
+        const int i = min(base + q, lc[k] - 1);
+        const int rr = __builtin_amdgcn_readfirstlane(s_lrow[g * BN + i]);
+        cf[q] = s_lcw[g * BN + i];
+        vw[q] = *reinterpret_cast<const uint32_t*>(Vg + static_cast<size_t>(rr) * row_bytes + v_lane_off);
+      }
+#pragma unroll
+      for (int q = 0; q < 32; ++q) {
+        if (base + q < lc[k]) {
+          acc0[k] = fmaf(cf[q], lo16_to_f32<BF16>(vw[q]), acc0[k]);
+          acc1[k] = fmaf(cf[q], hi16_to_f32<BF16>(vw[q]), acc1[k]);
+        }
+      }
+    }
+    lc[k] = 0;
+  };
 
   // stash entries of tile t for this lane's rows: u[k][p][0/1]
   uint16_t un0[HPW][NPAIR], un1[HPW][NPAIR];
@@ -260,8 +292,15 @@ __global__ __launch_bounds__(kThreads) void pass2_kernel(const uint16_t* __restr
 #pragma unroll
       for (int p = 0; p < NPAIR; ++p) {
         const int row = 32 * (4 * p + jrow) + 2 * qq;
-        un0[k][p] = (row < len) ? ub[static_cast<size_t>(n0 + row) * H + h] : static_cast<uint16_t>(0);
-        un1[k][p] = (row + 1 < len) ? ub[static_cast<size_t>(n0 + row + 1) * H + h] : static_cast<uint16_t>(0);
+        if constexpr (HM) {
+          // whole padded tiles are in the stash (0 past len)
+          const uint32_t w = *reinterpret_cast<const uint32_t*>(ub + static_cast<size_t>(h) * stash_ld + n0 + row);
+          un0[k][p] = static_cast<uint16_t>(w & 0xffffu);
+          un1[k][p] = static_cast<uint16_t>(w >> 16);
+        } else {
+          un0[k][p] = (row < len) ? ub[static_cast<size_t>(n0 + row) * H + h] : static_cast<uint16_t>(0);
+          un1[k][p] = (row + 1 < len) ? ub[static_cast<size_t>(n0 + row + 1) * H + h] : static_cast<uint16_t>(0);
+        }
       }
     }
   };
@@ -292,22 +331,31 @@ __global__ __launch_bounds__(kThreads) void pass2_kernel(const uint16_t* __restr
       int c0[NPAIR], c1[NPAIR];
       systematic_counts<NCH>(x0[k], x1[k], len, a0v[k], lane, c0, c1);
       const uint64_t below = (1ull << lane) - 1ull;
+      uint64_t nz0[NPAIR], nz1[NPAIR];
       int cnt = 0;
 #pragma unroll
       for (int p = 0; p < NPAIR; ++p) {
+        nz0[p] = __ballot(c0[p] != 0);
+        nz1[p] = __ballot(c1[p] != 0);
+        cnt += __popcll(nz0[p]) + __popcll(nz1[p]);
+      }
+      // the list keeps the head's sampled rows across tiles; it is gathered
+      // when this tile's rows would not fit (and at the end of the chunk)
+      if (lc[k] + cnt > BN) flush(k, g);
+      int pos = lc[k];
+#pragma unroll
+      for (int p = 0; p < NPAIR; ++p) {
         const int row = 32 * (4 * p + jrow) + 2 * qq;
-        const uint64_t nz0 = __ballot(c0[p] != 0);
-        const uint64_t nz1 = __ballot(c1[p] != 0);
         if (lane == 0) {
-          s_mask[par][g * NM + 2 * p + 0] = nz0;
-          s_mask[par][g * NM + 2 * p + 1] = nz1;
+          s_mask[par][g * NM + 2 * p + 0] = nz0[p];
+          s_mask[par][g * NM + 2 * p + 1] = nz1[p];
         }
         if (dbg_counts && row < BN) {
           int16_t* dc = dbg_counts + ((static_cast<size_t>(b) * H + h) * T_c + t) * BN + row;
           dc[0] = static_cast<int16_t>(c0[p]);
           dc[1] = static_cast<int16_t>(c1[p]);
         }
-        const int pos0 = cnt + __popcll(nz0 & below) + __popcll(nz1 & below);
+        const int pos0 = pos + __popcll(nz0[p] & below) + __popcll(nz1[p] & below);
         const int pos1 = pos0 + (c0[p] != 0 ? 1 : 0);
         if (c0[p] != 0) {
           s_lrow[g * BN + pos0] = n0 + row;
@@ -317,27 +365,9 @@ __global__ __launch_bounds__(kThreads) void pass2_kernel(const uint16_t* __restr
           s_lrow[g * BN + pos1] = n0 + row + 1;
           s_lcw[g * BN + pos1] = static_cast<float>(c1[p]);
         }
-        cnt += __popcll(nz0) + __popcll(nz1);
+        pos += __popcll(nz0[p]) + __popcll(nz1[p]);
       }
-      // count-weighted V rows, ascending, one fma per element (:843-857)
-      for (int base = 0; base < cnt; base += 8) {
-        float cf[8];
-        uint32_t vw[8];
-#pragma unroll
-        for (int q = 0; q < 8; ++q) {
-          const int i = min(base + q, cnt - 1);
-          const int rr = __builtin_amdgcn_readfirstlane(s_lrow[g * BN + i]);
-          cf[q] = s_lcw[g * BN + i];
-          vw[q] = *reinterpret_cast<const uint32_t*>(Vg + static_cast<size_t>(rr) * row_bytes + v_lane_off);
-        }
-#pragma unroll
-        for (int q = 0; q < 8; ++q) {
-          if (base + q < cnt) {
-            acc0[k] = fmaf(cf[q], lo16_to_f32<BF16>(vw[q]), acc0[k]);
-            acc1[k] = fmaf(cf[q], hi16_to_f32<BF16>(vw[q]), acc1[k]);
-          }
-        }
-      }
+      lc[k] = pos;
     }
     if (want_emit) {
       // masks double-buffered by tile parity: one barrier per tile
@@ -348,6 +378,7 @@ __global__ __launch_bounds__(kThreads) void pass2_kernel(const uint16_t* __restr
 
 #pragma unroll
   for (int k = 0; k < HPW; ++k) {
+    flush(k, wave + 4 * k);
     float* pp = part + (static_cast<size_t>(wg) * GH + wave + 4 * k) * kD;
     reinterpret_cast<float2*>(pp)[lane] = make_float2(acc0[k], acc1[k]);
   }
@@ -398,6 +429,7 @@ __global__ __launch_bounds__(kD) void finalize_kernel(const float* __restrict__ 
 struct Pass2Grid {
   const int* seq_lens;
   int n_wg;
+  int stash_ld;  // > 0: head-major stash [B, H, stash_ld] (block_n 256 only)
 };
 
 template <bool BF16, int GH, int BN>
@@ -408,8 +440,14 @@ static hipError_t launch_pass2_t(const uint16_t* V, const uint16_t* u_stash, int
   const unsigned grid = rg.seq_lens ? static_cast<unsigned>(rg.n_wg)
                                     : static_cast<unsigned>(B) * static_cast<unsigned>(KVH) * static_cast<unsigned>(cpg);
   if (grid == 0) return hipSuccess;
-  hipLaunchKernelGGL((pass2_kernel<BF16, GH, BN>), dim3(grid), dim3(kThreads), 0, stream, V, u_stash, H, KVH, L,
-                     L_storage, T_c, cs, cpg, invdelta, a0, counts, part, part_emit, want_emit, rg.seq_lens, B);
+  if (BN == 256 && rg.stash_ld > 0)
+    hipLaunchKernelGGL((pass2_kernel<BF16, GH, BN, true>), dim3(grid), dim3(kThreads), 0, stream, V, u_stash, H, KVH,
+                       L, L_storage, T_c, cs, cpg, invdelta, a0, counts, part, part_emit, want_emit, rg.seq_lens, B,
+                       rg.stash_ld);
+  else
+    hipLaunchKernelGGL((pass2_kernel<BF16, GH, BN, false>), dim3(grid), dim3(kThreads), 0, stream, V, u_stash, H,
+                       KVH, L, L_storage, T_c, cs, cpg, invdelta, a0, counts, part, part_emit, want_emit, rg.seq_lens,
+                       B, 0);
   return hipGetLastError();
 }
 
@@ -430,6 +468,9 @@ static hipError_t launch_pass2_bn(int bn, const uint16_t* V, const uint16_t* u_s
                                            part, part_emit, want_emit, rg, stream);
   }
 }
+
+// Leading dimension of the head-major stash: whole 256-row tiles.
+static int stash_ld(int L_storage) { return (L_storage + 255) / 256 * 256; }
 
 // Workspace of one decode call (offsets 256-B aligned).
 // T_c is the tile stride of the [B, H, T_c] arrays (the longest sequence's
@@ -461,8 +502,8 @@ static PropWs prop_ws_layout(int B, int H, int KVH, int L_storage, int T_c, long
   off = align_up(off + bht * sizeof(float));
   w.a0 = off;
   off = align_up(off + bht * sizeof(float));
-  w.stash = off;
-  off = align_up(off + static_cast<size_t>(B) * L_storage * H * sizeof(uint16_t));
+  w.stash = off;  // [B, L_storage, H] or head-major [B, H, stash_ld(L_storage)]
+  off = align_up(off + static_cast<size_t>(B) * stash_ld(L_storage) * H * sizeof(uint16_t));
   w.part = off;
   off = align_up(off + chunks * (H / KVH) * kD * sizeof(float));
   w.emit = off;
@@ -547,7 +588,7 @@ extern "C" int santa_prop_pass1(const void* q, const void* K, int dtype, int H, 
                      H / KVH, D, block_n);
   if (!q || !K || !m_tiles || !ell_tiles || !u_stash) return set_error(SANTA_ERR_INVALID, "null pointer argument");
   const hipError_t e = flash::launch_prop_pass1(q, K, dtype, 1, H, KVH, L, L, block_n, pass1_path, m_tiles, ell_tiles,
-                                                static_cast<uint16_t*>(u_stash), nullptr, 0, 0, stream);
+                                                static_cast<uint16_t*>(u_stash), nullptr, 0, 0, 0, stream);
   if (e != hipSuccess) return set_error(SANTA_ERR_HIP, "pass-1 launch failed: %s", hipGetErrorString(e));
   return clear_error();
 }
@@ -580,8 +621,9 @@ extern "C" int santa_prop_tile_budgets(const float* m_tiles, const float* ell_ti
 static int prop_pass2_launch(const void* V, const uint16_t* u_stash, int dtype, int B, int H, int KVH, int L,
                              int L_storage, int block_n, int T_c, int S, const float* invdelta, const float* a0,
                              int16_t* counts, void* out, int* vrows, const prop::PropWs& w, char* base,
-                             hipStream_t stream, const int* seq_lens = nullptr, const int* seq_S = nullptr) {
-  const prop::Pass2Grid rg{seq_lens, w.n_wg};
+                             hipStream_t stream, const int* seq_lens = nullptr, const int* seq_S = nullptr,
+                             int stash_ld = 0) {
+  const prop::Pass2Grid rg{seq_lens, w.n_wg, stash_ld};
   float* part = reinterpret_cast<float*>(base + w.part);
   int* pe = reinterpret_cast<int*>(base + w.emit);
   const int GH = H / KVH;
@@ -668,13 +710,15 @@ extern "C" int santa_prop_decode(const void* q, const void* K, const void* V, in
   float* inv = reinterpret_cast<float*>(base + w.inv);
   float* a0 = reinterpret_cast<float*>(base + w.a0);
   uint16_t* stash = reinterpret_cast<uint16_t*>(base + w.stash);
+  // the vec path keeps the stash head-major between its two passes
+  const int sld = (pass1_path == 0) ? prop::stash_ld(L) : 0;
   hipError_t e = flash::launch_prop_pass1(q, K, dtype, 1, H, KVH, L, L, block_n, pass1_path, m_tiles, ell_tiles,
-                                          stash, nullptr, 0, 0, stream);
+                                          stash, nullptr, 0, 0, sld, stream);
   if (e != hipSuccess) return set_error(SANTA_ERR_HIP, "pass-1 launch failed: %s", hipGetErrorString(e));
   if ((st = prop_budgets_launch(m_tiles, ell_tiles, H, H, T_c, S, seed, m_star, S_tiles, inv, a0, stream)) != SANTA_OK)
     return st;
   if ((st = prop_pass2_launch(V, stash, dtype, 1, H, KVH, L, L, block_n, T_c, S, inv, a0, nullptr, out, vrows, w, base,
-                              stream)) != SANTA_OK)
+                              stream, nullptr, nullptr, sld)) != SANTA_OK)
     return st;
   return clear_error();
 }
@@ -714,14 +758,15 @@ extern "C" int santa_prop_decode_batched(const void* q, const void* K, const voi
   float* inv = reinterpret_cast<float*>(base + w.inv);
   float* a0 = reinterpret_cast<float*>(base + w.a0);
   uint16_t* stash = reinterpret_cast<uint16_t*>(base + w.stash);
+  const int sld = (pass1_path == 0) ? prop::stash_ld(L_storage) : 0;
   hipError_t e = flash::launch_prop_pass1(q, K, dtype, B, H, KVH, max_len, L_storage, block_n, pass1_path, m_tiles,
-                                          ell_tiles, stash, seq_lens, w.cs, w.n_wg, stream);
+                                          ell_tiles, stash, seq_lens, w.cs, w.n_wg, sld, stream);
   if (e != hipSuccess) return set_error(SANTA_ERR_HIP, "pass-1 launch failed: %s", hipGetErrorString(e));
   if ((st = prop_budgets_launch(m_tiles, ell_tiles, B * H, H, T_c, 0, seed, m_star, S_tiles, inv, a0, stream, seq_lens,
                                 seq_S, block_n)) != SANTA_OK)
     return st;
   if ((st = prop_pass2_launch(V, stash, dtype, B, H, KVH, max_len, L_storage, block_n, T_c, 0, inv, a0, nullptr, out,
-                              vrows, w, base, stream, seq_lens, seq_S)) != SANTA_OK)
+                              vrows, w, base, stream, seq_lens, seq_S, sld)) != SANTA_OK)
     return st;
   return clear_error();
 }
