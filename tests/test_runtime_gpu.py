@@ -1,0 +1,59 @@
+"""The model-level decode runtime on the GPU (bf16, a small Llama shape with
+head_dim 128 and 4 query heads per KV head).
+
+* The exact float32 decode backend agrees with recomputing the prefix with
+  the prefill (bf16 model: tolerance on the logits).
+* santa_flash with a budget of many samples per row approaches exact
+  attention: its teacher-forced logits stay close to the exact ones and agree
+  on the top token; santa_prop runs through the same loop.
+
+Every case prints its name before touching the GPU.
+"""
+import pytest
+import torch
+
+from santa_amd import attention_backends as ab
+from santa_amd.runtime import ExactDecodeBackend, LlamaShape, NHDCache, RandomLlama, decode_deviation, greedy_decode
+
+pytestmark = pytest.mark.gpu
+
+SMALL = LlamaShape(hidden=512, intermediate=1024, heads=4, kv_heads=1, layers=2, vocab=1000)
+
+
+def _setup(P=700, B=2, seed=11):
+    dev = torch.device("cuda:0")
+    model = RandomLlama(SMALL, seed=seed, std=0.05, device=dev)
+    toks = torch.randint(0, SMALL.vocab, (B, P + 8), generator=torch.Generator().manual_seed(seed)).to(dev)
+    cache = NHDCache(SMALL, B, P + 16, torch.bfloat16, dev)
+    logits = model.prefill(toks[:, :P], cache, attn_chunk=128)
+    return model, toks, cache, logits
+
+
+def test_exact_decode_matches_recomputation():
+    print("\n[case] runtime exact decode vs prefill recomputation, P=700 B=2", flush=True)
+    model, toks, cache, logits = _setup()
+    res = greedy_decode(model, logits, 700, cache, ExactDecodeBackend(), 6, forced=toks[:, 700:706])
+    torch.cuda.synchronize()
+    for j in range(6):
+        ref = model.prefill(toks[:, :700 + j], NHDCache(SMALL, 2, 720, torch.bfloat16, toks.device), attn_chunk=128)
+        err = (res["logits"][j] - ref).abs().max().item()
+        scale = ref.abs().max().item()
+        assert err <= 0.05 * scale, (j, err, scale)
+
+
+def test_santa_backends_in_the_decode_loop():
+    print("\n[case] runtime santa_flash (large S) and santa_prop vs exact, P=700 B=2", flush=True)
+    model, toks, cache, logits = _setup()
+    exact = greedy_decode(model, logits, 700, cache.clone(), ExactDecodeBackend(), 6)
+    flash = ab.SantaFlashBackend(S=64 * 32 * 32, seed=1690, block_n=None)
+    res = greedy_decode(model, logits, 700, cache.clone(), flash, 6, forced=exact["tokens"])
+    torch.cuda.synchronize()
+    assert flash.actual_mode == "batch"
+    dev = decode_deviation(res["logits"], exact["logits"])
+    scale = exact["logits"].abs().max().item()
+    assert max(dev["max_abs"]) <= 0.1 * scale, (dev, scale)
+    assert min(dev["top1_agree"]) == 1.0, dev
+    prop = ab.SantaPropBackend(S=700, seed=1690, block_n=None)
+    res_p = greedy_decode(model, logits, 700, cache.clone(), prop, 6, forced=exact["tokens"])
+    torch.cuda.synchronize()
+    assert prop.actual_mode == "batch" and torch.isfinite(res_p["logits"]).all()
