@@ -302,11 +302,11 @@ __device__ __forceinline__ float wave_max_lane63(float v) {
 // The 32-row chunk totals (pre + x at the chunk's last row) are carried
 // sequentially; c = floor(a0 + pre + x) - floor(a0 + pre) clamped to
 // [0, 32767].
-template <int NCH, int NP = (NCH + 3) / 4>
-__device__ __forceinline__ void systematic_counts(const float (&x0)[NP], const float (&x1)[NP], int len, float a0,
-                                                  int lane, int (&c0)[NP], int (&c1)[NP]) {
-  const int jrow = lane >> 4;
-  const int qq = lane & 15;
+// In-row inclusive scan of the register pairs; pre0 / pre1 are the exclusive
+// prefixes of x0 / x1 inside each 32-row chunk.
+template <int NP>
+__device__ __forceinline__ void scan_pairs(const float (&x0)[NP], const float (&x1)[NP], float (&pre0)[NP],
+                                           float (&pre1)[NP]) {
   float r0[NP], r1[NP];
 #pragma unroll
   for (int p = 0; p < NP; ++p) {
@@ -324,39 +324,58 @@ __device__ __forceinline__ void systematic_counts(const float (&x0)[NP], const f
     r0[p] = r0[p] + dpp_shr_zero<8>(r0[p]);
     r1[p] = r1[p] + dpp_shr_zero<8>(r1[p]);
   }
-  float pre0[NP], pre1[NP], car[NP];
 #pragma unroll
   for (int p = 0; p < NP; ++p) {
     pre0[p] = r0[p] - x0[p];
     pre1[p] = r1[p] - x1[p];
   }
+}
+
+// The counts of a full tile (len = 32 * NCH): every chunk ends at its row's
+// lane 15, odd element.  No branch, so the callers can interleave heads.
+template <int NCH, int NP = (NCH + 3) / 4>
+__device__ __forceinline__ void systematic_counts_full(const float (&x0)[NP], const float (&x1)[NP], float a0,
+                                                       int lane, int (&c0)[NP], int (&c1)[NP]) {
+  const int jrow = lane >> 4;
+  float pre0[NP], pre1[NP], car[NP];
+  scan_pairs<NP>(x0, x1, pre0, pre1);
   float carry = 0.0f;
+#pragma unroll
+  for (int p = 0; p < NP; ++p) {
+    const float tot1 = pre1[p] + x1[p];
+    float cj[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      cj[j] = carry;
+      if (4 * p + j < NCH) carry = carry + __int_as_float(__builtin_amdgcn_readlane(__float_as_int(tot1), 16 * j + 15));
+    }
+    car[p] = (jrow == 0) ? cj[0] : (jrow == 1) ? cj[1] : (jrow == 2) ? cj[2] : cj[3];
+  }
+#pragma unroll
+  for (int p = 0; p < NP; ++p) {
+    const float pg0 = car[p] + pre0[p];
+    const float pg1 = car[p] + pre1[p];
+    c0[p] = count_from_floors(a0, pg0, pg0 + x0[p]);
+    c1[p] = count_from_floors(a0, pg1, pg1 + x1[p]);
+    if (32 * (4 * p + jrow) >= 32 * NCH) {  // rows past BN (BN < 128)
+      c0[p] = 0;
+      c1[p] = 0;
+    }
+  }
+}
+
+template <int NCH, int NP = (NCH + 3) / 4>
+__device__ __forceinline__ void systematic_counts(const float (&x0)[NP], const float (&x1)[NP], int len, float a0,
+                                                  int lane, int (&c0)[NP], int (&c1)[NP]) {
   if (len >= 32 * NCH) {
-    // full tile: every chunk ends at its row's lane 15, odd element
-#pragma unroll
-    for (int p = 0; p < NP; ++p) {
-      const float tot1 = pre1[p] + x1[p];
-      float cj[4];
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        cj[j] = carry;
-        if (4 * p + j < NCH) carry = carry + __int_as_float(__builtin_amdgcn_readlane(__float_as_int(tot1), 16 * j + 15));
-      }
-      car[p] = (jrow == 0) ? cj[0] : (jrow == 1) ? cj[1] : (jrow == 2) ? cj[2] : cj[3];
-    }
-#pragma unroll
-    for (int p = 0; p < NP; ++p) {
-      const float pg0 = car[p] + pre0[p];
-      const float pg1 = car[p] + pre1[p];
-      c0[p] = count_from_floors(a0, pg0, pg0 + x0[p]);
-      c1[p] = count_from_floors(a0, pg1, pg1 + x1[p]);
-      if (32 * (4 * p + jrow) >= 32 * NCH) {  // rows past BN (BN < 128)
-        c0[p] = 0;
-        c1[p] = 0;
-      }
-    }
+    systematic_counts_full<NCH>(x0, x1, a0, lane, c0, c1);
     return;
   }
+  const int jrow = lane >> 4;
+  const int qq = lane & 15;
+  float pre0[NP], pre1[NP], car[NP];
+  scan_pairs<NP>(x0, x1, pre0, pre1);
+  float carry = 0.0f;
 #pragma unroll
   for (int p = 0; p < NP; ++p) {
     const float tot0 = pre0[p] + x0[p];

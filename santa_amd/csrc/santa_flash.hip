@@ -47,6 +47,8 @@
 #include "santa_amd.h"
 #include "santa_internal.h"
 
+#include <type_traits>
+
 namespace santa {
 namespace flash {
 
@@ -837,20 +839,46 @@ __global__ __launch_bounds__(kThreads, 2) void wave_kernel(
   u32x4 kw[16];
   const int k_lane_off = static_cast<int>((lane >> 4) * 2u * row_bytes + 16u * (lane & 15));
   auto load_k = [&](int t, int sb) {
+    const uint32_t rb = row_bytes;
     const int len = (t < t_end) ? min(BN, L_valid - t * BN) : 0;
     const int r0 = 128 * (sb >> 1) + (sb & 1);
-    const char* kt = Kg + static_cast<size_t>(t * BN + r0) * row_bytes;
+    const char* kt = Kg + static_cast<size_t>(t * BN + r0) * rb;
 #pragma unroll
     for (int c = 0; c < 16; ++c) {
       // wave-uniform; readfirstlane keeps the descriptor in SGPRs
       const int nvalid = __builtin_amdgcn_readfirstlane(min(max(len - r0 - 8 * c, 0), 8));
       const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
-          const_cast<char*>(kt + static_cast<size_t>(8 * c) * row_bytes), static_cast<short>(0),
-          nvalid * static_cast<int>(row_bytes), kBufferWord3);
+          const_cast<char*>(kt + static_cast<size_t>(8 * c) * rb), static_cast<short>(0),
+          nvalid * static_cast<int>(rb), kBufferWord3);
       kw[c] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rs, k_lane_off, 0, kBufferNontemporal));
     }
   };
-  load_k(t_begin + wave, 0);
+  // Sub-block 0 of tile t straight into the staging area (buffer loads to LDS;
+  // no registers held while in flight), in the staged layout: the load of
+  // rows 4c .. 4c+3 fills slots 64c .. 64c+63 in lane order, so lane 16j + p
+  // fetches the 16-B piece p ^ ((4c + j) & 15) of row 4c + j.  The caller
+  // waits (vmcnt) before reading the rows and issues it only once the area's
+  // previous rows have been read.
+  uint32_t k_dma_off[4];
+#pragma unroll
+  for (int m = 0; m < 4; ++m)
+    k_dma_off[m] = (lane >> 4) * 2u * row_bytes + 16u * static_cast<uint32_t>((lane & 15) ^ (4 * m + (lane >> 4)));
+  auto dma_k = [&](int t) {
+    const uint32_t rb = row_bytes;
+    const int len = min(BN, L_valid - t * BN);
+    const char* kt = Kg + static_cast<size_t>(t * BN) * rb;
+#pragma unroll
+    for (int c = 0; c < 16; ++c) {
+      const int nvalid = __builtin_amdgcn_readfirstlane(min(max(len - 8 * c, 0), 8));
+      const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+          const_cast<char*>(kt + static_cast<size_t>(8 * c) * rb), static_cast<short>(0),
+          nvalid * static_cast<int>(rb), kBufferWord3);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (__attribute__((address_space(3))) void*)(wk + 64 * c), 16,
+                                               k_dma_off[c & 3], 0, 0, kBufferNontemporal);
+    }
+  };
+  if (t_begin + wave < t_end) dma_k(t_begin + wave);
+  load_k(t_begin + wave, 1);
 
   const int jrow = lane >> 4;
   const int qq = lane & 15;
@@ -863,14 +891,28 @@ __global__ __launch_bounds__(kThreads, 2) void wave_kernel(
     f32x4 sc[2][2][NHB];
 #pragma unroll
     for (int sb = 0; sb < 4; ++sb) {
+      if (sb == 0) {
+        // sub-block 0 came by DMA; for GH 8 the 16 loads of sub-block 1 were
+        // issued after it
+        if constexpr (GH == 4) {
+          asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        } else {
+          asm volatile("s_waitcnt vmcnt(16)" ::: "memory");
+        }
+      } else {
 #pragma unroll
-      for (int c = 0; c < 16; ++c) {
-        const int r = 4 * c + (lane >> 4);
-        wk[r * 16 + ((lane & 15) ^ (r & 15))] = kw[c];
+        for (int c = 0; c < 16; ++c) {
+          const int r = 4 * c + (lane >> 4);
+          wk[r * 16 + ((lane & 15) ^ (r & 15))] = kw[c];
+        }
+        // sub-blocks 2, 3, then the next tile's sub-block 1 (GH 4; GH 8 loads
+        // it after the tail, whose registers would not fit beside it)
+        if (sb < 3) {
+          load_k(t, sb + 1);
+        } else if constexpr (GH == 4) {
+          load_k(t + 4, 1);
+        }
       }
-      // GH = 8: the next tile's first sub-block is loaded after the tail (whose
-      // registers would not fit beside it; the 8-head tail is VALU-bound)
-      if (GH == 4 || sb < 3) load_k(sb == 3 ? t + 4 : t, (sb + 1) & 3);
       __builtin_amdgcn_wave_barrier();
       const int row = lane;
       if constexpr (NHB == 1) {
@@ -899,6 +941,10 @@ __global__ __launch_bounds__(kThreads, 2) void wave_kernel(
       }
     }
 
+    // every row of the staging area has been read: the next tile's sub-block 0
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    if (t + 4 < t_end) dma_k(t + 4);
+
     // ---- tile max per head (exact in any order) --------------------------------
     bool valid[2][2];
 #pragma unroll
@@ -918,96 +964,131 @@ __global__ __launch_bounds__(kThreads, 2) void wave_kernel(
       mg[g] = from_order_key(__builtin_amdgcn_readlane(k, 63));
     }
 
-    // ---- per head: u, ell, counts, sampled rows ----------------------------------
+    // ---- per block of four heads: u, ell, counts, running max, sampled rows -----
+    // Each step runs for the block's four heads side by side with no branch, so
+    // their dependency chains interleave; only the list appends are sequential.
     uint64_t uni[2][2] = {{0, 0}, {0, 0}};
     uint32_t ubits[P1 ? GH : 1][2][2];  // pass 1: the 16-bit u of this lane's rows
+    // (a lambda per block index, so both blocks of GH 8 are emitted unrolled:
+    // the per-head state stays in registers)
+    auto head_block = [&](auto hbc) {
+      constexpr int hb = decltype(hbc)::value;
+      float u[4][2][2], ub[4][2][2];
 #pragma unroll
-    for (int g = 0; g < GH; ++g) {
-      const int h = h0 + g;
-      float u[2][2], ub[2][2];
-#pragma unroll
-      for (int hh = 0; hh < 2; ++hh)
-#pragma unroll
-        for (int e = 0; e < 2; ++e) {
-          // s - m <= 0 for the rows that take part (inputs are finite)
-          u[hh][e] = valid[hh][e] ? santa_expf_nonpos(sc[hh][e][g >> 2][g & 3] - mg[g]) : 0.0f;
-          ub[hh][e] = round16_nonneg<BF16>(u[hh][e]);
-        }
-      const float ell = wave_ell<GH>(u);
-      if constexpr (P1) {
-        const size_t mt = (static_cast<size_t>(b) * H + h) * T_c + t;
-        if (lane == 0) {
-          dbg_m[mt] = mg[g];
-          dbg_ell[mt] = ell;
-        }
+      for (int k = 0; k < 4; ++k)
 #pragma unroll
         for (int hh = 0; hh < 2; ++hh)
 #pragma unroll
-          for (int e = 0; e < 2; ++e)
-            ubits[g][hh][e] = BF16 ? (__float_as_uint(ub[hh][e]) >> 16) : static_cast<uint32_t>(f32_to_h16<false>(u[hh][e]));
-        continue;
+          for (int e = 0; e < 2; ++e) {
+            // s - m <= 0 for the rows that take part (inputs are finite);
+            // rows past len take 0 in place of s - m and give u = 0
+            const float d = sc[hh][e][hb][k] - mg[4 * hb + k];
+            const float ex = santa_expf_nonpos(valid[hh][e] ? d : 0.0f);
+            u[k][hh][e] = valid[hh][e] ? ex : 0.0f;
+            ub[k][hh][e] = round16_nonneg<BF16>(u[k][hh][e]);
+          }
+      float ell[4];
+#pragma unroll
+      for (int k = 0; k < 4; ++k) ell[k] = wave_ell<GH>(u[k]);
+      if constexpr (P1) {
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          const size_t mt = (static_cast<size_t>(b) * H + h0 + 4 * hb + k) * T_c + t;
+          if (lane == 0) {
+            dbg_m[mt] = mg[4 * hb + k];
+            dbg_ell[mt] = ell[k];
+          }
+#pragma unroll
+          for (int hh = 0; hh < 2; ++hh)
+#pragma unroll
+            for (int e = 0; e < 2; ++e)
+              ubits[4 * hb + k][hh][e] =
+                  BF16 ? (__float_as_uint(ub[k][hh][e]) >> 16) : static_cast<uint32_t>(f32_to_h16<false>(u[k][hh][e]));
+        }
+        return;
       }
-      const float invdel = (S_pt > 0 && ell > 1e-20f) ? (static_cast<float>(S_pt) / ell) : 0.0f;
-      const float a0 = u01(seed, b * H + h, t);
       // u (so the 16-bit u) is 0 past len and invdel is finite and >= 0, so
       // x = ub * invdel is the reference's 0 there without a select
-      float x0[2], x1[2];
+      float x0[4][2], x1[4][2], a0[4];
 #pragma unroll
-      for (int hh = 0; hh < 2; ++hh) {
-        x0[hh] = ub[hh][0] * invdel;
-        x1[hh] = ub[hh][1] * invdel;
-      }
-      int cnt[2][2];
-      systematic_counts<8>(x0, x1, len, a0, lane, cnt[0], cnt[1]);
-      // cnt[0] / cnt[1] are the e = 0 / e = 1 rows of register pairs hh = 0, 1
-      if constexpr (DBG) {
-        const size_t mt = (static_cast<size_t>(b) * H + h) * T_c + t;
-        if (lane == 0) {
-          dbg_m[mt] = mg[g];
-          dbg_ell[mt] = ell;
-        }
+      for (int k = 0; k < 4; ++k) {
+        const float invdel = (S_pt > 0 && ell[k] > 1e-20f) ? (static_cast<float>(S_pt) / ell[k]) : 0.0f;
+        a0[k] = u01(seed, b * H + h0 + 4 * hb + k, t);
 #pragma unroll
         for (int hh = 0; hh < 2; ++hh) {
-          int16_t* dc = dbg_counts + mt * BN + 128 * hh + 32 * jrow + 2 * qq;
-          dc[0] = static_cast<int16_t>(cnt[0][hh]);
-          dc[1] = static_cast<int16_t>(cnt[1][hh]);
+          x0[k][hh] = ub[k][hh][0] * invdel;
+          x1[k][hh] = ub[k][hh][1] * invdel;
+        }
+      }
+      // cnt[k][0] / cnt[k][1] are the e = 0 / e = 1 rows of register pairs hh = 0, 1
+      int cnt[4][2][2];
+      if (len == BN) {
+#pragma unroll
+        for (int k = 0; k < 4; ++k) systematic_counts_full<8>(x0[k], x1[k], a0[k], lane, cnt[k][0], cnt[k][1]);
+      } else {
+#pragma unroll
+        for (int k = 0; k < 4; ++k) systematic_counts<8>(x0[k], x1[k], len, a0[k], lane, cnt[k][0], cnt[k][1]);
+      }
+      if constexpr (DBG) {
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          const size_t mt = (static_cast<size_t>(b) * H + h0 + 4 * hb + k) * T_c + t;
+          if (lane == 0) {
+            dbg_m[mt] = mg[4 * hb + k];
+            dbg_ell[mt] = ell[k];
+          }
+#pragma unroll
+          for (int hh = 0; hh < 2; ++hh) {
+            int16_t* dc = dbg_counts + mt * BN + 128 * hh + 32 * jrow + 2 * qq;
+            dc[0] = static_cast<int16_t>(cnt[k][0][hh]);
+            dc[1] = static_cast<int16_t>(cnt[k][1][hh]);
+          }
         }
       }
 
-      // running max and mass; listed coefficients follow the running max
-      float f;
-      if (mg[g] > runM[g]) {
-        const float r = santa_expf(runM[g] - mg[g]);
-        runZ[g] = fmaf(runZ[g], r, ell);
-        num0[g] *= r;
-        num1[g] *= r;
-        if (lane < lcnt[g]) lcw[g * LCAP + lane] *= r;
-        runM[g] = mg[g];
-        f = ell;
-      } else {
-        const float w = santa_expf(mg[g] - runM[g]);
-        runZ[g] = fmaf(w, ell, runZ[g]);
-        f = ell * w;
+      // running max and mass; a sampled row's coefficient is c * f, relative to
+      // the running max.  When the max grows, the numerator and the listed
+      // coefficients are rescaled by exp(old - new).
+      float f[4], rsc[4];
+      bool grow[4];
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const int g = 4 * hb + k;
+        grow[k] = mg[g] > runM[g];
+        const float ex = santa_expf(grow[k] ? runM[g] - mg[g] : mg[g] - runM[g]);
+        runZ[g] = grow[k] ? fmaf(runZ[g], ex, ell[k]) : fmaf(ex, ell[k], runZ[g]);
+        num0[g] = grow[k] ? num0[g] * ex : num0[g];
+        num1[g] = grow[k] ? num1[g] * ex : num1[g];
+        f[k] = grow[k] ? ell[k] : ell[k] * ex;
+        rsc[k] = ex;
+        runM[g] = grow[k] ? mg[g] : runM[g];
       }
 #pragma unroll
-      for (int hh = 0; hh < 2; ++hh)
+      for (int k = 0; k < 4; ++k) {
+        const int g = 4 * hb + k;
+        if (grow[k] && lane < lcnt[g]) lcw[g * LCAP + lane] *= rsc[k];
 #pragma unroll
-        for (int e = 0; e < 2; ++e) {
-          const int c = cnt[e][hh];
-          const uint64_t nz = __ballot(c != 0);
-          uni[hh][e] |= nz;
-          const int nn = __popcll(nz);
-          if (nn) {
-            if (lcnt[g] + nn > LCAP) flush(g);
-            const int pos = lcnt[g] + __popcll(nz & below);
-            if (c != 0) {
-              lrow[g * LCAP + pos] = n0 + 128 * hh + 32 * jrow + 2 * qq + e;
-              lcw[g * LCAP + pos] = static_cast<float>(c) * f;
+        for (int hh = 0; hh < 2; ++hh)
+#pragma unroll
+          for (int e = 0; e < 2; ++e) {
+            const int c = cnt[k][e][hh];
+            const uint64_t nz = __ballot(c != 0);
+            uni[hh][e] |= nz;
+            const int nn = __popcll(nz);
+            if (nn) {
+              if (lcnt[g] + nn > LCAP) flush(g);
+              const int pos = lcnt[g] + __popcll(nz & below);
+              if (c != 0) {
+                lrow[g * LCAP + pos] = n0 + 128 * hh + 32 * jrow + 2 * qq + e;
+                lcw[g * LCAP + pos] = static_cast<float>(c) * f[k];
+              }
+              lcnt[g] += nn;
             }
-            lcnt[g] += nn;
           }
-        }
-    }
+      }
+    };
+    head_block(std::integral_constant<int, 0>{});
+    if constexpr (NHB == 2) head_block(std::integral_constant<int, 1>{});
     if (P1 && stash_ld > 0) {
       // head-major stash: per head and register pair, the lane's two rows as
       // one 4-B store (whole tiles, 0 past len)
@@ -1039,8 +1120,10 @@ __global__ __launch_bounds__(kThreads, 2) void wave_kernel(
         }
     }
     emit_total += __popcll(uni[0][0]) + __popcll(uni[0][1]) + __popcll(uni[1][0]) + __popcll(uni[1][1]);
-    if constexpr (GH == 8) load_k(t + 4, 0);
+    if constexpr (GH == 8) load_k(t + 4, 1);
   }
+  // no load to LDS outstanding past here (the staging area is reused below)
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   if constexpr (P1) return;  // pass 1 writes no partials
 #pragma unroll
   for (int g = 0; g < GH; ++g) flush(g);
