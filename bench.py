@@ -44,6 +44,9 @@ def parse_args():
                          "Llama-3.1-8B shape, B=4, 32768-token prompt, 64 greedy steps, santa_flash S=256 vs exact; "
                          "cfg5: flash stress (B=32, 64q/8kv, 128k, S=512)")
     ap.add_argument("--cpu-sample-seqs", type=int, default=8, help="sequences timed for the CPU baseline")
+    ap.add_argument("--page-size", type=int, default=0,
+                    help="cfg2 / cfg3 through the paged-KV entry point: the same tokens scattered over a pool of "
+                         "pages of this many tokens in a seeded random order (0: contiguous cache)")
     ap.add_argument("--copy-calibration-mib", type=int, default=0,
                     help="first run a plain device copy of this many MiB 5 times (a known-size kernel "
                          "that calibrates rocprofv3 FETCH_SIZE / WRITE_SIZE)")
@@ -138,6 +141,83 @@ def device_inputs(B, L, H, KVH, D, seed, dev, keys="bias"):
     return q.bfloat16(), K, V
 
 
+def to_pages(K, V, P, seed):
+    """K, V [B, L, KVH, D] on the device -> a pool [B * ceil(L / P), P, KVH, D]
+    holding every sequence's pages in a seeded random order, and the int32
+    block table [B, ceil(L / P)]."""
+    import torch
+
+    B, L, KVH, D = K.shape
+    n = (L + P - 1) // P
+    perm = torch.randperm(B * n, generator=torch.Generator().manual_seed(seed + 1)).to(K.device)
+    pools = []
+    for X in (K, V):
+        if n * P != L:
+            X = torch.cat([X, X.new_zeros(B, n * P - L, KVH, D)], dim=1)
+        pool = torch.empty(B * n, P, KVH, D, dtype=X.dtype, device=X.device)
+        pool[perm] = X.reshape(B * n, P, KVH, D)
+        pools.append(pool)
+    return pools[0], pools[1], perm.view(B, n).to(torch.int32).contiguous()
+
+
+def time_steps(step, args):
+    """Mean ms per call of step() over args.steps calls after args.warmup,
+    with HIP events on torch's current stream; also the host wall time."""
+    import torch
+
+    for _ in range(args.warmup):
+        step()
+    stream = torch.cuda.current_stream()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    e0.record(stream)
+    for _ in range(args.steps):
+        step()
+    e1.record(stream)
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / args.steps, time.perf_counter() - t0
+
+
+def run_cfg2_paged(args, dev):
+    """The headline workload through decode_systematic_paged: the same tokens
+    in a pool of args.page_size-token pages (seeded random page order)."""
+    import torch
+    import santa_flash_batch_cuda as flash
+
+    B, L, S, seed, P = args.batch, args.ctx, args.S, args.seed, args.page_size
+    H, KVH, D = 32, 8, 128
+    q_c, K_c, V_c = make_inputs(B, L, H, KVH, D, seed)
+    q = q_c.to(dev)
+    Kp, Vp, table = to_pages(K_c.to(dev), V_c.to(dev), P, seed)
+    torch.cuda.synchronize()
+    lens = [L] * B
+
+    def step(want_vrows=False):
+        return flash.decode_systematic_paged(q, Kp, Vp, table, lens, S, seed=seed, want_vrows=want_vrows)
+
+    _, _, vrows = step(True)
+    v_rows = int(vrows.sum().item())
+    bytes_alg = B * L * KVH * D * 2 + v_rows * D * 2 + B * H * D * 2 * 2 + B * H * 4
+    ms_step, wall = time_steps(step, args)
+    achieved = bytes_alg / (ms_step * 1e-3) / 1e9
+    return {
+        "metric": "sampled-attn decode µs/step + achieved HBM TB/s (B=8, 32k ctx, S=256); tokens/s (paged KV)",
+        "value": B / (ms_step * 1e-3), "unit": "tokens/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": ms_step, "us_per_step": ms_step * 1e3, "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "bf16", "data": "synthetic",
+        "config": {"workload": f"santa_flash decode, Llama-3.1-8B attention shape (32q/8kv, d=128), B={B}, {L} "
+                               f"cached tokens in {P}-token pages (seeded random page order), S={S}, seed {seed}, "
+                               "K/V ~ N(0,1) + rank-4 key bias 0.5",
+                   "global_batch": B, "seq_len": L, "S": S, "page_size": P, "parallelism": "single GPU"},
+        "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                     "frac": achieved / HBM_PEAK_GBPS, "traffic": None,
+                     "kernel": "whole paged decode step (wave kernel + merge)", "kernel_us": ms_step * 1e3,
+                     "bytes_alg_per_launch": bytes_alg, "emitted_v_rows": v_rows},
+        "wall_s_timed": wall,
+    }
+
+
 def run_cfg3(args, dev):
     """Batched ragged santa_prop: B=16 sequences, L_b ~ U[8192, 131072] (seeded),
     S_b = L_b // 64, one decode_systematic_batched call per step."""
@@ -151,22 +231,20 @@ def run_cfg3(args, dev):
     L = max(lens)
     q, K, V = device_inputs(B, L, H, KVH, D, seed, dev)
     torch.cuda.synchronize()
-    _, _, vrows = prop.decode_systematic_batched(q, K, V, Ss, seed=seed, want_vrows=True, valid_len=lens)
+    P = args.page_size
+    if P:
+        Kp, Vp, table = to_pages(K, V, P, seed)
+        del K, V
+
+        def step(want_vrows=False):
+            return prop.decode_systematic_paged(q, Kp, Vp, table, lens, Ss, seed=seed, want_vrows=want_vrows)
+    else:
+        def step(want_vrows=False):
+            return prop.decode_systematic_batched(q, K, V, Ss, seed=seed, want_vrows=want_vrows, valid_len=lens)
+    _, _, vrows = step(True)
     v_rows = int(vrows.sum().item())
     bytes_alg = sum(lens) * KVH * D * 2 + v_rows * D * 2 + B * H * D * 2 * 2 + B * H * 4
-    for _ in range(args.warmup):
-        prop.decode_systematic_batched(q, K, V, Ss, seed=seed, valid_len=lens)
-    stream = torch.cuda.current_stream()
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    e0.record(stream)
-    for _ in range(args.steps):
-        prop.decode_systematic_batched(q, K, V, Ss, seed=seed, valid_len=lens)
-    e1.record(stream)
-    torch.cuda.synchronize()
-    wall = time.perf_counter() - t0
-    ms_step = e0.elapsed_time(e1) / args.steps
+    ms_step, wall = time_steps(step, args)
     achieved = bytes_alg / (ms_step * 1e-3) / 1e9
     return {
         "metric": "sampled-attn decode µs/step + achieved HBM TB/s; tokens/s (cfg3: batched ragged santa_prop)",
@@ -174,7 +252,8 @@ def run_cfg3(args, dev):
         "warmup": args.warmup, "ms_per_step": ms_step, "us_per_step": ms_step * 1e3, "higher_is_better": True,
         "scaling": "weak", "vs_baseline": None, "dtype": "bf16", "data": "synthetic",
         "config": {"workload": f"santa_prop batched ragged decode, 32q/8kv, d=128, B={B}, L_b seeded U[8192, 131072] "
-                               f"(sum {sum(lens)}), S_b = L_b // 64, seed {seed}, K/V ~ N(0,1) + rank-4 key bias 0.5",
+                               f"(sum {sum(lens)}), S_b = L_b // 64, seed {seed}, K/V ~ N(0,1) + rank-4 key bias 0.5"
+                               + (f", paged KV ({P}-token pages in a seeded random order)" if P else ""),
                    "global_batch": B, "seq_len": lens, "S": Ss, "parallelism": "single GPU"},
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                      "frac": achieved / HBM_PEAK_GBPS, "traffic": None,
@@ -300,8 +379,11 @@ def main():
         return 2
     import torch
 
-    if args.workload != "cfg2":
+    if args.workload != "cfg2" or args.page_size:
         dev = torch.device("cuda:0")
+        if args.workload == "cfg2":
+            print(json.dumps(run_cfg2_paged(args, dev)))
+            return 0
         line = {"cfg3": run_cfg3, "cfg4": run_cfg4, "cfg5": run_cfg5}[args.workload](args, dev)
         print(json.dumps(line))
         return 0

@@ -121,12 +121,31 @@ int santa_flash_decode_merge(const void* workspace, size_t workspace_bytes, int 
  * seq_lens (<= L_storage) and total_tiles = sum over b of
  * ceil(seq_lens[b] / block_n), from the host; one block_n (32, 64 or 256)
  * for every sequence.  out [B,H,D], m_star [B,H], vrows [B,KVH] (may be
- * NULL).  Lengths are clamped on the device to [1, max_len]. */
-size_t santa_flash_ragged_workspace_size(int B, int H, int KVH, int D, long long total_tiles);
+ * NULL).  Lengths are clamped on the device to [1, max_len].  Workspace:
+ * santa_flash_ragged_workspace_size with max_tiles = ceil(max_len / block_n). */
+size_t santa_flash_ragged_workspace_size(int B, int H, int KVH, int D, int max_tiles, long long total_tiles);
 int santa_flash_decode_ragged(const void* q, const void* K, const void* V, int dtype, int B, int H, int KVH, int D,
                               int L_storage, const int* seq_lens, int max_len, long long total_tiles, int block_n,
                               int64_t S, uint64_t seed, void* out, float* m_star, int* vrows, void* workspace,
                               size_t workspace_bytes, hipStream_t stream);
+
+/* Paged flash (no counterpart in the reference, which reads contiguous NHD
+ * caches only, README.md:257 and tutorial_code/runtime_common.py:340-397):
+ * santa_flash_decode_ragged over a page pool K_pages / V_pages
+ * [num_pages, page_size, KVH, D] in place of the contiguous cache.  Token n
+ * of sequence b is row n % page_size of page
+ * block_table[b * table_stride + n / page_size]; block_table is a device int
+ * array [B, table_stride] with table_stride >= ceil(max_len / page_size).
+ * page_size is a power of two in [8, 2^20].  Page ids are clamped to
+ * [0, num_pages) on the device.  Results are bit-identical to the ragged call
+ * on the same tokens stored contiguously.  Workspace:
+ * santa_flash_ragged_workspace_size(B, H, KVH, D, ceil(max_len / block_n),
+ * total_tiles). */
+int santa_flash_decode_paged(const void* q, const void* K_pages, const void* V_pages, int dtype, int B, int H, int KVH,
+                             int D, int num_pages, int page_size, const int* block_table, int table_stride,
+                             const int* seq_lens, int max_len, long long total_tiles, int block_n, int64_t S,
+                             uint64_t seed, void* out, float* m_star, int* vrows, void* workspace,
+                             size_t workspace_bytes, hipStream_t stream);
 
 /* -------------------------------------------------------------- prop */
 
@@ -178,6 +197,19 @@ int santa_prop_decode_batched(const void* q, const void* K, const void* V, int d
                               int L_storage, const int* seq_lens, const int* seq_S, int max_len, long long total_tiles,
                               int block_n, int pass1_path, uint64_t seed, void* out, float* m_star, int* vrows,
                               void* workspace, size_t workspace_bytes, hipStream_t stream);
+
+/* Paged santa_prop (no counterpart in the reference, which reads contiguous
+ * NHD caches only, README.md:257): santa_prop_decode_batched over a page
+ * pool K_pages / V_pages [num_pages, page_size, KVH, D], with the block table
+ * and page geometry of santa_flash_decode_paged.  Results are bit-identical
+ * to the batched call on the same tokens stored contiguously.  Workspace:
+ * santa_prop_batched_workspace_size(B, H, KVH, D, max_len, ceil(max_len /
+ * block_n), total_tiles). */
+int santa_prop_decode_paged(const void* q, const void* K_pages, const void* V_pages, int dtype, int B, int H, int KVH,
+                            int D, int num_pages, int page_size, const int* block_table, int table_stride,
+                            const int* seq_lens, const int* seq_S, int max_len, long long total_tiles, int block_n,
+                            int pass1_path, uint64_t seed, void* out, float* m_star, int* vrows, void* workspace,
+                            size_t workspace_bytes, hipStream_t stream);
 
 #ifdef __cplusplus
 }

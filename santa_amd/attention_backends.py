@@ -185,6 +185,22 @@ class _SantaBaseBackend(DecodeAttentionBackend):
             outputs.append(self._unwrap_tensor_out(fn(q_bhd[b].contiguous(), k_b, v_b, self.S, **kwargs)))
         return torch.stack(outputs, dim=0).contiguous()
 
+    def decode_paged(self, q_bhd: torch.Tensor, k_pages: torch.Tensor, v_pages: torch.Tensor,
+                     block_table: torch.Tensor, seq_lens) -> torch.Tensor:
+        """Decode over a paged cache (not in the reference's adapters, whose
+        caches are contiguous): k_pages / v_pages [num_pages, page_size, KVH, D],
+        block_table int32 [B, pages per sequence], seq_lens an int or one
+        length per sequence.  Same S, seed and block_n as decode()."""
+        fn = getattr(self.module, "decode_systematic_paged", None)
+        if fn is None:
+            raise BackendError(f"Module {self.module_name} does not expose a paged decode entry point.")
+        kwargs: Dict[str, Any] = {"seed": self.seed, "want_vrows": False}
+        if self.block_n is not None:
+            kwargs["block_n"] = int(self.block_n)
+        out = fn(q_bhd.contiguous(), k_pages, v_pages, block_table, seq_lens, self.S, **kwargs)
+        self.actual_mode = "paged"
+        return self._unwrap_tensor_out(out).contiguous()
+
     def info(self) -> Dict[str, Any]:
         return {**super().info(), "module": self.module_name, "requested_S": self.S, "seed": self.seed,
                 "block_n": self.block_n, "actual_mode": self.actual_mode}

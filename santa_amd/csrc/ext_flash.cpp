@@ -98,6 +98,17 @@ at::Tensor aligned_q(const at::Tensor& q_h) {
   return q;
 }
 
+// Small per-call metadata (lengths, budgets) to the device without a host
+// synchronisation: staged in pinned memory from torch's caching host
+// allocator, which keeps the buffer until the copy on the current stream has
+// run, then copied asynchronously.
+at::Tensor to_device_async(const std::vector<int32_t>& host, const at::Device& dev) {
+  at::Tensor pinned = at::empty({static_cast<int64_t>(host.size())},
+                                at::TensorOptions().dtype(at::kInt).pinned_memory(true));
+  std::copy(host.begin(), host.end(), pinned.data_ptr<int32_t>());
+  return pinned.to(dev, /*non_blocking=*/true);
+}
+
 hipStream_t current_stream(const at::Tensor& t) {
   return c10::hip::getCurrentHIPStream(t.device().index()).stream();
 }
@@ -175,20 +186,106 @@ std::tuple<at::Tensor, at::Tensor, at::Tensor> decode_ragged(at::Tensor q_h, at:
     host[b] = static_cast<int32_t>(lens[b]);
     total += (lens[b] + p.bn - 1) / p.bn;
   }
-  at::Tensor dlens = at::from_blob(host.data(), {static_cast<int64_t>(host.size())},
-                                   at::TensorOptions().dtype(at::kInt)).to(q.device());
+  at::Tensor dlens = to_device_async(host, q.device());
   auto optsF = q.options().dtype(at::kFloat);
   auto optsI = q.options().dtype(at::kInt);
   at::Tensor out = at::empty({in.B, in.H, in.D}, q.options());
   at::Tensor m_star = at::empty({in.B, in.H}, optsF);
   at::Tensor vrows = want_vrows ? at::empty({in.B, in.KVH}, optsI) : at::empty({0}, optsI);
-  const size_t ws_bytes = santa_flash_ragged_workspace_size(in.B, in.H, in.KVH, in.D, total);
+  const size_t ws_bytes = santa_flash_ragged_workspace_size(in.B, in.H, in.KVH, in.D, p.T_c, total);
   at::Tensor ws = at::empty({static_cast<int64_t>(ws_bytes)}, q.options().dtype(at::kByte));
   const int rc = santa_flash_decode_ragged(q.data_ptr(), K_g.data_ptr(), V_g.data_ptr(), p.dtype, in.B, in.H, in.KVH,
                                            in.D, in.L_storage, dlens.data_ptr<int>(), static_cast<int>(max_len), total,
                                            p.bn, S, seed, out.data_ptr(), m_star.data_ptr<float>(),
                                            want_vrows ? vrows.data_ptr<int>() : nullptr, ws.data_ptr(), ws_bytes,
                                            current_stream(q));
+  TORCH_CHECK(rc == SANTA_OK, santa_last_error());
+  return std::make_tuple(out, m_star, vrows);
+}
+
+// Paged KV (an addition over the reference, whose caches are contiguous NHD,
+// README.md:257): K_pages / V_pages [num_pages, page_size, KVH, D], block_table
+// int32 [B, table_stride] on the device, seq_lens an int or one length per
+// sequence.  Token n of sequence b is row n % page_size of page
+// block_table[b, n / page_size].  block_n is planned from the longest
+// sequence (or given) as in the ragged call, whose results this call
+// reproduces bit for bit on the same tokens stored contiguously.
+std::tuple<at::Tensor, at::Tensor, at::Tensor> decode_paged(at::Tensor q_h, at::Tensor K_pages, at::Tensor V_pages,
+                                                            at::Tensor block_table, py::object seq_lens, int64_t S,
+                                                            uint64_t seed, int64_t block_n, bool want_vrows) {
+  TORCH_CHECK(q_h.is_cuda(), "q_h must be CUDA");
+  TORCH_CHECK(K_pages.is_cuda() && V_pages.is_cuda(), "K_pages and V_pages must be CUDA");
+  TORCH_CHECK(block_table.is_cuda(), "block_table must be CUDA");
+  TORCH_CHECK((q_h.scalar_type() == at::kBFloat16 || q_h.scalar_type() == at::kHalf), "q_h must be bf16 or f16");
+  TORCH_CHECK(K_pages.scalar_type() == q_h.scalar_type() && V_pages.scalar_type() == q_h.scalar_type(),
+              "q_h dtype must match K_pages/V_pages dtype");
+  TORCH_CHECK(q_h.device() == K_pages.device() && q_h.device() == V_pages.device() &&
+                  q_h.device() == block_table.device(),
+              "device mismatch");
+  TORCH_CHECK(q_h.dim() == 3 && K_pages.dim() == 4 && V_pages.dim() == 4,
+              "Paged path expects q_h [B,H,D], K_pages/V_pages [num_pages,page_size,KVH,D]");
+  TORCH_CHECK(K_pages.sizes() == V_pages.sizes(), "K_pages and V_pages must have the same shape");
+  TORCH_CHECK(K_pages.is_contiguous() && V_pages.is_contiguous(), "K_pages/V_pages must be contiguous");
+  TORCH_CHECK(block_table.scalar_type() == at::kInt && block_table.dim() == 2 && block_table.is_contiguous(),
+              "block_table must be a contiguous int32 [B, pages_per_sequence] tensor");
+  const int B = static_cast<int>(q_h.size(0)), H = static_cast<int>(q_h.size(1)), D = static_cast<int>(q_h.size(2));
+  const int num_pages = static_cast<int>(K_pages.size(0)), page_size = static_cast<int>(K_pages.size(1));
+  const int KVH = static_cast<int>(K_pages.size(2));
+  TORCH_CHECK(q_h.size(2) == K_pages.size(3), "D mismatch (q_h.size(2) vs K_pages.size(3))");
+  TORCH_CHECK(block_table.size(0) == B, "block_table must have one row per sequence (", B, ")");
+  const int stride = static_cast<int>(block_table.size(1));
+  const long long capacity = static_cast<long long>(stride) * page_size;
+  std::vector<int64_t> lens;
+  if (py::isinstance<py::int_>(seq_lens)) {
+    lens.assign(static_cast<size_t>(B), seq_lens.cast<int64_t>());
+  } else if (THPVariable_Check(seq_lens.ptr())) {
+    const at::Tensor t = seq_lens.cast<at::Tensor>().to(at::kCPU).to(at::kLong).contiguous();
+    TORCH_CHECK(t.dim() == 1, "seq_lens must be an int or a 1-D list of per-sequence lengths");
+    lens.assign(t.data_ptr<int64_t>(), t.data_ptr<int64_t>() + t.numel());
+  } else {
+    lens = seq_lens.cast<std::vector<int64_t>>();
+  }
+  TORCH_CHECK(static_cast<int64_t>(lens.size()) == B, "seq_lens must be an int or have one entry per sequence (", B,
+              ")");
+  int64_t max_len = 0;
+  for (const int64_t l : lens) {
+    TORCH_CHECK(l > 0, "valid_len must be > 0; got ", l);
+    TORCH_CHECK(l <= capacity, "seq_lens exceeds the block table's capacity: ", l, " > ", capacity);
+    max_len = std::max(max_len, l);
+  }
+  TORCH_CHECK(D == 128, "This build supports only D=128. Got D=", D);
+  TORCH_CHECK(KVH > 0 && H % KVH == 0, "H must be divisible by KVH. Got H=", H, " KVH=", KVH);
+  const int GH = H / KVH;
+  TORCH_CHECK(GH == 4 || GH == 8, "This build supports only GH=4 or GH=8 (H/KVH). Got GH=", GH, " (H=", H,
+              " KVH=", KVH, ")");
+  int L = 0, bn = 0, T_c = 0, S_pt = 0;
+  int rc = santa_flash_plan(max_len, max_len, block_n, S, &L, &bn, &T_c, &S_pt);
+  TORCH_CHECK(rc == SANTA_OK, santa_last_error());
+  TORCH_CHECK(reinterpret_cast<uintptr_t>(K_pages.data_ptr()) % 16 == 0 &&
+                  reinterpret_cast<uintptr_t>(V_pages.data_ptr()) % 16 == 0,
+              "K_pages/V_pages storage must be 16-byte aligned");
+  c10::DeviceGuard guard(q_h.device());
+  const at::Tensor q = aligned_q(q_h);
+  long long total = 0;
+  std::vector<int32_t> host(lens.size());
+  for (size_t b = 0; b < lens.size(); ++b) {
+    host[b] = static_cast<int32_t>(lens[b]);
+    total += (lens[b] + bn - 1) / bn;
+  }
+  at::Tensor dlens = to_device_async(host, q.device());
+  auto optsF = q.options().dtype(at::kFloat);
+  auto optsI = q.options().dtype(at::kInt);
+  at::Tensor out = at::empty({B, H, D}, q.options());
+  at::Tensor m_star = at::empty({B, H}, optsF);
+  at::Tensor vrows = want_vrows ? at::empty({B, KVH}, optsI) : at::empty({0}, optsI);
+  const size_t ws_bytes = santa_flash_ragged_workspace_size(B, H, KVH, D, T_c, total);
+  at::Tensor ws = at::empty({static_cast<int64_t>(ws_bytes)}, q.options().dtype(at::kByte));
+  const int dtype = (q.scalar_type() == at::kBFloat16) ? SANTA_BF16 : SANTA_F16;
+  rc = santa_flash_decode_paged(q.data_ptr(), K_pages.data_ptr(), V_pages.data_ptr(), dtype, B, H, KVH, D, num_pages,
+                                page_size, block_table.data_ptr<int>(), stride, dlens.data_ptr<int>(),
+                                static_cast<int>(max_len), total, bn, S, seed, out.data_ptr(),
+                                m_star.data_ptr<float>(), want_vrows ? vrows.data_ptr<int>() : nullptr, ws.data_ptr(),
+                                ws_bytes, current_stream(q));
   TORCH_CHECK(rc == SANTA_OK, santa_last_error());
   return std::make_tuple(out, m_star, vrows);
 }
@@ -315,6 +412,9 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
   m.def("decode_systematic_batched", &decode_systematic_scalar, py::arg("q_h"), py::arg("K_g"), py::arg("V_g"),
         py::arg("S"), py::arg("seed") = 42ULL, py::arg("block_n") = 0, py::arg("want_vrows") = false,
         py::arg("valid_len") = py::int_(-1));
+  m.def("decode_systematic_paged", &decode_paged, py::arg("q_h"), py::arg("K_pages"), py::arg("V_pages"),
+        py::arg("block_table"), py::arg("seq_lens"), py::arg("S"), py::arg("seed") = 42ULL, py::arg("block_n") = 0,
+        py::arg("want_vrows") = false);
   m.def("_debug_tiles", &debug_tiles, py::arg("q_h"), py::arg("K_g"), py::arg("V_g"), py::arg("S"),
         py::arg("seed") = 42ULL, py::arg("block_n") = 0, py::arg("valid_len") = -1);
   m.def("_debug_wave", &debug_wave, py::arg("q_h"), py::arg("K_g"), py::arg("V_g"), py::arg("S"),

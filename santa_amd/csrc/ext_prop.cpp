@@ -62,6 +62,17 @@ at::Tensor aligned_q(const at::Tensor& q_h) {
   return q;
 }
 
+// Small per-call metadata (lengths, budgets) to the device without a host
+// synchronisation: staged in pinned memory from torch's caching host
+// allocator, which keeps the buffer until the copy on the current stream has
+// run, then copied asynchronously.
+at::Tensor to_device_async(const std::vector<int32_t>& host, const at::Device& dev) {
+  at::Tensor pinned = at::empty({static_cast<int64_t>(host.size())},
+                                at::TensorOptions().dtype(at::kInt).pinned_memory(true));
+  std::copy(host.begin(), host.end(), pinned.data_ptr<int32_t>());
+  return pinned.to(dev, /*non_blocking=*/true);
+}
+
 hipStream_t current_stream(const at::Tensor& t) {
   return c10::hip::getCurrentHIPStream(t.device().index()).stream();
 }
@@ -205,7 +216,7 @@ std::tuple<at::Tensor, at::Tensor, at::Tensor> decode_batched(at::Tensor q_h, at
       host[b] = static_cast<int32_t>(lens[b]);
       host[B + b] = static_cast<int32_t>(Ss[b]);
     }
-    at::Tensor meta = at::from_blob(host.data(), {2 * B}, at::TensorOptions().dtype(at::kInt)).to(q.device());
+    at::Tensor meta = to_device_async(host, q.device());
     const size_t ws_bytes = santa_prop_batched_workspace_size(B, H, KVH, D, L_st, max_tiles, total);
     at::Tensor ws = at::empty({static_cast<int64_t>(ws_bytes)}, q.options().dtype(at::kByte));
     const int rc = santa_prop_decode_batched(q.data_ptr(), K_g.data_ptr(), V_g.data_ptr(), dtype, B, H, KVH, D, L_st,
@@ -234,6 +245,99 @@ std::tuple<at::Tensor, at::Tensor, at::Tensor> decode_batched(at::Tensor q_h, at
   return std::make_tuple(out, m_star, vrows);
 }
 
+// Paged santa_prop (an addition over the reference, whose caches are
+// contiguous NHD, README.md:257): K_pages / V_pages [num_pages, page_size,
+// KVH, D], block_table int32 [B, table_stride] on the device; seq_lens and S
+// are ints or per-sequence lists / tensors.  Sequence b is decoded exactly as
+// decode_systematic_scalar on its seq_lens[b] tokens stored contiguously.
+std::tuple<at::Tensor, at::Tensor, at::Tensor> decode_paged(at::Tensor q_h, at::Tensor K_pages, at::Tensor V_pages,
+                                                            at::Tensor block_table, py::object seq_lens, py::object S,
+                                                            uint64_t seed, int64_t block_n, bool want_vrows) {
+  TORCH_CHECK(q_h.is_cuda(), "q_h must be CUDA");
+  TORCH_CHECK(K_pages.is_cuda() && V_pages.is_cuda(), "K_pages and V_pages must be CUDA");
+  TORCH_CHECK(block_table.is_cuda(), "block_table must be CUDA");
+  TORCH_CHECK((q_h.scalar_type() == at::kBFloat16 || q_h.scalar_type() == at::kHalf), "q_h must be bf16 or f16");
+  TORCH_CHECK(K_pages.scalar_type() == q_h.scalar_type() && V_pages.scalar_type() == q_h.scalar_type(),
+              "q_h dtype must match K_pages/V_pages");
+  TORCH_CHECK(q_h.device() == K_pages.device() && q_h.device() == V_pages.device() &&
+                  q_h.device() == block_table.device(),
+              "device mismatch");
+  TORCH_CHECK(q_h.dim() == 3 && K_pages.dim() == 4 && V_pages.dim() == 4,
+              "Paged path expects q_h [B,H,D], K_pages/V_pages [num_pages,page_size,KVH,D]");
+  TORCH_CHECK(K_pages.sizes() == V_pages.sizes(), "K_pages and V_pages must have the same shape");
+  TORCH_CHECK(K_pages.is_contiguous() && V_pages.is_contiguous(), "K_pages/V_pages must be contiguous");
+  TORCH_CHECK(block_table.scalar_type() == at::kInt && block_table.dim() == 2 && block_table.is_contiguous(),
+              "block_table must be a contiguous int32 [B, pages_per_sequence] tensor");
+  TORCH_CHECK(q_h.size(2) == K_pages.size(3), "D mismatch (q_h.size(2) vs K_pages.size(3))");
+  TORCH_CHECK(K_pages.size(2) > 0 && q_h.size(1) % K_pages.size(2) == 0,
+              "H must be divisible by KVH (expected KVH == K_pages.size(2) for NHD)");
+  const int B = static_cast<int>(q_h.size(0)), H = static_cast<int>(q_h.size(1)), D = static_cast<int>(q_h.size(2));
+  const int num_pages = static_cast<int>(K_pages.size(0)), page_size = static_cast<int>(K_pages.size(1));
+  const int KVH = static_cast<int>(K_pages.size(2));
+  TORCH_CHECK(block_table.size(0) == B, "block_table must have one row per sequence (", B, ")");
+  const int stride = static_cast<int>(block_table.size(1));
+  const long long capacity = static_cast<long long>(stride) * page_size;
+  const std::vector<int64_t> Ss = per_sequence(S, B, "S");
+  const std::vector<int64_t> lens = per_sequence(seq_lens, B, "seq_lens");
+  const char* env = std::getenv("SANTA_PASS1");
+  std::vector<int> bn(B), tc(B), path(B);
+  for (int b = 0; b < B; ++b) {
+    TORCH_CHECK(lens[b] > 0, "seq_lens must be > 0; got ", lens[b]);
+    TORCH_CHECK(lens[b] <= capacity, "seq_lens exceeds the block table's capacity: ", lens[b], " > ", capacity);
+    const int rc = santa_prop_plan(static_cast<int>(lens[b]), H, KVH, D, block_n, env, &bn[b], &tc[b], &path[b]);
+    TORCH_CHECK(rc == SANTA_OK, santa_last_error());
+  }
+  c10::DeviceGuard guard(q_h.device());
+  const at::Tensor q = aligned_q(q_h);
+  const int dtype = (q.scalar_type() == at::kBFloat16) ? SANTA_BF16 : SANTA_F16;
+  TORCH_CHECK(reinterpret_cast<uintptr_t>(K_pages.data_ptr()) % 16 == 0 &&
+                  reinterpret_cast<uintptr_t>(V_pages.data_ptr()) % 4 == 0,
+              "K_pages/V_pages storage must be 16-byte aligned");
+  auto optsF = q.options().dtype(at::kFloat);
+  auto optsI = q.options().dtype(at::kInt);
+  at::Tensor out = at::empty({B, H, D}, q.options());
+  at::Tensor m_star = at::empty({B, H}, optsF);
+  at::Tensor vrows = want_vrows ? at::empty({B, KVH}, optsI) : at::empty({0}, optsI);
+  hipStream_t st = current_stream(q);
+  std::vector<int32_t> host(2 * static_cast<size_t>(B));
+  for (int b = 0; b < B; ++b) {
+    host[b] = static_cast<int32_t>(lens[b]);
+    host[B + b] = static_cast<int32_t>(Ss[b]);
+  }
+  at::Tensor meta = to_device_async(host, q.device());
+  // one launch sequence over [b0, b1) with a common block size and pass-1 path
+  auto launch = [&](int b0, int b1) {
+    const int nb = b1 - b0;
+    long long total = 0;
+    int max_len = 0, max_tiles = 0;
+    for (int b = b0; b < b1; ++b) {
+      total += tc[b];
+      max_len = std::max(max_len, static_cast<int>(lens[b]));
+      max_tiles = std::max(max_tiles, tc[b]);
+    }
+    const size_t ws_bytes = santa_prop_batched_workspace_size(nb, H, KVH, D, max_len, max_tiles, total);
+    at::Tensor ws = at::empty({static_cast<int64_t>(ws_bytes)}, q.options().dtype(at::kByte));
+    const int rc = santa_prop_decode_paged(
+        static_cast<const char*>(q.data_ptr()) + static_cast<size_t>(b0) * H * D * q.element_size(), K_pages.data_ptr(),
+        V_pages.data_ptr(), dtype, nb, H, KVH, D, num_pages, page_size,
+        block_table.data_ptr<int>() + static_cast<size_t>(b0) * stride, stride, meta.data_ptr<int>() + b0,
+        meta.data_ptr<int>() + B + b0, max_len, total, bn[b0], path[b0], seed,
+        static_cast<char*>(out.data_ptr()) + static_cast<size_t>(b0) * H * D * out.element_size(),
+        m_star.data_ptr<float>() + static_cast<size_t>(b0) * H,
+        want_vrows ? vrows.data_ptr<int>() + static_cast<size_t>(b0) * KVH : nullptr, ws.data_ptr(), ws_bytes, st);
+    TORCH_CHECK(rc == SANTA_OK, santa_last_error());
+  };
+  bool uniform = true;
+  for (int b = 1; b < B; ++b) uniform = uniform && bn[b] == bn[0] && path[b] == path[0];
+  if (uniform) {
+    launch(0, B);
+  } else {
+    // sequences on different block sizes / pass-1 paths: one launch sequence each
+    for (int b = 0; b < B; ++b) launch(b, b + 1);
+  }
+  return std::make_tuple(out, m_star, vrows);
+}
+
 }  // namespace
 
 PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
@@ -243,6 +347,9 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
   m.def("decode_systematic_batched", &decode_batched, py::arg("q_h"), py::arg("K_g"), py::arg("V_g"), py::arg("S"),
         py::arg("seed") = 42ULL, py::arg("block_n") = 0, py::arg("want_vrows") = false,
         py::arg("valid_len") = py::int_(-1));
+  m.def("decode_systematic_paged", &decode_paged, py::arg("q_h"), py::arg("K_pages"), py::arg("V_pages"),
+        py::arg("block_table"), py::arg("seq_lens"), py::arg("S"), py::arg("seed") = 42ULL, py::arg("block_n") = 0,
+        py::arg("want_vrows") = false);
   m.def("_debug_pass", &debug_pass, py::arg("q_h"), py::arg("K_g"), py::arg("V_g"), py::arg("S"),
         py::arg("seed") = 42ULL, py::arg("block_n") = 0);
   m.def("_library_version", []() { return std::string(santa_version()); });

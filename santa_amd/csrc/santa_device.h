@@ -11,6 +11,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "santa_internal.h"  // PageTable
+
 namespace santa {
 
 // ---------------------------------------------------------------- 16-bit I/O
@@ -213,6 +215,33 @@ __device__ __forceinline__ GridPos grid_pos(int wg, const int* seq_lens, int B, 
     base += n;
   }
   return p;
+}
+
+// ---------------------------------------------------------------- paged KV
+// Paged caches (PageTable): page ids are clamped to [0, num_pages), so a
+// malformed table gives wrong numbers, never an access outside the pool.
+
+// The pages of rows [n0, n0 + rows) of sequence b that lie below len, one per
+// lane: lane i holds the page of row block (n0 >> shift) + i; lanes past the
+// last such page (all lanes when n0 >= len) hold page 0.
+__device__ __forceinline__ int pages_of_rows(const PageTable& pt, int b, int n0, int rows, int len, int lane) {
+  const int last = min(n0 + rows, len) - 1;
+  const int p0 = n0 >> pt.shift;
+  const int np = (last >= n0) ? (last >> pt.shift) - p0 + 1 : 0;
+  int v = 0;
+  if (lane < np) v = pt.table[static_cast<size_t>(b) * pt.stride + p0 + lane];
+  return min(max(v, 0), pt.num_pages - 1);
+}
+
+// Per lane: the page of token `row` of sequence b (page 0 where !ok).
+__device__ __forceinline__ int page_of_row(const PageTable& pt, int b, int row, bool ok) {
+  const int v = ok ? pt.table[static_cast<size_t>(b) * pt.stride + (row >> pt.shift)] : 0;
+  return min(max(v, 0), pt.num_pages - 1);
+}
+
+// Byte offset from the pool base of token n, which lies in page `page`.
+__device__ __forceinline__ size_t paged_row(const PageTable& pt, int page, int n, uint32_t row_bytes) {
+  return ((static_cast<size_t>(page) << pt.shift) + static_cast<size_t>(n & ((1 << pt.shift) - 1))) * row_bytes;
 }
 
 // ---------------------------------------------------------------- DPP

@@ -191,15 +191,16 @@ __device__ __forceinline__ float tile_max_of(const int* s_wmax, int g) {
   return from_order_key(max(max(s_wmax[g], s_wmax[GH + g]), max(s_wmax[2 * GH + g], s_wmax[3 * GH + g])));
 }
 
-template <bool BF16, int GH, int BN, int MODE>
+template <bool BF16, int GH, int BN, int MODE, bool PAGED = false>
 __global__ __launch_bounds__(kThreads, 2) void tile_kernel(
     const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K, const uint16_t* __restrict__ V, int H, int KVH,
     int L_valid, int L_storage, int T_c, int cs, int cpg, float q_scale, int S_pt, uint64_t seed,
     float* __restrict__ m_tiles, float* __restrict__ ell_tiles, float* __restrict__ out_tiles,
     int* __restrict__ emit_cnt, int16_t* __restrict__ dbg_counts, float* __restrict__ part,
     int* __restrict__ part_emit, uint16_t* __restrict__ u_stash, const int* __restrict__ seq_lens, int B,
-    long long S_total) {
+    long long S_total, PageTable pt) {
   static_assert(BN == 32 || BN == 64 || BN == 256, "block_n");
+  static_assert(!PAGED || MODE != kPerTile, "the reference-structured per-tile mode reads contiguous caches only");
   static_assert(GH == 4 || GH == 8, "group size");
   constexpr int NT_REF = (BN == 256) ? 256 : 128;  // reference block size (launchers :521,:559)
   constexpr int NW_REF = NT_REF / 32;
@@ -242,12 +243,12 @@ __global__ __launch_bounds__(kThreads, 2) void tile_kernel(
 
   // Addresses: a wave-uniform 64-bit base (SGPRs) plus a 32-bit per-lane byte
   // offset, so loads take the scalar-base form and need no 64-bit VALU math.
+  // Paged: the base is the pool's (plus this KV head), rows go through pt.
   const size_t row_stride = static_cast<size_t>(KVH) * kD;
   const uint32_t row_bytes = static_cast<uint32_t>(KVH) * kD * 2u;
-  const char* Kg = reinterpret_cast<const char*>(K + static_cast<size_t>(b) * L_storage * row_stride +
-                                                 static_cast<size_t>(kv) * kD);
-  const char* Vg = reinterpret_cast<const char*>(V + static_cast<size_t>(b) * L_storage * row_stride +
-                                                 static_cast<size_t>(kv) * kD);
+  const size_t seq_off = PAGED ? 0 : static_cast<size_t>(b) * L_storage * row_stride;
+  const char* Kg = reinterpret_cast<const char*>(K + seq_off + static_cast<size_t>(kv) * kD);
+  const char* Vg = reinterpret_cast<const char*>(V + seq_off + static_cast<size_t>(kv) * kD);
   const uint32_t v_lane_off = 4u * static_cast<uint32_t>(lane);  // dims 2*lane, 2*lane+1
 
   // Online-merge state: per head owned by this wave, running max M, mass Z
@@ -326,6 +327,7 @@ __global__ __launch_bounds__(kThreads, 2) void tile_kernel(
       const bool ok = i < lcnt[k];
       const int rowv = ok ? s_lrow[g * LCAP + i] : 0;
       const float coefv = ok ? s_lcw[g * LCAP + i] * santa_expf(s_lm[g * LCAP + i] - Mf) : 0.0f;
+      const int pgv = PAGED ? page_of_row(pt, b, rowv, ok) : 0;
       const int nb = min(64, lcnt[k] - base);
       for (int q0 = 0; q0 < nb; q0 += 16) {
         float coef[16];
@@ -335,7 +337,9 @@ __global__ __launch_bounds__(kThreads, 2) void tile_kernel(
           const int j = min(q0 + q, nb - 1);
           const int row = __builtin_amdgcn_readlane(rowv, j);
           coef[q] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(coefv), j));
-          vw[q] = *reinterpret_cast<const uint32_t*>(Vg + static_cast<size_t>(row) * row_bytes + v_lane_off);
+          const size_t off = PAGED ? paged_row(pt, __builtin_amdgcn_readlane(pgv, j), row, row_bytes)
+                                   : static_cast<size_t>(row) * row_bytes;
+          vw[q] = *reinterpret_cast<const uint32_t*>(Vg + off + v_lane_off);
         }
 #pragma unroll
         for (int q = 0; q < 16; ++q) {
@@ -357,9 +361,11 @@ __global__ __launch_bounds__(kThreads, 2) void tile_kernel(
   // so one unconditional call site covers short tiles, waves without rows and
   // the missing successor of a chunk's last tile (no branches, so the loaded
   // registers are never copied and no wait lands before the scores).
+  // Paged: pv holds the pages of the wave's 64 rows of the tile (one per
+  // lane), loaded a tile ahead; a 4-row group never straddles two pages.
   u32x4 kw[16];
   const int k_lane_off = static_cast<int>((lane >> 4) * row_bytes + 16u * (lane & 15));
-  auto load_k = [&](int t) {
+  auto load_k = [&](int t, int pv) {
     const int n0 = t * BN;
     const int len = (t < t_end) ? min(BN, L_valid - n0) : 0;
     const char* kt = Kg + static_cast<size_t>(n0 + 64 * wave) * row_bytes;
@@ -367,13 +373,24 @@ __global__ __launch_bounds__(kThreads, 2) void tile_kernel(
     for (int c = 0; c < 16; ++c) {
       // wave-uniform; readfirstlane keeps the descriptor in SGPRs
       const int nvalid = __builtin_amdgcn_readfirstlane(min(max(len - 64 * wave - 4 * c, 0), 4));
+      const char* gb;
+      if constexpr (PAGED) {
+        const int n = n0 + 64 * wave + 4 * c;
+        const int page = __builtin_amdgcn_readlane(pv, (n >> pt.shift) - ((n0 + 64 * wave) >> pt.shift));
+        gb = Kg + paged_row(pt, page, n, row_bytes);
+      } else {
+        gb = kt + static_cast<size_t>(4 * c) * row_bytes;
+      }
       const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
-          const_cast<char*>(kt + static_cast<size_t>(4 * c) * row_bytes), static_cast<short>(0),
-          nvalid * static_cast<int>(row_bytes), kBufferWord3);
+          const_cast<char*>(gb), static_cast<short>(0), nvalid * static_cast<int>(row_bytes), kBufferWord3);
       kw[c] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rs, k_lane_off, 0, kBufferNontemporal));
     }
   };
-  load_k(t_begin);
+  auto wave_pages = [&](int t) -> int {
+    return PAGED ? pages_of_rows(pt, b, t * BN + 64 * wave, 64, L_valid, lane) : 0;
+  };
+  load_k(t_begin, wave_pages(t_begin));
+  int pv_next = wave_pages(t_begin + 1);
 
   for (int t = t_begin; t < t_end; ++t) {
     const int n0 = t * BN;
@@ -392,7 +409,8 @@ __global__ __launch_bounds__(kThreads, 2) void tile_kernel(
       }
     }
     // the next tile's rows stream in through this tile's scores and tail
-    load_k(t + 1);
+    load_k(t + 1, pv_next);
+    if constexpr (PAGED) pv_next = wave_pages(t + 2);
     // LDS operations of one wave complete in order; the barrier only keeps
     // the compiler from moving the reads above the writes
     __builtin_amdgcn_wave_barrier();
@@ -744,13 +762,13 @@ __device__ __forceinline__ float wave_ell(const float (&u)[2][2]) {
 // P1: santa_prop pass 1 with the vec path's numerics (the flash tile
 // statistics): per tile and head m and ell into dbg_m / dbg_ell ([B, H, T_c])
 // and the 16-bit u into u_stash ([B, L_storage, H]); no sampling, no partials.
-template <bool BF16, int GH, bool DBG, bool P1 = false>
+template <bool BF16, int GH, bool DBG, bool P1 = false, bool PAGED = false>
 __global__ __launch_bounds__(kThreads, 2) void wave_kernel(
     const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K, const uint16_t* __restrict__ V, int H, int KVH,
     int L_valid, int L_storage, int T_c, int cs, int cpg, float q_scale, int S_pt, uint64_t seed,
     float* __restrict__ part, int* __restrict__ part_emit, const int* __restrict__ seq_lens, int B, long long S_total,
     float* __restrict__ dbg_m, float* __restrict__ dbg_ell, int16_t* __restrict__ dbg_counts,
-    uint16_t* __restrict__ u_stash = nullptr, int stash_ld = 0) {
+    uint16_t* __restrict__ u_stash, int stash_ld, PageTable pt) {
   constexpr int BN = 256;
   constexpr int NHB = GH / 4;
   constexpr int LCAP = kWaveListCap;
@@ -778,12 +796,12 @@ __global__ __launch_bounds__(kThreads, 2) void wave_kernel(
   int* const lrow = s_lrow + wave * GH * LCAP;
   float* const lcw = s_lcw + wave * GH * LCAP;
 
+  // Paged: the base is the pool's (plus this KV head), rows go through pt.
   const size_t row_stride = static_cast<size_t>(KVH) * kD;
   const uint32_t row_bytes = static_cast<uint32_t>(KVH) * kD * 2u;
-  const char* Kg = reinterpret_cast<const char*>(K + static_cast<size_t>(b) * L_storage * row_stride +
-                                                 static_cast<size_t>(kv) * kD);
-  const char* Vg = reinterpret_cast<const char*>(V + static_cast<size_t>(b) * L_storage * row_stride +
-                                                 static_cast<size_t>(kv) * kD);
+  const size_t seq_off = PAGED ? 0 : static_cast<size_t>(b) * L_storage * row_stride;
+  const char* Kg = reinterpret_cast<const char*>(K + seq_off + static_cast<size_t>(kv) * kD);
+  const char* Vg = reinterpret_cast<const char*>(V + seq_off + static_cast<size_t>(kv) * kD);
   const uint32_t v_lane_off = 4u * static_cast<uint32_t>(lane);
 
   float qa[NHB][8];
@@ -812,6 +830,7 @@ __global__ __launch_bounds__(kThreads, 2) void wave_kernel(
     if (n == 0) return;
     const int rowv = (lane < n) ? lrow[g * LCAP + lane] : 0;
     const float coefv = (lane < n) ? lcw[g * LCAP + lane] : 0.0f;
+    const int pgv = PAGED ? page_of_row(pt, b, rowv, lane < n) : 0;
     for (int q0 = 0; q0 < n; q0 += 16) {
       float coef[16];
       uint32_t vw[16];
@@ -820,7 +839,9 @@ __global__ __launch_bounds__(kThreads, 2) void wave_kernel(
         const int j = min(q0 + q, n - 1);
         const int row = __builtin_amdgcn_readlane(rowv, j);
         coef[q] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(coefv), j));
-        vw[q] = *reinterpret_cast<const uint32_t*>(Vg + static_cast<size_t>(row) * row_bytes + v_lane_off);
+        const size_t off = PAGED ? paged_row(pt, __builtin_amdgcn_readlane(pgv, j), row, row_bytes)
+                                 : static_cast<size_t>(row) * row_bytes;
+        vw[q] = *reinterpret_cast<const uint32_t*>(Vg + off + v_lane_off);
       }
 #pragma unroll
       for (int q = 0; q < 16; ++q) {
@@ -835,10 +856,24 @@ __global__ __launch_bounds__(kThreads, 2) void wave_kernel(
 
   // Sub-block sb = 2 hh + e of tile t: 16 loads of 4 rows (stride 2), one
   // descriptor each; rows at or past the tile's end (and every row of a tile
-  // at or past t_end) read as zero and cost no traffic.
+  // at or past t_end) read as zero and cost no traffic.  A load's rows lie in
+  // one 8-row aligned block, so in a paged cache in one page: pv holds the
+  // tile's pages, one per lane.
   u32x4 kw[16];
   const int k_lane_off = static_cast<int>((lane >> 4) * 2u * row_bytes + 16u * (lane & 15));
-  auto load_k = [&](int t, int sb) {
+  auto group_base = [&](int t, int r, int pv) -> const char* {  // row t*BN + r, first of its load group
+    const int n = t * BN + r;
+    if constexpr (PAGED) {
+      const int page = __builtin_amdgcn_readlane(pv, (n >> pt.shift) - ((t * BN) >> pt.shift));
+      return Kg + paged_row(pt, page, n, row_bytes);
+    } else {
+      return Kg + static_cast<size_t>(n) * row_bytes;
+    }
+  };
+  auto tile_pages = [&](int t) -> int {
+    return PAGED ? pages_of_rows(pt, b, t * BN, BN, L_valid, lane) : 0;
+  };
+  auto load_k = [&](int t, int sb, int pv) {
     const uint32_t rb = row_bytes;
     const int len = (t < t_end) ? min(BN, L_valid - t * BN) : 0;
     const int r0 = 128 * (sb >> 1) + (sb & 1);
@@ -847,9 +882,9 @@ __global__ __launch_bounds__(kThreads, 2) void wave_kernel(
     for (int c = 0; c < 16; ++c) {
       // wave-uniform; readfirstlane keeps the descriptor in SGPRs
       const int nvalid = __builtin_amdgcn_readfirstlane(min(max(len - r0 - 8 * c, 0), 8));
+      const char* gb = PAGED ? group_base(t, r0 + 8 * c, pv) : kt + static_cast<size_t>(8 * c) * rb;
       const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
-          const_cast<char*>(kt + static_cast<size_t>(8 * c) * rb), static_cast<short>(0),
-          nvalid * static_cast<int>(rb), kBufferWord3);
+          const_cast<char*>(gb), static_cast<short>(0), nvalid * static_cast<int>(rb), kBufferWord3);
       kw[c] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rs, k_lane_off, 0, kBufferNontemporal));
     }
   };
@@ -863,22 +898,26 @@ __global__ __launch_bounds__(kThreads, 2) void wave_kernel(
 #pragma unroll
   for (int m = 0; m < 4; ++m)
     k_dma_off[m] = (lane >> 4) * 2u * row_bytes + 16u * static_cast<uint32_t>((lane & 15) ^ (4 * m + (lane >> 4)));
-  auto dma_k = [&](int t) {
+  auto dma_k = [&](int t, int pv) {
     const uint32_t rb = row_bytes;
     const int len = min(BN, L_valid - t * BN);
     const char* kt = Kg + static_cast<size_t>(t * BN) * rb;
 #pragma unroll
     for (int c = 0; c < 16; ++c) {
       const int nvalid = __builtin_amdgcn_readfirstlane(min(max(len - 8 * c, 0), 8));
+      const char* gb = PAGED ? group_base(t, 8 * c, pv) : kt + static_cast<size_t>(8 * c) * rb;
       const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
-          const_cast<char*>(kt + static_cast<size_t>(8 * c) * rb), static_cast<short>(0),
-          nvalid * static_cast<int>(rb), kBufferWord3);
+          const_cast<char*>(gb), static_cast<short>(0), nvalid * static_cast<int>(rb), kBufferWord3);
       __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (__attribute__((address_space(3))) void*)(wk + 64 * c), 16,
                                                k_dma_off[c & 3], 0, 0, kBufferNontemporal);
     }
   };
-  if (t_begin + wave < t_end) dma_k(t_begin + wave);
-  load_k(t_begin + wave, 1);
+  // pv: pages of the current tile; pv_next: of the wave's next tile (loaded
+  // while the current one is scored)
+  int pv = tile_pages(t_begin + wave);
+  int pv_next = 0;
+  if (t_begin + wave < t_end) dma_k(t_begin + wave, pv);
+  load_k(t_begin + wave, 1, pv);
 
   const int jrow = lane >> 4;
   const int qq = lane & 15;
@@ -899,6 +938,7 @@ __global__ __launch_bounds__(kThreads, 2) void wave_kernel(
         } else {
           asm volatile("s_waitcnt vmcnt(16)" ::: "memory");
         }
+        if constexpr (PAGED) pv_next = tile_pages(t + 4);
       } else {
 #pragma unroll
         for (int c = 0; c < 16; ++c) {
@@ -908,9 +948,9 @@ __global__ __launch_bounds__(kThreads, 2) void wave_kernel(
         // sub-blocks 2, 3, then the next tile's sub-block 1 (GH 4; GH 8 loads
         // it after the tail, whose registers would not fit beside it)
         if (sb < 3) {
-          load_k(t, sb + 1);
+          load_k(t, sb + 1, pv);
         } else if constexpr (GH == 4) {
-          load_k(t + 4, 1);
+          load_k(t + 4, 1, pv_next);
         }
       }
       __builtin_amdgcn_wave_barrier();
@@ -943,7 +983,7 @@ __global__ __launch_bounds__(kThreads, 2) void wave_kernel(
 
     // every row of the staging area has been read: the next tile's sub-block 0
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-    if (t + 4 < t_end) dma_k(t + 4);
+    if (t + 4 < t_end) dma_k(t + 4, pv_next);
 
     // ---- tile max per head (exact in any order) --------------------------------
     bool valid[2][2];
@@ -1120,7 +1160,8 @@ __global__ __launch_bounds__(kThreads, 2) void wave_kernel(
         }
     }
     emit_total += __popcll(uni[0][0]) + __popcll(uni[0][1]) + __popcll(uni[1][0]) + __popcll(uni[1][1]);
-    if constexpr (GH == 8) load_k(t + 4, 1);
+    if constexpr (GH == 8) load_k(t + 4, 1, pv_next);
+    pv = pv_next;
   }
   // no load to LDS outstanding past here (the staging area is reused below)
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
@@ -1334,20 +1375,32 @@ struct Args {
   const int* seq_lens;  // ragged form (prop pass 1, ragged flash) or nullptr
   int n_wg;             // grid size of the ragged form
   long long S_total;    // ragged flash: S, for each sequence's S_per_tile
+  PageTable pt;         // paged K/V (pt.table set) or contiguous
 };
 
-template <bool BF16, int GH, int BN, int MODE>
-static hipError_t launch_t(const Args& a, hipStream_t stream) {
+template <bool BF16, int GH, int BN, int MODE, bool PAGED>
+static hipError_t launch_tk(const Args& a, hipStream_t stream) {
   const float q_scale = 1.0f / sqrtf(static_cast<float>(kD));
   const unsigned grid = a.seq_lens ? static_cast<unsigned>(a.n_wg)
                                    : static_cast<unsigned>(a.B) * static_cast<unsigned>(a.KVH) * static_cast<unsigned>(a.cpg);
   if (grid == 0) return hipSuccess;
-  hipLaunchKernelGGL((tile_kernel<BF16, GH, BN, MODE>), dim3(grid), dim3(kThreads), 0, stream,
+  hipLaunchKernelGGL((tile_kernel<BF16, GH, BN, MODE, PAGED>), dim3(grid), dim3(kThreads), 0, stream,
                      static_cast<const uint16_t*>(a.q), static_cast<const uint16_t*>(a.K),
                      static_cast<const uint16_t*>(a.V), a.H, a.KVH, a.L_valid, a.L_storage, a.T_c, a.cs, a.cpg,
                      q_scale, a.S_pt, a.seed, a.m_tiles, a.ell_tiles, a.out_tiles, a.emit_cnt, a.counts, a.part,
-                     a.part_emit, a.u_stash, a.seq_lens, a.B, a.S_total);
+                     a.part_emit, a.u_stash, a.seq_lens, a.B, a.S_total, a.pt);
   return hipGetLastError();
+}
+
+// Paged caches go through the online mode at block_n 32/64 (block_n 256 is
+// the wave kernel's) and the general pass 1.
+template <bool BF16, int GH, int BN, int MODE>
+static hipError_t launch_t(const Args& a, hipStream_t stream) {
+  if (a.pt.table) {
+    if constexpr ((MODE == kOnline && BN != 256) || MODE == kPass1Gen) return launch_tk<BF16, GH, BN, MODE, true>(a, stream);
+    return hipErrorInvalidValue;
+  }
+  return launch_tk<BF16, GH, BN, MODE, false>(a, stream);
 }
 
 template <bool BF16, int GH, int MODE>
@@ -1369,18 +1422,26 @@ static hipError_t launch_wave_t(const Args& a, float* dbg_m, float* dbg_ell, int
   const unsigned grid = a.seq_lens ? static_cast<unsigned>(a.n_wg)
                                    : static_cast<unsigned>(a.B) * static_cast<unsigned>(a.KVH) * static_cast<unsigned>(a.cpg);
   if (grid == 0) return hipSuccess;
-  if (dbg_counts)
+  if (dbg_counts) {
+    if (a.pt.table) return hipErrorInvalidValue;  // the statistics check reads contiguous caches
     hipLaunchKernelGGL((wave_kernel<BF16, GH, true>), dim3(grid), dim3(kThreads), 0, stream,
                        static_cast<const uint16_t*>(a.q), static_cast<const uint16_t*>(a.K),
                        static_cast<const uint16_t*>(a.V), a.H, a.KVH, a.L_valid, a.L_storage, a.T_c, a.cs, a.cpg,
                        q_scale, a.S_pt, a.seed, a.part, a.part_emit, a.seq_lens, a.B, a.S_total, dbg_m, dbg_ell,
-                       dbg_counts);
-  else
+                       dbg_counts, nullptr, 0, a.pt);
+  } else if (a.pt.table) {
+    hipLaunchKernelGGL((wave_kernel<BF16, GH, false, false, true>), dim3(grid), dim3(kThreads), 0, stream,
+                       static_cast<const uint16_t*>(a.q), static_cast<const uint16_t*>(a.K),
+                       static_cast<const uint16_t*>(a.V), a.H, a.KVH, a.L_valid, a.L_storage, a.T_c, a.cs, a.cpg,
+                       q_scale, a.S_pt, a.seed, a.part, a.part_emit, a.seq_lens, a.B, a.S_total, nullptr,
+                       nullptr, nullptr, nullptr, 0, a.pt);
+  } else {
     hipLaunchKernelGGL((wave_kernel<BF16, GH, false>), dim3(grid), dim3(kThreads), 0, stream,
                        static_cast<const uint16_t*>(a.q), static_cast<const uint16_t*>(a.K),
                        static_cast<const uint16_t*>(a.V), a.H, a.KVH, a.L_valid, a.L_storage, a.T_c, a.cs, a.cpg,
                        q_scale, a.S_pt, a.seed, a.part, a.part_emit, a.seq_lens, a.B, a.S_total, nullptr,
-                       nullptr, nullptr);
+                       nullptr, nullptr, nullptr, 0, a.pt);
+  }
   return hipGetLastError();
 }
 
@@ -1473,9 +1534,11 @@ hipError_t launch_expf(const float* x, float* y, size_t n, hipStream_t stream) {
 // santa_prop pass 1 on the tile kernel (declared in santa_internal.h).
 hipError_t launch_prop_pass1(const void* q, const void* K, int dtype, int B, int H, int KVH, int L, int L_storage,
                              int block_n, int path, float* m_tiles, float* ell_tiles, uint16_t* u_stash,
-                             const int* seq_lens, int cs, int n_wg, int stash_ld, hipStream_t stream) {
+                             const int* seq_lens, int cs, int n_wg, int stash_ld, hipStream_t stream,
+                             PageTable pt) {
   Args a{q, K, nullptr, B, H, KVH, L, L_storage, (L + block_n - 1) / block_n, 0, 0, m_tiles, ell_tiles, nullptr,
          nullptr, nullptr, nullptr, nullptr, 0, 0, u_stash, seq_lens};
+  a.pt = pt;
   if (seq_lens) {
     // ragged: L is the longest sequence; n_wg workgroups of cs tiles
     a.cs = cs;
@@ -1491,16 +1554,17 @@ hipError_t launch_prop_pass1(const void* q, const void* K, int dtype, int B, int
     const unsigned grid = a.seq_lens ? static_cast<unsigned>(a.n_wg)
                                      : static_cast<unsigned>(a.B) * static_cast<unsigned>(a.KVH) * static_cast<unsigned>(a.cpg);
     if (grid == 0) return hipSuccess;
-    if (dtype == SANTA_BF16)
-      hipLaunchKernelGGL((wave_kernel<true, 4, false, true>), dim3(grid), dim3(kThreads), 0, stream,
-                         static_cast<const uint16_t*>(a.q), static_cast<const uint16_t*>(a.K), nullptr, a.H, a.KVH,
-                         a.L_valid, a.L_storage, a.T_c, a.cs, a.cpg, q_scale, 0, 0ULL, nullptr, nullptr, a.seq_lens,
-                         a.B, 0LL, m_tiles, ell_tiles, nullptr, u_stash, stash_ld);
-    else
-      hipLaunchKernelGGL((wave_kernel<false, 4, false, true>), dim3(grid), dim3(kThreads), 0, stream,
-                         static_cast<const uint16_t*>(a.q), static_cast<const uint16_t*>(a.K), nullptr, a.H, a.KVH,
-                         a.L_valid, a.L_storage, a.T_c, a.cs, a.cpg, q_scale, 0, 0ULL, nullptr, nullptr, a.seq_lens,
-                         a.B, 0LL, m_tiles, ell_tiles, nullptr, u_stash, stash_ld);
+#define SANTA_P1_LAUNCH(BF, PG)                                                                                   \
+  hipLaunchKernelGGL((wave_kernel<BF, 4, false, true, PG>), dim3(grid), dim3(kThreads), 0, stream,                \
+                     static_cast<const uint16_t*>(a.q), static_cast<const uint16_t*>(a.K), nullptr, a.H, a.KVH,     \
+                     a.L_valid, a.L_storage, a.T_c, a.cs, a.cpg, q_scale, 0, 0ULL, nullptr, nullptr, a.seq_lens,   \
+                     a.B, 0LL, m_tiles, ell_tiles, nullptr, u_stash, stash_ld, a.pt)
+    if (dtype == SANTA_BF16) {
+      if (a.pt.table) SANTA_P1_LAUNCH(true, true); else SANTA_P1_LAUNCH(true, false);
+    } else {
+      if (a.pt.table) SANTA_P1_LAUNCH(false, true); else SANTA_P1_LAUNCH(false, false);
+    }
+#undef SANTA_P1_LAUNCH
     return hipGetLastError();
   }
   if (dtype == SANTA_BF16)
@@ -1519,13 +1583,24 @@ void plan_chunks(int B, int KVH, int T_c, int* cs, int* cpg) { chunk_plan(B, KVH
 // B * KVH slots of each round are counted for those).  Eight rounds measured
 // best for santa_prop on 16 sequences of 8k-128k tokens (one round: 824 us,
 // four: 795, eight: 745, sixteen: 750).
-void plan_ragged(int B, int KVH, long long total_tiles, int* cs, int* n_wg) {
+void plan_ragged(int B, int KVH, long long total_tiles, int max_tiles, int* cs, int* n_wg) {
+  if (max_tiles > 0 && total_tiles == static_cast<long long>(B) * max_tiles) {
+    // every sequence has the same tile count: the uniform plan (one resident
+    // round), whose workgroups the ragged grid enumerates in the same order
+    int cpg = 1;
+    chunk_plan(B, KVH, max_tiles, cs, &cpg);
+    *n_wg = B * KVH * cpg;
+    return;
+  }
+  // uneven lengths: chunks for about eight resident rounds, so that the
+  // hardware dispatcher balances the sequences' partial chunks; a multiple of
+  // four tiles, one per wave of the block_n = 256 kernel
   const long long items = total_tiles * KVH;
   const long long resident = resident_workgroups();
   const long long slack = static_cast<long long>(B) * KVH;
   const long long want = 8 * ((resident > 2 * slack) ? resident - slack : (resident + 1) / 2);
   long long c = (items + want - 1) / want;
-  if (c < 1) c = 1;
+  c = (c + 3) / 4 * 4;
   *cs = static_cast<int>(c);
   *n_wg = static_cast<int>(KVH * ((total_tiles + c - 1) / c + B));
 }
@@ -1724,9 +1799,9 @@ struct RaggedWs {
   size_t part, emit, total;
   int cs, n_wg;
 };
-RaggedWs ragged_ws_layout(int B, int H, int KVH, long long total_tiles) {
+RaggedWs ragged_ws_layout(int B, int H, int KVH, long long total_tiles, int max_tiles) {
   RaggedWs w{};
-  flash::plan_ragged(B, KVH, total_tiles, &w.cs, &w.n_wg);
+  flash::plan_ragged(B, KVH, total_tiles, max_tiles, &w.cs, &w.n_wg);
   const size_t chunks = static_cast<size_t>(w.n_wg);
   size_t off = 0;
   w.part = off;
@@ -1738,30 +1813,33 @@ RaggedWs ragged_ws_layout(int B, int H, int KVH, long long total_tiles) {
 }
 }  // namespace
 
-extern "C" size_t santa_flash_ragged_workspace_size(int B, int H, int KVH, int D, long long total_tiles) {
+extern "C" size_t santa_flash_ragged_workspace_size(int B, int H, int KVH, int D, int max_tiles,
+                                                    long long total_tiles) {
   (void)D;
-  if (B <= 0 || H <= 0 || KVH <= 0 || H % KVH != 0 || total_tiles < 0) return 0;
-  return ragged_ws_layout(B, H, KVH, total_tiles).total;
+  if (B <= 0 || H <= 0 || KVH <= 0 || H % KVH != 0 || max_tiles <= 0 || total_tiles < 0) return 0;
+  return ragged_ws_layout(B, H, KVH, total_tiles, max_tiles).total;
 }
 
-extern "C" int santa_flash_decode_ragged(const void* q, const void* K, const void* V, int dtype, int B, int H, int KVH,
-                                         int D, int L_storage, const int* seq_lens, int max_len, long long total_tiles,
-                                         int block_n, int64_t S, uint64_t seed, void* out, float* m_star, int* vrows,
-                                         void* workspace, size_t workspace_bytes, hipStream_t stream) {
+// The ragged decode over a contiguous [B, L_storage, KVH, D] cache or, with
+// pt.table set, a paged one (L_storage is then only checked against max_len).
+static int flash_decode_ragged(const void* q, const void* K, const void* V, int dtype, int B, int H, int KVH, int D,
+                               int L_storage, const int* seq_lens, int max_len, long long total_tiles, int block_n,
+                               int64_t S, uint64_t seed, void* out, float* m_star, int* vrows, void* workspace,
+                               size_t workspace_bytes, hipStream_t stream, const PageTable& pt) {
   int st = check_flash_shape(dtype, B, H, KVH, D, max_len, L_storage, block_n);
   if (st != SANTA_OK) return st;
   if (!q || !K || !V || !out || !seq_lens) return set_error(SANTA_ERR_INVALID, "null pointer argument");
   const int T_c = (max_len + block_n - 1) / block_n;
   if (total_tiles < 0 || total_tiles > static_cast<long long>(B) * T_c)
     return set_error(SANTA_ERR_INVALID, "total_tiles out of range");
-  const RaggedWs w = ragged_ws_layout(B, H, KVH, total_tiles);
+  const RaggedWs w = ragged_ws_layout(B, H, KVH, total_tiles, T_c);
   if (!workspace || workspace_bytes < w.total)
     return set_error(SANTA_ERR_WORKSPACE, "workspace too small: need %zu bytes, got %zu", w.total, workspace_bytes);
   char* base = static_cast<char*>(workspace);
   float* part = reinterpret_cast<float*>(base + w.part);
   int* pe = reinterpret_cast<int*>(base + w.emit);
   flash::Args a{q, K, V, B, H, KVH, max_len, L_storage, T_c, 0, seed, nullptr, nullptr, nullptr, nullptr, nullptr,
-                part, pe, w.cs, 0, nullptr, seq_lens, w.n_wg, static_cast<long long>(S)};
+                part, pe, w.cs, 0, nullptr, seq_lens, w.n_wg, static_cast<long long>(S), pt};
   hipError_t e = (block_n == 256) ? flash::launch_wave(dtype, H / KVH, a, nullptr, nullptr, nullptr, stream)
                                   : flash::launch_tiles<flash::kOnline>(dtype, H / KVH, block_n, a, stream);
   if (e != hipSuccess) return set_error(SANTA_ERR_HIP, "tile launch failed: %s", hipGetErrorString(e));
@@ -1769,4 +1847,24 @@ extern "C" int santa_flash_decode_ragged(const void* q, const void* K, const voi
                           w.n_wg, static_cast<long long>(S), stream);
   if (e != hipSuccess) return set_error(SANTA_ERR_HIP, "merge launch failed: %s", hipGetErrorString(e));
   return clear_error();
+}
+
+extern "C" int santa_flash_decode_ragged(const void* q, const void* K, const void* V, int dtype, int B, int H, int KVH,
+                                         int D, int L_storage, const int* seq_lens, int max_len, long long total_tiles,
+                                         int block_n, int64_t S, uint64_t seed, void* out, float* m_star, int* vrows,
+                                         void* workspace, size_t workspace_bytes, hipStream_t stream) {
+  return flash_decode_ragged(q, K, V, dtype, B, H, KVH, D, L_storage, seq_lens, max_len, total_tiles, block_n, S, seed,
+                             out, m_star, vrows, workspace, workspace_bytes, stream, PageTable{nullptr, 0, 3, 1});
+}
+
+extern "C" int santa_flash_decode_paged(const void* q, const void* K_pages, const void* V_pages, int dtype, int B,
+                                        int H, int KVH, int D, int num_pages, int page_size, const int* block_table,
+                                        int table_stride, const int* seq_lens, int max_len, long long total_tiles,
+                                        int block_n, int64_t S, uint64_t seed, void* out, float* m_star, int* vrows,
+                                        void* workspace, size_t workspace_bytes, hipStream_t stream) {
+  PageTable pt{};
+  const int st = check_page_table(block_table, num_pages, page_size, table_stride, max_len, &pt);
+  if (st != SANTA_OK) return st;
+  return flash_decode_ragged(q, K_pages, V_pages, dtype, B, H, KVH, D, max_len, seq_lens, max_len, total_tiles,
+                             block_n, S, seed, out, m_star, vrows, workspace, workspace_bytes, stream, pt);
 }

@@ -7,11 +7,26 @@
 
 namespace santa {
 
+// Paged KV cache: a pool of pages [num_pages, 1 << shift, KVH, D]; token n of
+// sequence b is row n & ((1 << shift) - 1) of page
+// table[b * stride + (n >> shift)].  table == nullptr selects the contiguous
+// [B, L_storage, KVH, D] layout.  shift >= 3, so an 8-row aligned block of
+// tokens never straddles two pages.
+struct PageTable {
+  const int* table;
+  int stride;  // table entries per sequence
+  int shift;   // log2 of the page size
+  int num_pages;
+};
+
 // Records a printf-style message as the calling thread's last error and
 // returns `code`.
 int set_error(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
 // Clears the calling thread's last error and returns SANTA_OK.
 int clear_error();
+// Checks a paged cache's geometry (page_size a power of two in [8, 2^20],
+// num_pages > 0, table_stride >= ceil(max_len / page_size)) and fills pt.
+int check_page_table(const int* table, int num_pages, int page_size, int table_stride, int max_len, PageTable* pt);
 
 constexpr size_t kWsAlign = 256;
 inline size_t align_up(size_t x) { return (x + kWsAlign - 1) & ~(kWsAlign - 1); }
@@ -27,10 +42,12 @@ namespace flash {
 // whole 256-row tiles, 0 past each sequence's length.
 hipError_t launch_prop_pass1(const void* q, const void* K, int dtype, int B, int H, int KVH, int L, int L_storage,
                              int block_n, int path, float* m_tiles, float* ell_tiles, uint16_t* u_stash,
-                             const int* seq_lens, int cs, int n_wg, int stash_ld, hipStream_t stream);
-// Chunking of a ragged batch with total_tiles tiles: cs tiles per chunk and
-// an upper bound n_wg on the workgroups of the ragged grid.
-void plan_ragged(int B, int KVH, long long total_tiles, int* cs, int* n_wg);
+                             const int* seq_lens, int cs, int n_wg, int stash_ld, hipStream_t stream,
+                             PageTable pt = PageTable{nullptr, 0, 3, 1});
+// Chunking of a ragged batch with total_tiles tiles, the longest sequence
+// having max_tiles: cs tiles per chunk and an upper bound n_wg on the
+// workgroups of the ragged grid.
+void plan_ragged(int B, int KVH, long long total_tiles, int max_tiles, int* cs, int* n_wg);
 // The block_n = 256 online tile pass (the wave kernel) with its per-tile
 // statistics m, ell [B, H, T_c] and counts [B, H, T_c, 256] written out
 // (test hook; the chunk partials go to the santa_flash_decode workspace).

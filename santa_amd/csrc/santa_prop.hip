@@ -201,7 +201,8 @@ __device__ __forceinline__ int union_rows(const uint64_t* s_mask, int lane) {
 // HM: the stash is head-major [B, H, stash_ld] (the fused decode's layout
 // for the vec path: a lane reads its row pair with one 4-B load); otherwise
 // the reference's [B, L_storage, H].
-template <bool BF16, int GH, int BN, bool HM>
+// PAGED: V is a page pool read through pt (the stash is indexed by token).
+template <bool BF16, int GH, int BN, bool HM, bool PAGED = false>
 __global__ __launch_bounds__(kThreads) void pass2_kernel(const uint16_t* __restrict__ V,
                                                          const uint16_t* __restrict__ u_stash, int H, int KVH,
                                                          int L, int L_storage, int T_c, int cs, int cpg,
@@ -209,7 +210,8 @@ __global__ __launch_bounds__(kThreads) void pass2_kernel(const uint16_t* __restr
                                                          const float* __restrict__ a0_tile,
                                                          int16_t* __restrict__ dbg_counts, float* __restrict__ part,
                                                          int* __restrict__ part_emit, int want_emit,
-                                                         const int* __restrict__ seq_lens, int B, int stash_ld) {
+                                                         const int* __restrict__ seq_lens, int B, int stash_ld,
+                                                         PageTable pt) {
   constexpr int NCH = BN / 32;
   constexpr int NPAIR = (NCH + 3) / 4;
   constexpr int HPW = GH / 4;
@@ -239,8 +241,8 @@ __global__ __launch_bounds__(kThreads) void pass2_kernel(const uint16_t* __restr
   const size_t row_stride = static_cast<size_t>(KVH) * kD;
   const uint32_t row_bytes = static_cast<uint32_t>(KVH) * kD * 2u;
   // wave-uniform 64-bit base + 32-bit lane offset (scalar-base loads)
-  const char* Vg = reinterpret_cast<const char*>(V + static_cast<size_t>(b) * L_storage * row_stride +
-                                                 static_cast<size_t>(kv) * kD);
+  const size_t seq_off = PAGED ? 0 : static_cast<size_t>(b) * L_storage * row_stride;
+  const char* Vg = reinterpret_cast<const char*>(V + seq_off + static_cast<size_t>(kv) * kD);
   const uint32_t v_lane_off = 4u * static_cast<uint32_t>(lane);
   const uint16_t* ub = u_stash + static_cast<size_t>(b) * (HM ? static_cast<size_t>(H) * stash_ld
                                                               : static_cast<size_t>(L_storage) * H);
@@ -263,12 +265,20 @@ __global__ __launch_bounds__(kThreads) void pass2_kernel(const uint16_t* __restr
     for (int base = 0; base < lc[k]; base += 32) {
       float cf[32];
       uint32_t vw[32];
+      // paged: lane q looks up the page of the batch's q-th row
+      int pgv = 0;
+      if constexpr (PAGED) {
+        const int iq = min(base + (lane & 31), lc[k] - 1);
+        pgv = page_of_row(pt, b, s_lrow[g * BN + iq], true);
+      }
 #pragma unroll
       for (int q = 0; q < 32; ++q) {
         const int i = min(base + q, lc[k] - 1);
         const int rr = __builtin_amdgcn_readfirstlane(s_lrow[g * BN + i]);
         cf[q] = s_lcw[g * BN + i];
-        vw[q] = *reinterpret_cast<const uint32_t*>(Vg + static_cast<size_t>(rr) * row_bytes + v_lane_off);
+        const size_t off = PAGED ? paged_row(pt, __builtin_amdgcn_readlane(pgv, q), rr, row_bytes)
+                                 : static_cast<size_t>(rr) * row_bytes;
+        vw[q] = *reinterpret_cast<const uint32_t*>(Vg + off + v_lane_off);
       }
 #pragma unroll
       for (int q = 0; q < 32; ++q) {
@@ -430,6 +440,7 @@ struct Pass2Grid {
   const int* seq_lens;
   int n_wg;
   int stash_ld;  // > 0: head-major stash [B, H, stash_ld] (block_n 256 only)
+  PageTable pt;  // paged V (pt.table set) or contiguous
 };
 
 template <bool BF16, int GH, int BN>
@@ -440,14 +451,17 @@ static hipError_t launch_pass2_t(const uint16_t* V, const uint16_t* u_stash, int
   const unsigned grid = rg.seq_lens ? static_cast<unsigned>(rg.n_wg)
                                     : static_cast<unsigned>(B) * static_cast<unsigned>(KVH) * static_cast<unsigned>(cpg);
   if (grid == 0) return hipSuccess;
-  if (BN == 256 && rg.stash_ld > 0)
-    hipLaunchKernelGGL((pass2_kernel<BF16, GH, BN, true>), dim3(grid), dim3(kThreads), 0, stream, V, u_stash, H, KVH,
-                       L, L_storage, T_c, cs, cpg, invdelta, a0, counts, part, part_emit, want_emit, rg.seq_lens, B,
-                       rg.stash_ld);
-  else
-    hipLaunchKernelGGL((pass2_kernel<BF16, GH, BN, false>), dim3(grid), dim3(kThreads), 0, stream, V, u_stash, H,
-                       KVH, L, L_storage, T_c, cs, cpg, invdelta, a0, counts, part, part_emit, want_emit, rg.seq_lens,
-                       B, 0);
+#define SANTA_P2_LAUNCH(HM, PG, SLD)                                                                               \
+  hipLaunchKernelGGL((pass2_kernel<BF16, GH, BN, HM, PG>), dim3(grid), dim3(kThreads), 0, stream, V, u_stash, H, KVH, \
+                     L, L_storage, T_c, cs, cpg, invdelta, a0, counts, part, part_emit, want_emit, rg.seq_lens, B,    \
+                     SLD, rg.pt)
+  const bool hm = BN == 256 && rg.stash_ld > 0;
+  if (rg.pt.table) {
+    if (hm) SANTA_P2_LAUNCH(true, true, rg.stash_ld); else SANTA_P2_LAUNCH(false, true, 0);
+  } else {
+    if (hm) SANTA_P2_LAUNCH(true, false, rg.stash_ld); else SANTA_P2_LAUNCH(false, false, 0);
+  }
+#undef SANTA_P2_LAUNCH
   return hipGetLastError();
 }
 
@@ -483,7 +497,7 @@ static PropWs prop_ws_layout(int B, int H, int KVH, int L_storage, int T_c, long
   PropWs w{};
   size_t chunks;
   if (total_tiles >= 0) {
-    flash::plan_ragged(B, KVH, total_tiles, &w.cs, &w.n_wg);
+    flash::plan_ragged(B, KVH, total_tiles, T_c, &w.cs, &w.n_wg);
     w.cpg = 0;
     chunks = static_cast<size_t>(w.n_wg);
   } else {
@@ -622,8 +636,8 @@ static int prop_pass2_launch(const void* V, const uint16_t* u_stash, int dtype, 
                              int L_storage, int block_n, int T_c, int S, const float* invdelta, const float* a0,
                              int16_t* counts, void* out, int* vrows, const prop::PropWs& w, char* base,
                              hipStream_t stream, const int* seq_lens = nullptr, const int* seq_S = nullptr,
-                             int stash_ld = 0) {
-  const prop::Pass2Grid rg{seq_lens, w.n_wg, stash_ld};
+                             int stash_ld = 0, PageTable pt = PageTable{nullptr, 0, 3, 1}) {
+  const prop::Pass2Grid rg{seq_lens, w.n_wg, stash_ld, pt};
   float* part = reinterpret_cast<float*>(base + w.part);
   int* pe = reinterpret_cast<int*>(base + w.emit);
   const int GH = H / KVH;
@@ -730,11 +744,13 @@ extern "C" size_t santa_prop_batched_workspace_size(int B, int H, int KVH, int D
   return prop::prop_ws_layout(B, H, KVH, L_storage, max_tiles, total_tiles).total;
 }
 
-extern "C" int santa_prop_decode_batched(const void* q, const void* K, const void* V, int dtype, int B, int H, int KVH,
-                                         int D, int L_storage, const int* seq_lens, const int* seq_S, int max_len,
-                                         long long total_tiles, int block_n, int pass1_path, uint64_t seed, void* out,
-                                         float* m_star, int* vrows, void* workspace, size_t workspace_bytes,
-                                         hipStream_t stream) {
+// The batched decode over a contiguous [B, L_storage, KVH, D] cache or, with
+// pt.table set, a paged one (L_storage then only sizes the stash).
+static int prop_decode_batched(const void* q, const void* K, const void* V, int dtype, int B, int H, int KVH, int D,
+                               int L_storage, const int* seq_lens, const int* seq_S, int max_len,
+                               long long total_tiles, int block_n, int pass1_path, uint64_t seed, void* out,
+                               float* m_star, int* vrows, void* workspace, size_t workspace_bytes, hipStream_t stream,
+                               const PageTable& pt) {
   int st = prop::check_common(dtype, H, KVH, D);
   if (st != SANTA_OK) return st;
   if (B <= 0) return set_error(SANTA_ERR_INVALID, "empty batch");
@@ -760,13 +776,36 @@ extern "C" int santa_prop_decode_batched(const void* q, const void* K, const voi
   uint16_t* stash = reinterpret_cast<uint16_t*>(base + w.stash);
   const int sld = (pass1_path == 0) ? prop::stash_ld(L_storage) : 0;
   hipError_t e = flash::launch_prop_pass1(q, K, dtype, B, H, KVH, max_len, L_storage, block_n, pass1_path, m_tiles,
-                                          ell_tiles, stash, seq_lens, w.cs, w.n_wg, sld, stream);
+                                          ell_tiles, stash, seq_lens, w.cs, w.n_wg, sld, stream, pt);
   if (e != hipSuccess) return set_error(SANTA_ERR_HIP, "pass-1 launch failed: %s", hipGetErrorString(e));
   if ((st = prop_budgets_launch(m_tiles, ell_tiles, B * H, H, T_c, 0, seed, m_star, S_tiles, inv, a0, stream, seq_lens,
                                 seq_S, block_n)) != SANTA_OK)
     return st;
   if ((st = prop_pass2_launch(V, stash, dtype, B, H, KVH, max_len, L_storage, block_n, T_c, 0, inv, a0, nullptr, out,
-                              vrows, w, base, stream, seq_lens, seq_S, sld)) != SANTA_OK)
+                              vrows, w, base, stream, seq_lens, seq_S, sld, pt)) != SANTA_OK)
     return st;
   return clear_error();
+}
+
+extern "C" int santa_prop_decode_batched(const void* q, const void* K, const void* V, int dtype, int B, int H, int KVH,
+                                         int D, int L_storage, const int* seq_lens, const int* seq_S, int max_len,
+                                         long long total_tiles, int block_n, int pass1_path, uint64_t seed, void* out,
+                                         float* m_star, int* vrows, void* workspace, size_t workspace_bytes,
+                                         hipStream_t stream) {
+  return prop_decode_batched(q, K, V, dtype, B, H, KVH, D, L_storage, seq_lens, seq_S, max_len, total_tiles, block_n,
+                             pass1_path, seed, out, m_star, vrows, workspace, workspace_bytes, stream,
+                             PageTable{nullptr, 0, 3, 1});
+}
+
+extern "C" int santa_prop_decode_paged(const void* q, const void* K_pages, const void* V_pages, int dtype, int B, int H,
+                                       int KVH, int D, int num_pages, int page_size, const int* block_table,
+                                       int table_stride, const int* seq_lens, const int* seq_S, int max_len,
+                                       long long total_tiles, int block_n, int pass1_path, uint64_t seed, void* out,
+                                       float* m_star, int* vrows, void* workspace, size_t workspace_bytes,
+                                       hipStream_t stream) {
+  PageTable pt{};
+  const int st = check_page_table(block_table, num_pages, page_size, table_stride, max_len, &pt);
+  if (st != SANTA_OK) return st;
+  return prop_decode_batched(q, K_pages, V_pages, dtype, B, H, KVH, D, max_len, seq_lens, seq_S, max_len, total_tiles,
+                             block_n, pass1_path, seed, out, m_star, vrows, workspace, workspace_bytes, stream, pt);
 }

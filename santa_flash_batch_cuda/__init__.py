@@ -5,6 +5,14 @@ reference's `santa_flash_batch_cuda` extension module
     decode_systematic_scalar(q_h, K_g, V_g, S, seed=42, block_n=0,
                              want_vrows=False, valid_len=-1) -> (out, m_star, vrows)
     decode_systematic_batched(...)   # the same function
+    decode_systematic_paged(q_h, K_pages, V_pages, block_table, seq_lens, S,
+                            seed=42, block_n=0, want_vrows=False) -> (out, m_star, vrows)
+
+decode_systematic_paged (an addition over the reference, which reads
+contiguous caches only) takes a page pool K_pages / V_pages
+[num_pages, page_size, KVH, D] and an int32 block table [B, pages per
+sequence]: token n of sequence b is row n % page_size of page
+block_table[b, n // page_size].  page_size is a power of two >= 8.
 
 torch is imported first so that the native module binds to torch's HIP runtime.
 """
@@ -19,5 +27,6 @@ from ._C import (  # noqa: F401
     _library_version,
     _workspace_bytes,
     decode_systematic_batched,
+    decode_systematic_paged,
     decode_systematic_scalar,
 )

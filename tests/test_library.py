@@ -142,6 +142,31 @@ def test_compute_entry_points_validate_before_any_launch(lib):
     assert rc == ERR_INVALID
 
 
+def test_paged_entry_points_validate_the_page_table(lib):
+    null = ctypes.c_void_p(0)
+    table = (ctypes.c_int * 4)()  # host memory: only its address is checked before a launch
+
+    def flash(page_size, num_pages, stride, max_len, block_table=table):
+        return lib.santa_flash_decode_paged(null, null, null, 0, 1, 32, 8, 128, num_pages, page_size, block_table,
+                                            stride, null, max_len, ctypes.c_longlong(1), 256, ctypes.c_int64(256),
+                                            ctypes.c_uint64(1), null, null, null, null, ctypes.c_size_t(0), null)
+
+    rc = flash(24, 4, 4, 64)
+    assert rc == ERR_INVALID and b"page_size must be a power of two" in lib.santa_last_error()
+    rc = flash(4, 4, 4, 16)
+    assert rc == ERR_INVALID and b"page_size must be a power of two in [8" in lib.santa_last_error()
+    rc = flash(16, 0, 4, 64)
+    assert rc == ERR_INVALID and b"num_pages must be > 0" in lib.santa_last_error()
+    rc = flash(16, 8, 3, 64)  # 64 tokens need 4 pages of 16
+    assert rc == ERR_INVALID and b"block table too narrow" in lib.santa_last_error()
+    rc = flash(16, 8, 4, 64, block_table=null)
+    assert rc == ERR_INVALID and b"null pointer" in lib.santa_last_error()
+    rc = lib.santa_prop_decode_paged(null, null, null, 0, 1, 32, 8, 128, 8, 12, table, 4, null, null, 64,
+                                     ctypes.c_longlong(1), 256, 0, ctypes.c_uint64(1), null, null, null, null,
+                                     ctypes.c_size_t(0), null)
+    assert rc == ERR_INVALID and b"page_size must be a power of two" in lib.santa_last_error()
+
+
 def test_workspace_sizes_are_host_only(lib):
     lib.santa_flash_workspace_size.restype = ctypes.c_size_t
     lib.santa_prop_workspace_size.restype = ctypes.c_size_t
