@@ -1166,8 +1166,52 @@ __global__ __launch_bounds__(kThreads, 2) void wave_kernel(
   // no load to LDS outstanding past here (the staging area is reused below)
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   if constexpr (P1) return;  // pass 1 writes no partials
+  // The chunk's remaining listed rows: the loads of up to 16 rows of every
+  // head are issued together (one memory round trip per 16 rows, not one per
+  // head), then accumulated head by head in list order, as flush() does.
+  {
+    int rowv[GH], pgv[GH];
+    float coefv[GH];
+    int nmax = 0;
 #pragma unroll
-  for (int g = 0; g < GH; ++g) flush(g);
+    for (int g = 0; g < GH; ++g) {
+      rowv[g] = (lane < lcnt[g]) ? lrow[g * LCAP + lane] : 0;
+      coefv[g] = (lane < lcnt[g]) ? lcw[g * LCAP + lane] : 0.0f;
+      pgv[g] = PAGED ? page_of_row(pt, b, rowv[g], lane < lcnt[g]) : 0;
+      nmax = max(nmax, lcnt[g]);
+    }
+    for (int q0 = 0; q0 < nmax; q0 += 16) {
+      uint32_t vw[GH][16];
+#pragma unroll
+      for (int g = 0; g < GH; ++g) {
+        if (lcnt[g] > q0) {
+#pragma unroll
+          for (int q = 0; q < 16; ++q) {
+            const int j = min(q0 + q, lcnt[g] - 1);
+            const int row = __builtin_amdgcn_readlane(rowv[g], j);
+            const size_t off = PAGED ? paged_row(pt, __builtin_amdgcn_readlane(pgv[g], j), row, row_bytes)
+                                     : static_cast<size_t>(row) * row_bytes;
+            vw[g][q] = *reinterpret_cast<const uint32_t*>(Vg + off + v_lane_off);
+          }
+        }
+      }
+#pragma unroll
+      for (int g = 0; g < GH; ++g) {
+        if (lcnt[g] > q0) {
+#pragma unroll
+          for (int q = 0; q < 16; ++q) {
+            if (q0 + q < lcnt[g]) {
+              const float c = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(coefv[g]), q0 + q));
+              num0[g] = fmaf(c, lo16_to_f32<BF16>(vw[g][q]), num0[g]);
+              num1[g] = fmaf(c, hi16_to_f32<BF16>(vw[g][q]), num1[g]);
+            }
+          }
+        }
+      }
+    }
+#pragma unroll
+    for (int g = 0; g < GH; ++g) lcnt[g] = 0;
+  }
 
   // ---- the four waves' partials, merged in wave order -----------------------------
   __syncthreads();  // every wave is done with its staging area
