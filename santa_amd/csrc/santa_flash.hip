@@ -47,6 +47,7 @@
 #include "santa_amd.h"
 #include "santa_internal.h"
 
+#include <algorithm>
 #include <type_traits>
 
 namespace santa {
@@ -762,8 +763,13 @@ __device__ __forceinline__ float wave_ell(const float (&u)[2][2]) {
 // P1: santa_prop pass 1 with the vec path's numerics (the flash tile
 // statistics): per tile and head m and ell into dbg_m / dbg_ell ([B, H, T_c])
 // and the 16-bit u into u_stash ([B, L_storage, H]); no sampling, no partials.
-template <bool BF16, int GH, bool DBG, bool P1 = false, bool PAGED = false>
-__global__ __launch_bounds__(kThreads, 2) void wave_kernel(
+// ROWS: a workgroup of KVH waves (KVH <= 8), wave kv taking KV head kv over
+// every tile of the workgroup's chunk, so the KV heads of a token chunk are
+// read together, row by row, by one CU; each wave writes its own chunk
+// partial.  Otherwise four waves share one KV head, taking every fourth
+// tile, and merge their partials at the end of the chunk.
+template <bool BF16, int GH, bool DBG, bool P1 = false, bool PAGED = false, bool ROWS = false>
+__global__ __launch_bounds__(ROWS ? 512 : kThreads, ROWS ? 1 : 2) void wave_kernel(
     const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K, const uint16_t* __restrict__ V, int H, int KVH,
     int L_valid, int L_storage, int T_c, int cs, int cpg, float q_scale, int S_pt, uint64_t seed,
     float* __restrict__ part, int* __restrict__ part_emit, const int* __restrict__ seq_lens, int B, long long S_total,
@@ -776,8 +782,15 @@ __global__ __launch_bounds__(kThreads, 2) void wave_kernel(
   // uniform grid, or the ragged one (seq_lens: per-sequence lengths, L_valid
   // the longest; workgroups past the last sequence only write an empty
   // partial)
-  const GridPos gp = grid_pos(wg, seq_lens, B, KVH, BN, L_valid, T_c, cs, cpg);
-  const int kv = gp.kv;
+  constexpr int NWV = ROWS ? 8 : 4;  // waves per workgroup (at most)
+  constexpr int TS = ROWS ? 1 : 4;    // tile stride of a wave
+  const int tid = static_cast<int>(threadIdx.x);
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  // ROWS workgroups enumerate (sequence, chunk) items (grid_pos with one
+  // "head"); the KV head is the wave
+  const GridPos gp = grid_pos(wg, seq_lens, B, ROWS ? 1 : KVH, BN, L_valid, T_c, cs, cpg);
+  const int kv = ROWS ? wave : gp.kv;
   const int b = gp.b < 0 ? 0 : gp.b;
   const int h0 = kv * GH;
   L_valid = gp.len;
@@ -785,13 +798,11 @@ __global__ __launch_bounds__(kThreads, 2) void wave_kernel(
   const int t_end = (gp.b < 0) ? t_begin : min(gp.n_tiles, t_begin + cs);
   if (seq_lens)  // S_per_tile from this sequence's tile count (flash/santa_cuda.cpp:204-208)
     S_pt = (S_total > 0) ? static_cast<int>(max(1LL, S_total / static_cast<long long>(max(gp.n_tiles, 1)))) : 0;
-  const int tid = static_cast<int>(threadIdx.x);
-  const int lane = tid & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int t_first = ROWS ? t_begin : t_begin + wave;
 
-  __shared__ u32x4 s_k[4 * 64 * 16];  // per wave: 64 rows x 256 B staging; the chunk merge reuses it
-  __shared__ int s_lrow[4 * GH * LCAP];
-  __shared__ float s_lcw[4 * GH * LCAP];
+  __shared__ u32x4 s_k[NWV * 64 * 16];  // per wave: 64 rows x 256 B staging; the chunk merge reuses it
+  __shared__ int s_lrow[NWV * GH * LCAP];
+  __shared__ float s_lcw[NWV * GH * LCAP];
   u32x4* const wk = s_k + wave * 64 * 16;
   int* const lrow = s_lrow + wave * GH * LCAP;
   float* const lcw = s_lcw + wave * GH * LCAP;
@@ -914,15 +925,15 @@ __global__ __launch_bounds__(kThreads, 2) void wave_kernel(
   };
   // pv: pages of the current tile; pv_next: of the wave's next tile (loaded
   // while the current one is scored)
-  int pv = tile_pages(t_begin + wave);
+  int pv = tile_pages(t_first);
   int pv_next = 0;
-  if (t_begin + wave < t_end) dma_k(t_begin + wave, pv);
-  load_k(t_begin + wave, 1, pv);
+  if (t_first < t_end) dma_k(t_first, pv);
+  load_k(t_first, 1, pv);
 
   const int jrow = lane >> 4;
   const int qq = lane & 15;
   const uint64_t below = (1ull << lane) - 1ull;
-  for (int t = t_begin + wave; t < t_end; t += 4) {
+  for (int t = t_first; t < t_end; t += TS) {
     const int n0 = t * BN;
     const int len = min(BN, L_valid - n0);
 
@@ -938,7 +949,7 @@ __global__ __launch_bounds__(kThreads, 2) void wave_kernel(
         } else {
           asm volatile("s_waitcnt vmcnt(16)" ::: "memory");
         }
-        if constexpr (PAGED) pv_next = tile_pages(t + 4);
+        if constexpr (PAGED) pv_next = tile_pages(t + TS);
       } else {
 #pragma unroll
         for (int c = 0; c < 16; ++c) {
@@ -950,7 +961,7 @@ __global__ __launch_bounds__(kThreads, 2) void wave_kernel(
         if (sb < 3) {
           load_k(t, sb + 1, pv);
         } else if constexpr (GH == 4) {
-          load_k(t + 4, 1, pv_next);
+          load_k(t + TS, 1, pv_next);
         }
       }
       __builtin_amdgcn_wave_barrier();
@@ -983,7 +994,7 @@ __global__ __launch_bounds__(kThreads, 2) void wave_kernel(
 
     // every row of the staging area has been read: the next tile's sub-block 0
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-    if (t + 4 < t_end) dma_k(t + 4, pv_next);
+    if (t + TS < t_end) dma_k(t + TS, pv_next);
 
     // ---- tile max per head (exact in any order) --------------------------------
     bool valid[2][2];
@@ -1160,7 +1171,7 @@ __global__ __launch_bounds__(kThreads, 2) void wave_kernel(
         }
     }
     emit_total += __popcll(uni[0][0]) + __popcll(uni[0][1]) + __popcll(uni[1][0]) + __popcll(uni[1][1]);
-    if constexpr (GH == 8) load_k(t + 4, 1, pv_next);
+    if constexpr (GH == 8) load_k(t + TS, 1, pv_next);
     pv = pv_next;
   }
   // no load to LDS outstanding past here (the staging area is reused below)
@@ -1211,6 +1222,23 @@ __global__ __launch_bounds__(kThreads, 2) void wave_kernel(
     }
 #pragma unroll
     for (int g = 0; g < GH; ++g) lcnt[g] = 0;
+  }
+
+  if constexpr (ROWS) {
+    // this wave's partial is the (b, kv, chunk) partial
+    const size_t slot = static_cast<size_t>(wg) * KVH + wave;
+#pragma unroll
+    for (int g = 0; g < GH; ++g) {
+      float* pp = part + (slot * GH + g) * kPartStride;
+      if (lane == 0) {
+        pp[0] = runM[g];
+        pp[1] = runZ[g];
+      }
+      pp[2 + 2 * lane] = num0[g];
+      pp[3 + 2 * lane] = num1[g];
+    }
+    if (lane == 0) part_emit[slot] = emit_total;
+    return;
   }
 
   // ---- the four waves' partials, merged in wave order -----------------------------
@@ -1334,18 +1362,20 @@ __global__ __launch_bounds__(kThreads) void finalize_kernel(const float* __restr
 // Merge of the chunk partials of one (b, h): m* = max_c M_c,
 // w_c = exp(M_c - m*), out = (sum_c w_c num_c) / ((sum_c w_c Z_c) S_pt).
 template <bool BF16, int GH>
-__global__ __launch_bounds__(kD) void merge_kernel(const float* __restrict__ part, const int* __restrict__ part_emit,
-                                                   int H, int KVH, int cpg, int S_pt, uint16_t* __restrict__ out,
-                                                   float* __restrict__ m_star, int* __restrict__ vrows,
-                                                   const int* __restrict__ seq_lens, int BN, int cs, int max_len,
-                                                   int n_wg, long long S_total) {
+__global__ __launch_bounds__(1024) void merge_kernel(const float* __restrict__ part, const int* __restrict__ part_emit,
+                                                     int H, int KVH, int cpg, int S_pt, uint16_t* __restrict__ out,
+                                                     float* __restrict__ m_star, int* __restrict__ vrows,
+                                                     const int* __restrict__ seq_lens, int BN, int cs, int max_len,
+                                                     int n_wg, long long S_total) {
   const int bh = static_cast<int>(blockIdx.x);
   const int b = bh / H;
   const int h = bh % H;
   const int kv = h / GH;
   const int g = h % GH;
   const int bk = b * KVH + kv;
-  const int d = static_cast<int>(threadIdx.x);
+  const int d = static_cast<int>(threadIdx.x) & (kD - 1);
+  const int grp = static_cast<int>(threadIdx.x) / kD;   // thread group: a range of chunks
+  const int ngrp = static_cast<int>(blockDim.x) / kD;
   // chunk c of (b, kv) was workgroup base_b + c * KVH + kv
   int base = b * cpg * KVH;
   if (seq_lens) {
@@ -1358,49 +1388,82 @@ __global__ __launch_bounds__(kD) void merge_kernel(const float* __restrict__ par
   }
   const float* pb = part + ((static_cast<size_t>(base) + kv) * GH + g) * kPartStride;
   const size_t cstride = static_cast<size_t>(KVH) * GH * kPartStride;
-  // The partials are read in batches of up to 16 chunks with every load of
-  // a batch issued before the first use (one memory round trip per batch,
-  // usually the only one); max and sums keep the ascending chunk order.
+  // Each thread group merges a contiguous range of chunks, with the loads of
+  // a batch of up to 16 chunks issued before the first use (one memory round
+  // trip per batch, usually the only one); max and sums keep the ascending
+  // chunk order inside a range, and the ranges are combined in group order.
   constexpr int kBatch = 16;
+  const int per = (cpg + ngrp - 1) / ngrp;
+  const int c0 = min(cpg, grp * per);
+  const int n = min(cpg, c0 + per) - c0;
   float ms = -__builtin_inff();
   float Z = 0.0f, num = 0.0f;
-  if (cpg <= kBatch) {
+  int e = 0;
+  if (n <= kBatch) {
     float mc[kBatch], zc[kBatch], nc[kBatch];
+    int ec[kBatch];
 #pragma unroll
     for (int c = 0; c < kBatch; ++c) {
-      const float* pc = pb + static_cast<size_t>(c < cpg ? c : 0) * cstride;
+      const int cc = c0 + (c < n ? c : 0);
+      const float* pc = pb + static_cast<size_t>(cc) * cstride;
       mc[c] = pc[0];
       zc[c] = pc[1];
       nc[c] = pc[2 + d];
+      ec[c] = (vrows && d == 0) ? part_emit[static_cast<size_t>(base) + cc * KVH + kv] : 0;
     }
+    if (n > 0) {
 #pragma unroll
-    for (int c = 0; c < kBatch; ++c)
-      if (c < cpg) ms = fmaxf(ms, mc[c]);
+      for (int c = 0; c < kBatch; ++c)
+        if (c < n) ms = fmaxf(ms, mc[c]);
 #pragma unroll
-    for (int c = 0; c < kBatch; ++c) {
-      if (c < cpg) {
-        const float w = santa_expf(mc[c] - ms);
-        Z = fmaf(w, zc[c], Z);
-        num = fmaf(w, nc[c], num);
+      for (int c = 0; c < kBatch; ++c) {
+        if (c < n) {
+          const float w = santa_expf(mc[c] - ms);
+          Z = fmaf(w, zc[c], Z);
+          num = fmaf(w, nc[c], num);
+          e += ec[c];
+        }
       }
     }
   } else {
-    for (int c = 0; c < cpg; ++c) ms = fmaxf(ms, pb[c * cstride]);
-    for (int c = 0; c < cpg; ++c) {
+    for (int c = c0; c < c0 + n; ++c) ms = fmaxf(ms, pb[c * cstride]);
+    for (int c = c0; c < c0 + n; ++c) {
       const float* pc = pb + c * cstride;
       const float w = santa_expf(pc[0] - ms);
       Z = fmaf(w, pc[1], Z);
       num = fmaf(w, pc[2 + d], num);
+      if (vrows && d == 0) e += part_emit[static_cast<size_t>(base) + c * KVH + kv];
     }
+  }
+  if (ngrp > 1) {
+    __shared__ float s_m[8], s_z[8], s_n[8][kD];
+    __shared__ int s_e[8];
+    if (d == 0) {
+      s_m[grp] = ms;
+      s_z[grp] = Z;
+      s_e[grp] = e;
+    }
+    s_n[grp][d] = num;
+    __syncthreads();
+    if (grp != 0) return;
+    ms = -__builtin_inff();
+    for (int j = 0; j < ngrp; ++j) ms = fmaxf(ms, s_m[j]);
+    Z = 0.0f;
+    num = 0.0f;
+    e = 0;
+    if (ms != -__builtin_inff()) {
+      for (int j = 0; j < ngrp; ++j) {
+        const float w = santa_expf(s_m[j] - ms);
+        Z = fmaf(w, s_z[j], Z);
+        num = fmaf(w, s_n[j][d], num);
+      }
+    }
+    for (int j = 0; j < ngrp; ++j) e += s_e[j];
   }
   const float inv_norm = (S_pt > 0 && Z > 0.0f) ? (1.0f / (Z * static_cast<float>(S_pt))) : 0.0f;
   out[static_cast<size_t>(bh) * kD + d] = f32_to_h16<BF16>(num * inv_norm);
   if (d == 0 && m_star) m_star[bh] = ms;
-  if (vrows && g == 0 && d == 0) {
-    int e = 0;
-    for (int c = 0; c < cpg; ++c) e += part_emit[static_cast<size_t>(base) + c * KVH + kv];
-    vrows[bk] = e;
-  }
+  if (vrows && g == 0 && d == 0) vrows[bk] = e;
 }
 
 struct Args {
@@ -1473,6 +1536,22 @@ static hipError_t launch_wave_t(const Args& a, float* dbg_m, float* dbg_ell, int
                        static_cast<const uint16_t*>(a.V), a.H, a.KVH, a.L_valid, a.L_storage, a.T_c, a.cs, a.cpg,
                        q_scale, a.S_pt, a.seed, a.part, a.part_emit, a.seq_lens, a.B, a.S_total, dbg_m, dbg_ell,
                        dbg_counts, nullptr, 0, a.pt);
+  } else if (rows_layout(a.KVH)) {
+    // one workgroup of KVH waves per (sequence, chunk) item
+    const unsigned rgrid = grid / static_cast<unsigned>(a.KVH);
+    const dim3 block(static_cast<unsigned>(64 * a.KVH));
+    if (a.pt.table)
+      hipLaunchKernelGGL((wave_kernel<BF16, GH, false, false, true, true>), dim3(rgrid), block, 0, stream,
+                         static_cast<const uint16_t*>(a.q), static_cast<const uint16_t*>(a.K),
+                         static_cast<const uint16_t*>(a.V), a.H, a.KVH, a.L_valid, a.L_storage, a.T_c, a.cs, a.cpg,
+                         q_scale, a.S_pt, a.seed, a.part, a.part_emit, a.seq_lens, a.B, a.S_total, nullptr,
+                         nullptr, nullptr, nullptr, 0, a.pt);
+    else
+      hipLaunchKernelGGL((wave_kernel<BF16, GH, false, false, false, true>), dim3(rgrid), block, 0, stream,
+                         static_cast<const uint16_t*>(a.q), static_cast<const uint16_t*>(a.K),
+                         static_cast<const uint16_t*>(a.V), a.H, a.KVH, a.L_valid, a.L_storage, a.T_c, a.cs, a.cpg,
+                         q_scale, a.S_pt, a.seed, a.part, a.part_emit, a.seq_lens, a.B, a.S_total, nullptr,
+                         nullptr, nullptr, nullptr, 0, a.pt);
   } else if (a.pt.table) {
     hipLaunchKernelGGL((wave_kernel<BF16, GH, false, false, true>), dim3(grid), dim3(kThreads), 0, stream,
                        static_cast<const uint16_t*>(a.q), static_cast<const uint16_t*>(a.K),
@@ -1508,19 +1587,23 @@ static hipError_t launch_merge(const float* part, const int* pe, int dtype, int 
   const int GH = H / KVH;
   const unsigned grid = static_cast<unsigned>(B) * static_cast<unsigned>(H);
   uint16_t* o = static_cast<uint16_t*>(out);
+  // thread groups of 128: enough that each merges at most 16 chunks (up to 8)
+  const int max_chunks = seq_lens ? ((max_len + bn - 1) / bn + cs - 1) / cs : cpg;
+  const int ngrp = std::min(8, std::max(1, (max_chunks + 15) / 16));
+  const dim3 block(static_cast<unsigned>(kD * ngrp));
   if (dtype == SANTA_BF16) {
     if (GH == 4)
-      hipLaunchKernelGGL((merge_kernel<true, 4>), dim3(grid), dim3(kD), 0, stream, part, pe, H, KVH, cpg, S_pt, o,
+      hipLaunchKernelGGL((merge_kernel<true, 4>), dim3(grid), block, 0, stream, part, pe, H, KVH, cpg, S_pt, o,
                          m_star, vrows, seq_lens, bn, cs, max_len, n_wg, S_total);
     else
-      hipLaunchKernelGGL((merge_kernel<true, 8>), dim3(grid), dim3(kD), 0, stream, part, pe, H, KVH, cpg, S_pt, o,
+      hipLaunchKernelGGL((merge_kernel<true, 8>), dim3(grid), block, 0, stream, part, pe, H, KVH, cpg, S_pt, o,
                          m_star, vrows, seq_lens, bn, cs, max_len, n_wg, S_total);
   } else {
     if (GH == 4)
-      hipLaunchKernelGGL((merge_kernel<false, 4>), dim3(grid), dim3(kD), 0, stream, part, pe, H, KVH, cpg, S_pt, o,
+      hipLaunchKernelGGL((merge_kernel<false, 4>), dim3(grid), block, 0, stream, part, pe, H, KVH, cpg, S_pt, o,
                          m_star, vrows, seq_lens, bn, cs, max_len, n_wg, S_total);
     else
-      hipLaunchKernelGGL((merge_kernel<false, 8>), dim3(grid), dim3(kD), 0, stream, part, pe, H, KVH, cpg, S_pt, o,
+      hipLaunchKernelGGL((merge_kernel<false, 8>), dim3(grid), block, 0, stream, part, pe, H, KVH, cpg, S_pt, o,
                          m_star, vrows, seq_lens, bn, cs, max_len, n_wg, S_total);
   }
   return hipGetLastError();
@@ -1550,10 +1633,11 @@ static int resident_workgroups() {
 }
 
 // Chunking of each group's T_c tiles so that B*KVH*cpg is about one resident
-// round: cpg chunks of cs tiles (the last may be shorter).
-static void chunk_plan(int B, int KVH, int T_c, int* cs, int* cpg) {
+// round of per_round items (0: resident_workgroups(), one 4-wave workgroup
+// per item): cpg chunks of cs tiles (the last may be shorter).
+static void chunk_plan(int B, int KVH, int T_c, int* cs, int* cpg, int per_round = 0) {
   const long long groups = static_cast<long long>(B) * KVH;
-  long long want = (resident_workgroups() + groups / 2) / groups;
+  long long want = ((per_round > 0 ? per_round : resident_workgroups()) + groups / 2) / groups;
   if (want < 1) want = 1;
   if (want > T_c) want = T_c;
   const int c = static_cast<int>((T_c + want - 1) / want);
@@ -1621,30 +1705,37 @@ hipError_t launch_prop_pass1(const void* q, const void* K, int dtype, int B, int
 // Tile chunking shared with santa_prop's pass 2.
 void plan_chunks(int B, int KVH, int T_c, int* cs, int* cpg) { chunk_plan(B, KVH, T_c, cs, cpg); }
 
+// The flash tile pass runs its ROWS form (one wave per KV head) for KVH = 8
+// (its LDS is sized for eight waves); its chunks are then planned for one
+// resident round of single-wave items (four per 4-wave workgroup slot).
+bool rows_layout(int KVH) { return KVH == 8; }
+int rows_per_round() { return 4 * resident_workgroups(); }
+
 // Ragged batches: chunks small enough for about eight resident rounds over
 // all (kv, tile) items, so the hardware's workgroup dispatch evens out the
 // uneven chunks (each sequence adds at most one partial chunk per KV head;
 // B * KVH slots of each round are counted for those).  Eight rounds measured
 // best for santa_prop on 16 sequences of 8k-128k tokens (one round: 824 us,
 // four: 795, eight: 745, sixteen: 750).
-void plan_ragged(int B, int KVH, long long total_tiles, int max_tiles, int* cs, int* n_wg) {
+void plan_ragged(int B, int KVH, long long total_tiles, int max_tiles, int* cs, int* n_wg, int per_round,
+                 int granule) {
   if (max_tiles > 0 && total_tiles == static_cast<long long>(B) * max_tiles) {
     // every sequence has the same tile count: the uniform plan (one resident
     // round), whose workgroups the ragged grid enumerates in the same order
     int cpg = 1;
-    chunk_plan(B, KVH, max_tiles, cs, &cpg);
+    chunk_plan(B, KVH, max_tiles, cs, &cpg, per_round);
     *n_wg = B * KVH * cpg;
     return;
   }
   // uneven lengths: chunks for about eight resident rounds, so that the
   // hardware dispatcher balances the sequences' partial chunks; a multiple of
-  // four tiles, one per wave of the block_n = 256 kernel
+  // `granule` tiles (4: one per wave of the 4-wave block_n = 256 kernel)
   const long long items = total_tiles * KVH;
-  const long long resident = resident_workgroups();
+  const long long resident = per_round > 0 ? per_round : resident_workgroups();
   const long long slack = static_cast<long long>(B) * KVH;
   const long long want = 8 * ((resident > 2 * slack) ? resident - slack : (resident + 1) / 2);
   long long c = (items + want - 1) / want;
-  c = (c + 3) / 4 * 4;
+  c = (c + granule - 1) / granule * granule;
   *cs = static_cast<int>(c);
   *n_wg = static_cast<int>(KVH * ((total_tiles + c - 1) / c + B));
 }
@@ -1746,7 +1837,7 @@ struct FlashWs {
 };
 FlashWs flash_ws_layout(int B, int H, int KVH, int T_c) {
   FlashWs w{};
-  flash::chunk_plan(B, KVH, T_c, &w.cs, &w.cpg);
+  flash::chunk_plan(B, KVH, T_c, &w.cs, &w.cpg, flash::rows_layout(KVH) ? flash::rows_per_round() : 0);
   const size_t chunks = static_cast<size_t>(B) * KVH * w.cpg;
   const int GH = H / KVH;
   size_t off = 0;
@@ -1845,7 +1936,9 @@ struct RaggedWs {
 };
 RaggedWs ragged_ws_layout(int B, int H, int KVH, long long total_tiles, int max_tiles) {
   RaggedWs w{};
-  flash::plan_ragged(B, KVH, total_tiles, max_tiles, &w.cs, &w.n_wg);
+  const bool rows = flash::rows_layout(KVH);
+  flash::plan_ragged(B, KVH, total_tiles, max_tiles, &w.cs, &w.n_wg, rows ? flash::rows_per_round() : 0,
+                     rows ? 1 : 4);
   const size_t chunks = static_cast<size_t>(w.n_wg);
   size_t off = 0;
   w.part = off;

@@ -47,7 +47,14 @@ hipError_t launch_prop_pass1(const void* q, const void* K, int dtype, int B, int
 // Chunking of a ragged batch with total_tiles tiles, the longest sequence
 // having max_tiles: cs tiles per chunk and an upper bound n_wg on the
 // workgroups of the ragged grid.
-void plan_ragged(int B, int KVH, long long total_tiles, int max_tiles, int* cs, int* n_wg);
+// per_round: work items per resident round (0: one per 4-wave workgroup
+// slot); granule: cs is a multiple of it for uneven lengths.
+void plan_ragged(int B, int KVH, long long total_tiles, int max_tiles, int* cs, int* n_wg, int per_round = 0,
+                 int granule = 4);
+// The flash tile pass's layout: one wave per KV head (ROWS) for KVH = 8, its
+// chunks planned for rows_per_round() items per round.
+bool rows_layout(int KVH);
+int rows_per_round();
 // The block_n = 256 online tile pass (the wave kernel) with its per-tile
 // statistics m, ell [B, H, T_c] and counts [B, H, T_c, 256] written out
 // (test hook; the chunk partials go to the santa_flash_decode workspace).
