@@ -933,9 +933,28 @@ __global__ __launch_bounds__(ROWS ? 512 : kThreads, ROWS ? 1 : 2) void wave_kern
   const int jrow = lane >> 4;
   const int qq = lane & 15;
   const uint64_t below = (1ull << lane) - 1ull;
+  // ROWS: waves w and w ^ 4 share a SIMD and the same tiles; the one that
+  // is behind takes the higher issue priority, so the pair ends together
+  // rather than one finishing with its SIMD half idle.
+  // (GH 8 has no LDS left for it and keeps the default priority.)
+  constexpr bool PRIO = ROWS && GH == 4;
+  __shared__ int s_prog[PRIO ? 8 : 1];
+  if constexpr (PRIO) {
+    if (lane == 0) s_prog[wave] = t_first;
+    __syncthreads();
+  }
   for (int t = t_first; t < t_end; t += TS) {
     const int n0 = t * BN;
     const int len = min(BN, L_valid - n0);
+    if constexpr (PRIO) {
+      if (lane == 0) s_prog[wave] = t;
+      const int partner = wave ^ 4;
+      if (partner < KVH && t < s_prog[partner]) {
+        __builtin_amdgcn_s_setprio(2);
+      } else {
+        __builtin_amdgcn_s_setprio(0);
+      }
+    }
 
     // ---- scores of the four sub-blocks -------------------------------------
     f32x4 sc[2][2][NHB];
