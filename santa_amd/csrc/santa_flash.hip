@@ -933,28 +933,35 @@ __global__ __launch_bounds__(ROWS ? 512 : kThreads, ROWS ? 1 : 2) void wave_kern
   const int jrow = lane >> 4;
   const int qq = lane & 15;
   const uint64_t below = (1ull << lane) - 1ull;
-  // ROWS: waves w and w ^ 4 share a SIMD and the same tiles; the one that
-  // is behind takes the higher issue priority, so the pair ends together
-  // rather than one finishing with its SIMD half idle.
+  // ROWS: waves w and w ^ 4 share a SIMD and walk the same tiles.  Left to
+  // the oldest-first issue order, waves 0-3 would end their loops about 14 us
+  // (at 32k tokens, 4 tiles per wave) before waves 4-7 and leave half of
+  // each SIMD idle meanwhile.  Each wave publishes a checkpoint count three times per
+  // tile (tile start, sub-block 2, scores done) and the one behind takes the
+  // higher issue priority.  (More checkpoints cost more in LDS waits than
+  // they balance.)
   // (GH 8 has no LDS left for it and keeps the default priority.)
   constexpr bool PRIO = ROWS && GH == 4;
   __shared__ int s_prog[PRIO ? 8 : 1];
   if constexpr (PRIO) {
-    if (lane == 0) s_prog[wave] = t_first;
+    if (lane == 0) s_prog[wave] = 0;
     __syncthreads();
   }
-  for (int t = t_first; t < t_end; t += TS) {
-    const int n0 = t * BN;
-    const int len = min(BN, L_valid - n0);
+  auto balance = [&](int c) {
     if constexpr (PRIO) {
-      if (lane == 0) s_prog[wave] = t;
-      const int partner = wave ^ 4;
-      if (partner < KVH && t < s_prog[partner]) {
+      if (lane == 0) s_prog[wave] = c;
+      const int pc = __builtin_amdgcn_readfirstlane(s_prog[wave ^ 4]);
+      if (c < pc) {
         __builtin_amdgcn_s_setprio(2);
       } else {
         __builtin_amdgcn_s_setprio(0);
       }
     }
+  };
+  for (int t = t_first; t < t_end; t += TS) {
+    const int n0 = t * BN;
+    const int len = min(BN, L_valid - n0);
+    balance(3 * (t - t_first));
 
     // ---- scores of the four sub-blocks -------------------------------------
     f32x4 sc[2][2][NHB];
@@ -982,6 +989,7 @@ __global__ __launch_bounds__(ROWS ? 512 : kThreads, ROWS ? 1 : 2) void wave_kern
         } else if constexpr (GH == 4) {
           load_k(t + TS, 1, pv_next);
         }
+        if (sb == 2) balance(3 * (t - t_first) + 1);
       }
       __builtin_amdgcn_wave_barrier();
       const int row = lane;
@@ -1014,6 +1022,7 @@ __global__ __launch_bounds__(ROWS ? 512 : kThreads, ROWS ? 1 : 2) void wave_kern
     // every row of the staging area has been read: the next tile's sub-block 0
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
     if (t + TS < t_end) dma_k(t + TS, pv_next);
+    balance(3 * (t - t_first) + 2);
 
     // ---- tile max per head (exact in any order) --------------------------------
     bool valid[2][2];
