@@ -1691,7 +1691,7 @@ hipError_t launch_expf(const float* x, float* y, size_t n, hipStream_t stream) {
 hipError_t launch_prop_pass1(const void* q, const void* K, int dtype, int B, int H, int KVH, int L, int L_storage,
                              int block_n, int path, float* m_tiles, float* ell_tiles, uint16_t* u_stash,
                              const int* seq_lens, int cs, int n_wg, int stash_ld, hipStream_t stream,
-                             PageTable pt) {
+                             PageTable pt, long long total_tiles) {
   Args a{q, K, nullptr, B, H, KVH, L, L_storage, (L + block_n - 1) / block_n, 0, 0, m_tiles, ell_tiles, nullptr,
          nullptr, nullptr, nullptr, nullptr, 0, 0, u_stash, seq_lens};
   a.pt = pt;
@@ -1705,20 +1705,40 @@ hipError_t launch_prop_pass1(const void* q, const void* K, int dtype, int B, int
   }
   const int GH = H / KVH;
   if (path == 0) {
-    // the vec path (GH 4, block_n 256) on the wave kernel
+    // the vec path (GH 4, block_n 256) on the wave kernel; for KVH = 8 in its
+    // rows form, with a plan of its own (pass 1 writes no chunk partials, so
+    // it need not share pass 2's chunking)
     const float q_scale = 1.0f / sqrtf(static_cast<float>(kD));
-    const unsigned grid = a.seq_lens ? static_cast<unsigned>(a.n_wg)
-                                     : static_cast<unsigned>(a.B) * static_cast<unsigned>(a.KVH) * static_cast<unsigned>(a.cpg);
+    const bool rows = rows_layout(a.KVH) && (!a.seq_lens || total_tiles >= 0);
+    if (rows) {
+      if (a.seq_lens) {
+        plan_ragged(a.B, a.KVH, total_tiles, a.T_c, &a.cs, &a.n_wg, rows_per_round(), 1);
+      } else {
+        chunk_plan(a.B, a.KVH, a.T_c, &a.cs, &a.cpg, rows_per_round());
+      }
+    }
+    unsigned grid = a.seq_lens ? static_cast<unsigned>(a.n_wg)
+                               : static_cast<unsigned>(a.B) * static_cast<unsigned>(a.KVH) * static_cast<unsigned>(a.cpg);
+    if (rows) grid /= static_cast<unsigned>(a.KVH);
     if (grid == 0) return hipSuccess;
-#define SANTA_P1_LAUNCH(BF, PG)                                                                                   \
-  hipLaunchKernelGGL((wave_kernel<BF, 4, false, true, PG>), dim3(grid), dim3(kThreads), 0, stream,                \
+    const dim3 block(rows ? static_cast<unsigned>(64 * a.KVH) : static_cast<unsigned>(kThreads));
+#define SANTA_P1_LAUNCH(BF, PG, RW)                                                                               \
+  hipLaunchKernelGGL((wave_kernel<BF, 4, false, true, PG, RW>), dim3(grid), block, 0, stream,                     \
                      static_cast<const uint16_t*>(a.q), static_cast<const uint16_t*>(a.K), nullptr, a.H, a.KVH,     \
                      a.L_valid, a.L_storage, a.T_c, a.cs, a.cpg, q_scale, 0, 0ULL, nullptr, nullptr, a.seq_lens,   \
                      a.B, 0LL, m_tiles, ell_tiles, nullptr, u_stash, stash_ld, a.pt)
     if (dtype == SANTA_BF16) {
-      if (a.pt.table) SANTA_P1_LAUNCH(true, true); else SANTA_P1_LAUNCH(true, false);
+      if (rows) {
+        if (a.pt.table) SANTA_P1_LAUNCH(true, true, true); else SANTA_P1_LAUNCH(true, false, true);
+      } else {
+        if (a.pt.table) SANTA_P1_LAUNCH(true, true, false); else SANTA_P1_LAUNCH(true, false, false);
+      }
     } else {
-      if (a.pt.table) SANTA_P1_LAUNCH(false, true); else SANTA_P1_LAUNCH(false, false);
+      if (rows) {
+        if (a.pt.table) SANTA_P1_LAUNCH(false, true, true); else SANTA_P1_LAUNCH(false, false, true);
+      } else {
+        if (a.pt.table) SANTA_P1_LAUNCH(false, true, false); else SANTA_P1_LAUNCH(false, false, false);
+      }
     }
 #undef SANTA_P1_LAUNCH
     return hipGetLastError();

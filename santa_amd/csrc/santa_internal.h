@@ -43,7 +43,7 @@ namespace flash {
 hipError_t launch_prop_pass1(const void* q, const void* K, int dtype, int B, int H, int KVH, int L, int L_storage,
                              int block_n, int path, float* m_tiles, float* ell_tiles, uint16_t* u_stash,
                              const int* seq_lens, int cs, int n_wg, int stash_ld, hipStream_t stream,
-                             PageTable pt = PageTable{nullptr, 0, 3, 1});
+                             PageTable pt = PageTable{nullptr, 0, 3, 1}, long long total_tiles = -1);
 // Chunking of a ragged batch with total_tiles tiles, the longest sequence
 // having max_tiles: cs tiles per chunk and an upper bound n_wg on the
 // workgroups of the ragged grid.

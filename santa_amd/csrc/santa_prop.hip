@@ -776,7 +776,7 @@ static int prop_decode_batched(const void* q, const void* K, const void* V, int 
   uint16_t* stash = reinterpret_cast<uint16_t*>(base + w.stash);
   const int sld = (pass1_path == 0) ? prop::stash_ld(L_storage) : 0;
   hipError_t e = flash::launch_prop_pass1(q, K, dtype, B, H, KVH, max_len, L_storage, block_n, pass1_path, m_tiles,
-                                          ell_tiles, stash, seq_lens, w.cs, w.n_wg, sld, stream, pt);
+                                          ell_tiles, stash, seq_lens, w.cs, w.n_wg, sld, stream, pt, total_tiles);
   if (e != hipSuccess) return set_error(SANTA_ERR_HIP, "pass-1 launch failed: %s", hipGetErrorString(e));
   if ((st = prop_budgets_launch(m_tiles, ell_tiles, B * H, H, T_c, 0, seed, m_star, S_tiles, inv, a0, stream, seq_lens,
                                 seq_S, block_n)) != SANTA_OK)
