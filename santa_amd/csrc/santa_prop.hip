@@ -24,6 +24,7 @@
 #include "santa_amd.h"
 #include "santa_internal.h"
 
+#include <algorithm>
 #include <cctype>
 #include <cfloat>
 #include <cstring>
@@ -33,30 +34,160 @@ namespace prop {
 
 constexpr int kD = 128;
 constexpr int kThreads = 256;
-constexpr int kBudgetThreads = 128;  // the reference's budget block (prop/santa_cuda_kernel.cu:904-915)
-constexpr int kMaxTiles = 4096;      // budgets keep frac, idx and S_t of every tile in LDS
+constexpr int kMaxTiles = 4096;  // budgets: 16 waves x 4 registers x 64 lanes
 
 // ---------------------------------------------------------------- budgets
-// prop/santa_cuda_kernel.cu:577-726, one workgroup per (b, h); the RNG key is
-// h (the reference's per-sequence call).  LDS: frac[T_c], idx[T_c], st[T_c].
-__global__ __launch_bounds__(kBudgetThreads) void budgets_kernel(const float* __restrict__ m_tiles,
-                                                                 const float* __restrict__ ell_tiles, int H, int T_c,
-                                                                 int S, uint64_t seed, float* __restrict__ m_star,
-                                                                 int* __restrict__ S_tiles,
-                                                                 float* __restrict__ invdelta,
-                                                                 float* __restrict__ a0_tile,
-                                                                 const int* __restrict__ seq_lens,
-                                                                 const int* __restrict__ seq_S, int BN) {
-  extern __shared__ float smem[];
-  float* frac = smem;
-  int* idx = reinterpret_cast<int*>(smem + T_c);
-  int* st = idx + T_c;
-  __shared__ float red[kBudgetThreads];
-  __shared__ int ired[kBudgetThreads];
+// prop/santa_cuda_kernel.cu:577-726, one workgroup of NW waves per (b, h);
+// the RNG key is h (the reference's per-sequence call).  Tile (and network
+// position) p = NT r + tid lives in register r of thread tid (NT = 64 NW
+// threads, R registers: every tile of the launch's longest sequence).
+//  * m* = max_t m_t: exact in any order.
+//  * Z keeps the association of 128 partial sums (partial i over tiles i,
+//    i + 128, ... ascending, read back from LDS), then a pairwise tree
+//    red[i] += red[i + s] for s = 64 .. 1 (s = 64 through LDS, the rest as
+//    lane shifts of wave 0).
+//  * The bitonic network (:686-707) runs as the reference's sequence of
+//    compare-exchange steps over N = next power of two >= T_c; each element
+//    takes its own side of every exchange (the pair's lower index decides
+//    the swap), elements at positions >= T_c stay (-inf, -1), which is the
+//    reference's "reads past T_c see (-inf, -1), writes are dropped".
+//    Exchanges at distance < 64 are between lanes of a wave (DPP within
+//    16-lane rows, LDS permutes across them), at distance < NT between
+//    waves (through LDS, between two barriers), and at larger distances
+//    between registers of one thread.
 
+// The value of lane (lane ^ J): DPP inside 16-lane rows (quad permutes for
+// 1 and 2; row shifts up or down for 4 and 8, picked by the lane's bit J),
+// an LDS permute across rows.
+template <int J>
+__device__ __forceinline__ int lane_xor(int v, int lane) {
+  if constexpr (J == 1) {
+    return __builtin_amdgcn_update_dpp(0, v, kDppQuadXor1, 0xF, 0xF, false);
+  } else if constexpr (J == 2) {
+    return __builtin_amdgcn_update_dpp(0, v, kDppQuadXor2, 0xF, 0xF, false);
+  } else if constexpr (J == 4 || J == 8) {
+    const int from_above = __builtin_amdgcn_update_dpp(0, v, 0x100 + J, 0xF, 0xF, true);  // lane + J
+    const int from_below = __builtin_amdgcn_update_dpp(0, v, 0x110 + J, 0xF, 0xF, true);  // lane - J
+    return (lane & J) ? from_below : from_above;
+  } else {
+    return __shfl_xor(v, J, 64);
+  }
+}
+
+// One compare-exchange step given each element's partner value (of, oi):
+// the pair's lower position decides, with up = (position & k) != 0.
+template <int NT, int R>
+__device__ __forceinline__ void bitonic_apply(float (&f)[R], int (&id)[R], const float (&of)[R], const int (&oi)[R],
+                                              int j, int k, int T_c, int tid) {
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const int p = NT * r + tid;
+    const bool lo = (p & j) == 0;
+    const bool up = (p & k) != 0;
+    const float alo = lo ? f[r] : of[r];
+    const float ahi = lo ? of[r] : f[r];
+    const bool sw = (p < T_c) && ((alo > ahi) == up);
+    f[r] = sw ? of[r] : f[r];
+    id[r] = sw ? oi[r] : id[r];
+  }
+}
+
+template <int NT, int R, int J>
+__device__ __forceinline__ void bitonic_lanes(float (&f)[R], int (&id)[R], int k, int T_c, int tid) {
+  // every exchange of the step is issued before the first is used
+  float of[R];
+  int oi[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    of[r] = __int_as_float(lane_xor<J>(__float_as_int(f[r]), tid & 63));
+    oi[r] = lane_xor<J>(id[r], tid & 63);
+  }
+  bitonic_apply<NT, R>(f, id, of, oi, J, k, T_c, tid);
+}
+
+template <int NT, int R, int JR>
+__device__ __forceinline__ void bitonic_regs(float (&f)[R], int (&id)[R], int k, int T_c, int tid) {
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    if (r & JR) continue;
+    const int rh = r | JR;
+    const int plo = NT * r + tid;
+    const int phi = NT * rh + tid;
+    const bool up = (plo & k) != 0;
+    const float alo = f[r], ahi = f[rh];
+    const int ilo = id[r], ihi = id[rh];
+    const bool sw = (alo > ahi) == up;
+    const bool wlo = plo < T_c && sw;
+    const bool whi = phi < T_c && sw;
+    f[r] = wlo ? ahi : alo;
+    id[r] = wlo ? ihi : ilo;
+    f[rh] = whi ? alo : ahi;
+    id[rh] = whi ? ilo : ihi;
+  }
+}
+
+template <int NW, int R>
+__device__ __forceinline__ void bitonic_desc(float (&f)[R], int (&id)[R], int T_c, int tid, float* s_f, int* s_i) {
+  constexpr int NT = 64 * NW;
+  int N = 1;
+  while (N < T_c) N <<= 1;
+  for (int k = 2; k <= N; k <<= 1) {
+    for (int j = k >> 1; j > 0; j >>= 1) {
+      if (j < 64) {
+        switch (j) {
+          case 1: bitonic_lanes<NT, R, 1>(f, id, k, T_c, tid); break;
+          case 2: bitonic_lanes<NT, R, 2>(f, id, k, T_c, tid); break;
+          case 4: bitonic_lanes<NT, R, 4>(f, id, k, T_c, tid); break;
+          case 8: bitonic_lanes<NT, R, 8>(f, id, k, T_c, tid); break;
+          case 16: bitonic_lanes<NT, R, 16>(f, id, k, T_c, tid); break;
+          default: bitonic_lanes<NT, R, 32>(f, id, k, T_c, tid); break;
+        }
+      } else if (j < NT) {
+        if constexpr (NW > 1) {
+          __syncthreads();  // the previous exchange's reads are done
+#pragma unroll
+          for (int r = 0; r < R; ++r) {
+            s_f[NT * r + tid] = f[r];
+            s_i[NT * r + tid] = id[r];
+          }
+          __syncthreads();
+          float of[R];
+          int oi[R];
+#pragma unroll
+          for (int r = 0; r < R; ++r) {
+            of[r] = s_f[(NT * r + tid) ^ j];
+            oi[r] = s_i[(NT * r + tid) ^ j];
+          }
+          bitonic_apply<NT, R>(f, id, of, oi, j, k, T_c, tid);
+        }
+      } else {
+        const int jr = j / NT;
+        if constexpr (R > 1) if (jr == 1) bitonic_regs<NT, R, 1>(f, id, k, T_c, tid);
+        if constexpr (R > 2) if (jr == 2) bitonic_regs<NT, R, 2>(f, id, k, T_c, tid);
+        if constexpr (R > 4) if (jr == 4) bitonic_regs<NT, R, 4>(f, id, k, T_c, tid);
+      }
+    }
+  }
+}
+
+template <int NW, int R>
+__global__ __launch_bounds__(64 * NW) void budgets_kernel(const float* __restrict__ m_tiles,
+                                                          const float* __restrict__ ell_tiles, int H, int T_c, int S,
+                                                          uint64_t seed, float* __restrict__ m_star,
+                                                          int* __restrict__ S_tiles, float* __restrict__ invdelta,
+                                                          float* __restrict__ a0_tile, const int* __restrict__ seq_lens,
+                                                          const int* __restrict__ seq_S, int BN) {
+  constexpr int NT = 64 * NW;
+  __shared__ float s_f[NT * R];  // W_t, then the network's exchanges
+  __shared__ int s_i[NT * R];    // the network's exchanges, then the +1 flags
+  __shared__ float s_z[128];
+  __shared__ float s_red[NW];
+  __shared__ int s_ired[NW];
   const int bh = static_cast<int>(blockIdx.x);
   const int h = bh % H;
   const int tid = static_cast<int>(threadIdx.x);
+  const int lane = tid & 63;
+  const int wv = tid >> 6;
   const size_t off = static_cast<size_t>(bh) * T_c;  // T_c: tile stride of the [B, H, T_c] arrays
   // ragged batches: this sequence's tile count and budget
   if (seq_lens) T_c = (ragged_len(seq_lens, bh / H, T_c * BN) + BN - 1) / BN;
@@ -64,113 +195,119 @@ __global__ __launch_bounds__(kBudgetThreads) void budgets_kernel(const float* __
   const float* mt = m_tiles + off;
   const float* lt = ell_tiles + off;
 
-  // m* = max_t m_t (exact in any order); -FLT_MAX start as in :597
-  float lm = -FLT_MAX;
-  for (int t = tid; t < T_c; t += kBudgetThreads) lm = fmaxf(lm, mt[t]);
-  red[tid] = lm;
-  __syncthreads();
-  for (int s = kBudgetThreads / 2; s > 0; s >>= 1) {
-    if (tid < s) red[tid] = fmaxf(red[tid], red[tid + s]);
-    __syncthreads();
+  float mv[R], lv[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const int t = NT * r + tid;
+    mv[r] = (t < T_c) ? mt[t] : 0.0f;
+    lv[r] = (t < T_c) ? lt[t] : 0.0f;
   }
-  const float ms = red[0];
+  // m* = max_t m_t (exact in any order); -FLT_MAX start as in :597
+  float ms = -FLT_MAX;
+#pragma unroll
+  for (int r = 0; r < R; ++r)
+    if (NT * r + tid < T_c) ms = fmaxf(ms, mv[r]);
+#pragma unroll
+  for (int s = 32; s > 0; s >>= 1) ms = fmaxf(ms, __shfl_xor(ms, s, 64));
+  if (lane == 0) s_red[wv] = ms;
   __syncthreads();
+  ms = s_red[0];
+#pragma unroll
+  for (int i = 1; i < NW; ++i) ms = fmaxf(ms, s_red[i]);
   if (tid == 0 && m_star) m_star[bh] = ms;
 
-  // W_t and Z in the fixed order
-  float z = 0.0f;
-  for (int t = tid; t < T_c; t += kBudgetThreads) {
-    const float wt = santa_expf(mt[t] - ms) * lt[t];
-    frac[t] = wt;
-    z += wt;
+  // W_t, then Z in the fixed order
+  float w[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const int t = NT * r + tid;
+    w[r] = 0.0f;
+    if (t < T_c) {
+      w[r] = santa_expf(mv[r] - ms) * lv[r];
+      s_f[t] = w[r];
+    }
   }
-  red[tid] = z;
   __syncthreads();
-  for (int s = kBudgetThreads / 2; s > 0; s >>= 1) {
-    if (tid < s) red[tid] = red[tid] + red[tid + s];
-    __syncthreads();
+  for (int tau = tid; tau < 128; tau += NT) {
+    float z = 0.0f;
+    for (int t = tau; t < T_c; t += 128) z += s_f[t];
+    s_z[tau] = z;
   }
-  const float Z = red[0];
+  __syncthreads();
+  if (wv == 0) {
+    float z = s_z[lane] + s_z[lane + 64];
+#pragma unroll
+    for (int s = 32; s > 0; s >>= 1) z = z + __shfl_down(z, s, 64);
+    if (lane == 0) s_z[0] = z;
+  }
+  __syncthreads();
+  const float Z = s_z[0];
 
   if (S <= 0 || !(Z > 0.0f)) {
-    for (int t = tid; t < T_c; t += kBudgetThreads) {
-      S_tiles[off + t] = 0;
-      invdelta[off + t] = 0.0f;
-      a0_tile[off + t] = u01(seed, h, t);
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const int t = NT * r + tid;
+      if (t < T_c) {
+        S_tiles[off + t] = 0;
+        invdelta[off + t] = 0.0f;
+        a0_tile[off + t] = u01(seed, h, t);
+      }
     }
     return;
   }
 
   // integer bases and jittered fractional parts (:662-678)
+  int bt[R], id[R];
+  float f[R];
   int base = 0;
-  for (int t = tid; t < T_c; t += kBudgetThreads) {
-    const float q = static_cast<float>(S) * (frac[t] / Z);
-    const float fq = floorf(q);
-    const int bt = (fq != fq) ? 0 : (fq >= 2147483648.0f ? 2147483647 : static_cast<int>(fq));
-    st[t] = bt;
-    base += bt;
-    const float ft = q - static_cast<float>(bt);
-    const float jitter = 1.0e-7f * u01(seed, h, t);
-    frac[t] = ft + jitter;
-    idx[t] = t;
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const int t = NT * r + tid;
+    bt[r] = 0;
+    f[r] = -__builtin_inff();
+    id[r] = -1;
+    if (t < T_c) {
+      const float q = static_cast<float>(S) * (w[r] / Z);
+      const float fq = floorf(q);
+      bt[r] = (fq != fq) ? 0 : (fq >= 2147483648.0f ? 2147483647 : static_cast<int>(fq));
+      base += bt[r];
+      const float ft = q - static_cast<float>(bt[r]);
+      const float jitter = 1.0e-7f * u01(seed, h, t);
+      f[r] = ft + jitter;
+      id[r] = t;
+    }
   }
-  ired[tid] = base;
+#pragma unroll
+  for (int s = 32; s > 0; s >>= 1) base += __shfl_xor(base, s, 64);
+  if (lane == 0) s_ired[wv] = base;
   __syncthreads();
-  for (int s = kBudgetThreads / 2; s > 0; s >>= 1) {
-    if (tid < s) ired[tid] += ired[tid + s];
-    __syncthreads();
-  }
-  int rem = S - ired[0];
+  base = 0;
+#pragma unroll
+  for (int i = 0; i < NW; ++i) base += s_ired[i];
+  int rem = S - base;
   if (rem < 0) rem = 0;
   if (rem > T_c) rem = T_c;
 
-  // bitonic network over N = next power of two >= T_c, descending; reads
-  // past T_c see (-inf, -1) and writes past T_c are dropped (:686-707)
-  int N = 1;
-  while (N < T_c) N <<= 1;
-  for (int k = 2; k <= N; k <<= 1) {
-    for (int j = k >> 1; j > 0; j >>= 1) {
-      for (int i = tid; i < N; i += kBudgetThreads) {
-        const int ixj = i ^ j;
-        if (ixj > i) {
-          const bool up = (i & k) != 0;
-          float ai = (i < T_c) ? frac[i] : -__builtin_inff();
-          float aj = (ixj < T_c) ? frac[ixj] : -__builtin_inff();
-          int ii = (i < T_c) ? idx[i] : -1;
-          int ij = (ixj < T_c) ? idx[ixj] : -1;
-          if ((ai > aj) == up) {
-            const float tf = ai;
-            ai = aj;
-            aj = tf;
-            const int ti = ii;
-            ii = ij;
-            ij = ti;
-          }
-          if (i < T_c) {
-            frac[i] = ai;
-            idx[i] = ii;
-          }
-          if (ixj < T_c) {
-            frac[ixj] = aj;
-            idx[ixj] = ij;
-          }
-        }
-      }
-      __syncthreads();
-    }
-  }
+  bitonic_desc<NW, R>(f, id, T_c, tid, s_f, s_i);
+
   // +1 to the top `rem` (distinct tiles, :710-716)
-  for (int r = tid; r < rem; r += kBudgetThreads) {
-    const int best = idx[r];
-    if (best >= 0) st[best] += 1;
-  }
+  __syncthreads();  // the network's last reads of s_i are done
+#pragma unroll
+  for (int r = 0; r < R; ++r) s_i[NT * r + tid] = 0;
   __syncthreads();
-  for (int t = tid; t < T_c; t += kBudgetThreads) {
-    const float ell = lt[t];
-    const int s_t = st[t];
-    S_tiles[off + t] = s_t;
-    invdelta[off + t] = (s_t > 0 && ell > 1e-20f) ? (static_cast<float>(s_t) / ell) : 0.0f;
-    a0_tile[off + t] = u01(seed, h, t);
+#pragma unroll
+  for (int r = 0; r < R; ++r)
+    if (NT * r + tid < rem && id[r] >= 0) s_i[id[r]] = 1;
+  __syncthreads();
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const int t = NT * r + tid;
+    if (t < T_c) {
+      const int s_t = bt[r] + s_i[t];
+      S_tiles[off + t] = s_t;
+      invdelta[off + t] = (s_t > 0 && lv[r] > 1e-20f) ? (static_cast<float>(s_t) / lv[r]) : 0.0f;
+      a0_tile[off + t] = u01(seed, h, t);
+    }
   }
 }
 
@@ -425,14 +562,32 @@ __global__ __launch_bounds__(kD) void finalize_kernel(const float* __restrict__ 
   }
   if (seq_S) scale_out = (seq_S[b] > 0) ? (1.0f / static_cast<float>(seq_S[b])) : 0.0f;
   const float* pb = part + ((static_cast<size_t>(base) + kv) * GH + g) * kD + d;
+  const size_t cstride = static_cast<size_t>(KVH) * GH * kD;
+  // chunks in ascending order; the loads of a batch of 16 are issued before
+  // the first add (one memory round trip per batch, not one per chunk)
+  constexpr int kBatch = 16;
+  const bool emit = vrows && g == 0 && d == 0;
   float s = 0.0f;
-  for (int c = 0; c < nch; ++c) s += pb[static_cast<size_t>(c) * KVH * GH * kD];
-  out[static_cast<size_t>(bh) * kD + d] = f32_to_h16<BF16>(s * scale_out);
-  if (vrows && g == 0 && d == 0) {
-    int e = 0;
-    for (int c = 0; c < nch; ++c) e += part_emit[static_cast<size_t>(base) + c * KVH + kv];
-    vrows[bk] = e;
+  int e = 0;
+  for (int c0 = 0; c0 < nch; c0 += kBatch) {
+    float v[kBatch];
+    int ev[kBatch];
+#pragma unroll
+    for (int i = 0; i < kBatch; ++i) {
+      const int c = min(c0 + i, nch - 1);
+      v[i] = pb[static_cast<size_t>(c) * cstride];
+      ev[i] = emit ? part_emit[static_cast<size_t>(base) + c * KVH + kv] : 0;
+    }
+#pragma unroll
+    for (int i = 0; i < kBatch; ++i) {
+      if (c0 + i < nch) {
+        s += v[i];
+        e += ev[i];
+      }
+    }
   }
+  out[static_cast<size_t>(bh) * kD + d] = f32_to_h16<BF16>(s * scale_out);
+  if (emit) vrows[bk] = e;
 }
 
 // Grid: B * KVH * cpg workgroups (uniform) or n_wg (ragged, seq_lens set).
@@ -611,9 +766,24 @@ static int prop_budgets_launch(const float* m_tiles, const float* ell_tiles, int
                                uint64_t seed, float* m_star, int* S_tiles, float* invdelta, float* a0,
                                hipStream_t stream, const int* seq_lens = nullptr, const int* seq_S = nullptr,
                                int block_n = 0) {
-  const size_t shmem = static_cast<size_t>(T_c) * (2 * sizeof(float) + sizeof(int));
-  hipLaunchKernelGGL(prop::budgets_kernel, dim3(BH), dim3(prop::kBudgetThreads), shmem, stream, m_tiles, ell_tiles, H,
-                     T_c, S, seed, m_star, S_tiles, invdelta, a0, seq_lens, seq_S, block_n);
+  // waves per (b, h) and registers per thread for every tile of the longest
+  // sequence (T_c <= kMaxTiles): two registers a thread, up to 16 waves
+  int N = 1;
+  while (N < T_c) N <<= 1;
+  const int NW = std::min(16, std::max(1, N / 128));
+  const int R = std::max(1, N / (64 * NW));
+#define SANTA_BUDGETS(W, RR)                                                                                      \
+  hipLaunchKernelGGL((prop::budgets_kernel<W, RR>), dim3(BH), dim3(64 * W), 0, stream, m_tiles, ell_tiles, H, T_c, \
+                     S, seed, m_star, S_tiles, invdelta, a0, seq_lens, seq_S, block_n)
+  if (NW == 1 && R == 1) SANTA_BUDGETS(1, 1);
+  else if (NW == 1 && R == 2) SANTA_BUDGETS(1, 2);
+  else if (NW == 2 && R == 2) SANTA_BUDGETS(2, 2);
+  else if (NW == 4 && R == 2) SANTA_BUDGETS(4, 2);
+  else if (NW == 8 && R == 2) SANTA_BUDGETS(8, 2);
+  else if (NW == 16 && R == 2) SANTA_BUDGETS(16, 2);
+  else if (NW == 16 && R == 4) SANTA_BUDGETS(16, 4);
+  else return set_error(SANTA_ERR_UNSUPPORTED, "too many tiles per sequence: T_c=%d (max %d)", T_c, prop::kMaxTiles);
+#undef SANTA_BUDGETS
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess) return set_error(SANTA_ERR_HIP, "budget launch failed: %s", hipGetErrorString(e));
   return SANTA_OK;
