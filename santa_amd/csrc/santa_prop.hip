@@ -429,8 +429,8 @@ __global__ __launch_bounds__(kThreads) void pass2_kernel(const uint16_t* __restr
   };
 
   // stash entries of tile t for this lane's rows: u[k][p][0/1]
-  uint16_t un0[HPW][NPAIR], un1[HPW][NPAIR];
-  auto load_u = [&](int t) {
+  using UBuf = uint16_t[HPW][NPAIR];
+  auto load_u = [&](int t, UBuf& un0, UBuf& un1) {
     const int n0 = t * BN;
     const int len = min(BN, L - n0);
 #pragma unroll
@@ -451,25 +451,45 @@ __global__ __launch_bounds__(kThreads) void pass2_kernel(const uint16_t* __restr
       }
     }
   };
-  if (t_begin < t_end) load_u(t_begin);
+  // The chunk's per-tile terms invdelta_t and a0_t, one tile per lane (64
+  // tiles at a time), so that no tile waits on a load of its own.
+  float inv_l[HPW], a0_l[HPW];
+  auto load_terms = [&](int t0) {
+    const int tt = min(t0 + lane, t_end - 1);
+#pragma unroll
+    for (int k = 0; k < HPW; ++k) {
+      const size_t ht = (static_cast<size_t>(b) * H + h0 + wave + 4 * k) * T_c + tt;
+      inv_l[k] = invdelta[ht];
+      a0_l[k] = a0_tile[ht];
+    }
+  };
+  // Stash entries two tiles ahead: tiles alternate between two buffers, and
+  // a buffer is refilled with tile t + 2 as soon as tile t has read it.
+  UBuf ua0, ua1, ub0, ub1;
+  if (t_begin < t_end) {
+    load_u(t_begin, ua0, ua1);
+    if (t_begin + 1 < t_end) load_u(t_begin + 1, ub0, ub1);
+    load_terms(t_begin);
+  }
 
-  for (int t = t_begin; t < t_end; ++t) {
+  auto tile_step = [&](int t, UBuf& un0, UBuf& un1) {
     const int n0 = t * BN;
     const int len = min(BN, L - n0);
     const int par = (t - t_begin) & 1;
+    const int li = (t - t_begin) & 63;
+    if (li == 0 && t != t_begin) load_terms(t);
     float x0[HPW][NPAIR], x1[HPW][NPAIR], inv[HPW], a0v[HPW];
 #pragma unroll
     for (int k = 0; k < HPW; ++k) {
-      const size_t ht = (static_cast<size_t>(b) * H + h0 + wave + 4 * k) * T_c + t;
-      inv[k] = invdelta[ht];
-      a0v[k] = a0_tile[ht];
+      inv[k] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(inv_l[k]), li));
+      a0v[k] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(a0_l[k]), li));
 #pragma unroll
       for (int p = 0; p < NPAIR; ++p) {
         x0[k][p] = (inv[k] > 0.0f) ? h16_to_f32<BF16>(un0[k][p]) * inv[k] : 0.0f;
         x1[k][p] = (inv[k] > 0.0f) ? h16_to_f32<BF16>(un1[k][p]) * inv[k] : 0.0f;
       }
     }
-    if (t + 1 < t_end) load_u(t + 1);
+    if (t + 2 < t_end) load_u(t + 2, un0, un1);
 
 #pragma unroll
     for (int k = 0; k < HPW; ++k) {
@@ -521,6 +541,10 @@ __global__ __launch_bounds__(kThreads) void pass2_kernel(const uint16_t* __restr
       __syncthreads();
       if (wave == 0) emit_total += union_rows<GH, NM>(s_mask[par], lane);
     }
+  };
+  for (int t = t_begin; t < t_end; t += 2) {
+    tile_step(t, ua0, ua1);
+    if (t + 1 < t_end) tile_step(t + 1, ub0, ub1);
   }
 
 #pragma unroll
