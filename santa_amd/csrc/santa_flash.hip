@@ -934,13 +934,13 @@ __global__ __launch_bounds__(ROWS ? 512 : kThreads, ROWS ? 1 : 2) void wave_kern
   const int qq = lane & 15;
   const uint64_t below = (1ull << lane) - 1ull;
   // ROWS: waves w and w ^ 4 share a SIMD and walk the same tiles.  Left to
-  // the oldest-first issue order, waves 0-3 would end their loops about 14 us
-  // (at 32k tokens, 4 tiles per wave) before waves 4-7 and leave half of
-  // each SIMD idle meanwhile.  Each wave publishes a checkpoint count three times per
-  // tile (tile start, sub-block 2, scores done) and the one behind takes the
-  // higher issue priority.  (More checkpoints cost more in LDS waits than
-  // they balance.)
-  // (GH 8 has no LDS left for it and keeps the default priority.)
+  // the oldest-first issue order, waves 0-3 would end their loops about
+  // 14 us (at 32k tokens, 4 tiles per wave) before waves 4-7 and leave half
+  // of each SIMD idle meanwhile.  Each wave publishes a checkpoint count
+  // three times per tile (tile start, sub-block 2, scores done) and the one
+  // behind takes the higher issue priority.  (More checkpoints cost more in
+  // LDS waits than they balance.)  GH 8 has no LDS left for the counts and
+  // keeps the default priority.
   constexpr bool PRIO = ROWS && GH == 4;
   __shared__ int s_prog[PRIO ? 8 : 1];
   if constexpr (PRIO) {
