@@ -1559,6 +1559,14 @@ static hipError_t launch_wave_t(const Args& a, float* dbg_m, float* dbg_ell, int
   if (grid == 0) return hipSuccess;
   if (dbg_counts) {
     if (a.pt.table) return hipErrorInvalidValue;  // the statistics check reads contiguous caches
+    if (rows_layout(a.KVH)) {  // the production layout, with the statistics written out
+      hipLaunchKernelGGL((wave_kernel<BF16, GH, true, false, false, true>), dim3(grid / static_cast<unsigned>(a.KVH)),
+                         dim3(static_cast<unsigned>(64 * a.KVH)), 0, stream, static_cast<const uint16_t*>(a.q),
+                         static_cast<const uint16_t*>(a.K), static_cast<const uint16_t*>(a.V), a.H, a.KVH, a.L_valid,
+                         a.L_storage, a.T_c, a.cs, a.cpg, q_scale, a.S_pt, a.seed, a.part, a.part_emit, a.seq_lens,
+                         a.B, a.S_total, dbg_m, dbg_ell, dbg_counts, nullptr, 0, a.pt);
+      return hipGetLastError();
+    }
     hipLaunchKernelGGL((wave_kernel<BF16, GH, true>), dim3(grid), dim3(kThreads), 0, stream,
                        static_cast<const uint16_t*>(a.q), static_cast<const uint16_t*>(a.K),
                        static_cast<const uint16_t*>(a.V), a.H, a.KVH, a.L_valid, a.L_storage, a.T_c, a.cs, a.cpg,

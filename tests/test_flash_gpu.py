@@ -172,11 +172,15 @@ def test_device_expf_matches_oracle():
         (1, 32, 8, 2048, 100000, -1, torch.bfloat16),  # lists overflow inside a tile
         (2, 32, 8, 32768, 256, -1, torch.bfloat16),    # several tiles per wave, cfg2 rows
         (2, 32, 8, 6000, 300, -1, torch.float16),
+        (2, 16, 4, 9000, 256, -1, torch.bfloat16),     # KVH 4: the four-wave layout
+        (1, 8, 2, 5000, 64, 4500, torch.bfloat16),     # KVH 2, valid_len < storage
     ],
 )
 def test_wave_kernel_statistics(B, H, KVH, L, S, valid_len, dtype):
     """The block_n=256 production kernel: tile max, tile mass and every count
-    bit-exact to the oracle, read back through its debug outputs."""
+    bit-exact to the oracle, read back through its debug outputs (in the
+    production layout: eight waves per (sequence, chunk) for KVH = 8, four
+    waves per (sequence, KV head, chunk) otherwise)."""
     _announce(f"wave kernel B={B} H={H} KVH={KVH} L={L} S={S} valid_len={valid_len} {dtype}")
     m = _mod()
     q, K, V = gen_qkv(B, H, KVH, L, seed=SEED + 7 * B + L, dtype=dtype, lowrank=0.5)
