@@ -205,3 +205,58 @@ def test_wave_kernel_statistics(B, H, KVH, L, S, valid_len, dtype):
     ref = estimator_given_counts(mt, lt, cnt, Vd, S, valid_len if valid_len > 0 else L)
     ok, mabs, mrel = tol_check(got, ref.to(dtype).float().numpy())
     assert ok, ("vs torch estimator", mabs, mrel)
+
+
+def test_headline_workload_parity():
+    """The benchmark's own workload (B=8, 32q/8kv, L=32768, S=256, seed 1690,
+    the rank-4 key bias recipe -- bench.py's make_inputs draws the same
+    tensors): the production wave kernel's tile max, tile mass and every count
+    bit-exact to the oracle, m* and vrows of the production call exact, its
+    output within the bf16 tolerance (max abs 2e-2, mean rel 1e-3)."""
+    B, H, KVH, L, S = 8, 32, 8, 32768, 256
+    _announce(f"headline workload B={B} H={H} KVH={KVH} L={L} S={S} seed={SEED}")
+    m = _mod()
+    q, K, V = gen_qkv(B, H, KVH, L, seed=SEED, lowrank=0.5)
+    dev = torch.device("cuda:0")
+    qd, Kd, Vd = q.to(dev), K.to(dev), V.to(dev)
+    mt, lt, cnt = m._debug_wave(qd, Kd, Vd, S, seed=SEED, valid_len=-1)
+    out, ms, vr = m.decode_systematic_batched(qd, Kd, Vd, S, seed=SEED, want_vrows=True)
+    torch.cuda.synchronize()
+    exp = oracle.flash_decode(q, K, V, S, seed=SEED, block_n=256, is_bf16=True, debug=True)
+    np.testing.assert_array_equal(mt.cpu().numpy().view(np.uint32), exp["m_tiles"].view(np.uint32), err_msg="m_tiles")
+    np.testing.assert_array_equal(lt.cpu().numpy().view(np.uint32), exp["ell_tiles"].view(np.uint32),
+                                  err_msg="ell_tiles")
+    c_gpu = cnt.cpu().numpy()
+    assert np.array_equal(c_gpu, exp["counts"]), f"counts differ at {np.argwhere(c_gpu != exp['counts'])[:8]}"
+    np.testing.assert_array_equal(ms.cpu().numpy().view(np.uint32), exp["m_star"].view(np.uint32), err_msg="m_star")
+    np.testing.assert_array_equal(vr.cpu().numpy(), exp["vrows"], err_msg="vrows")
+    ok, mabs, mrel = tol_check(h16_to_f32(bits16(out)), h16_to_f32(exp["out16"]))
+    assert ok, ("vs oracle", mabs, mrel)
+
+
+def test_cfg5_shape_parity():
+    """cfg5's per-sequence shape and key recipe (64q/8kv so GH 8, L=131072,
+    S=512, Student-t(3) keys with planted needles, bench.device_inputs) on 4
+    of its 32 sequences: the production (rows form, GH 8) tile max, tile mass
+    and every count bit-exact to the oracle, m* and vrows exact, output
+    within the bf16 tolerance."""
+    import bench
+
+    B, H, KVH, L, S = 4, 64, 8, 131072, 512
+    _announce(f"cfg5 shape B={B} H={H} KVH={KVH} L={L} S={S} needles seed={SEED}")
+    m = _mod()
+    dev = torch.device("cuda:0")
+    qd, Kd, Vd = bench.device_inputs(B, L, H, KVH, 128, SEED, dev, keys="needles")
+    mt, lt, cnt = m._debug_wave(qd, Kd, Vd, S, seed=SEED, valid_len=-1)
+    out, ms, vr = m.decode_systematic_batched(qd, Kd, Vd, S, seed=SEED, want_vrows=True)
+    torch.cuda.synchronize()
+    exp = oracle.flash_decode(qd.cpu(), Kd.cpu(), Vd.cpu(), S, seed=SEED, block_n=256, is_bf16=True, debug=True)
+    np.testing.assert_array_equal(mt.cpu().numpy().view(np.uint32), exp["m_tiles"].view(np.uint32), err_msg="m_tiles")
+    np.testing.assert_array_equal(lt.cpu().numpy().view(np.uint32), exp["ell_tiles"].view(np.uint32),
+                                  err_msg="ell_tiles")
+    c_gpu = cnt.cpu().numpy()
+    assert np.array_equal(c_gpu, exp["counts"]), f"counts differ at {np.argwhere(c_gpu != exp['counts'])[:8]}"
+    np.testing.assert_array_equal(ms.cpu().numpy().view(np.uint32), exp["m_star"].view(np.uint32), err_msg="m_star")
+    np.testing.assert_array_equal(vr.cpu().numpy(), exp["vrows"], err_msg="vrows")
+    ok, mabs, mrel = tol_check(h16_to_f32(bits16(out)), h16_to_f32(exp["out16"]))
+    assert ok, ("vs oracle", mabs, mrel)

@@ -131,3 +131,32 @@ def test_prop_batched_errors(monkeypatch):
     with pytest.raises(RuntimeError, match=r"\[B, L, KVH, D\]"):
         nc = Kd.transpose(0, 1).contiguous().transpose(0, 1)
         m.decode_systematic_batched(qd, nc, nc, 10)
+
+
+def test_cfg3_workload_parity():
+    """The benchmark's batched ragged workload at full size (bench.py
+    --workload cfg3: B=16, 32q/8kv, L_b seeded in [8192, 131072], S_b = L_b //
+    64, inputs drawn on the device by bench.device_inputs): every sequence's
+    m* and vrows exact against the CPU oracle of the per-sequence call, the
+    output within the bf16 tolerance (max abs 2e-2, mean rel 1e-3)."""
+    import bench
+    import santa_prop_batch_cuda as m
+
+    B, H, KVH, D = 16, 32, 8, 128
+    gl = torch.Generator().manual_seed(SEED)
+    lens = torch.randint(8192, 131072 + 1, (B,), generator=gl).tolist()
+    Ss = [l // 64 for l in lens]
+    print(f"\n[case] prop cfg3 workload B={B} lens={lens} S={Ss} seed={SEED}", flush=True)
+    dev = torch.device("cuda:0")
+    q, K, V = bench.device_inputs(B, max(lens), H, KVH, D, SEED, dev)
+    out, ms, vr = m.decode_systematic_batched(q, K, V, Ss, seed=SEED, want_vrows=True, valid_len=lens)
+    torch.cuda.synchronize()
+    qc, Kc, Vc = q.cpu(), K.cpu(), V.cpu()
+    del K, V
+    for b, (Lb, Sb) in enumerate(zip(lens, Ss)):
+        exp = oracle.prop_decode(qc[b], Kc[b, :Lb], Vc[b, :Lb], Sb, seed=SEED, debug=True)
+        np.testing.assert_array_equal(ms[b].cpu().numpy().view(np.uint32), exp["m_star"].view(np.uint32),
+                                      err_msg=f"m_star b={b}")
+        np.testing.assert_array_equal(vr[b].cpu().numpy(), exp["vrows"], err_msg=f"vrows b={b}")
+        ok, mabs, mrel = tol_check(h16_to_f32(bits16(out[b])), h16_to_f32(exp["out16"]))
+        assert ok, (f"b={b} vs oracle", mabs, mrel)
