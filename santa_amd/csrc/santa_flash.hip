@@ -940,7 +940,7 @@ __global__ __launch_bounds__(ROWS ? 512 : kThreads, ROWS ? 1 : 2) void wave_kern
   // three times per tile (tile start, sub-block 2, scores done) and the one
   // behind takes the higher issue priority.  (More checkpoints cost more in
   // LDS waits than they balance.)  GH 8 has no LDS left for the counts and
-  // keeps the default priority.
+  // alternates the favour by tile parity (below).
   constexpr bool PRIO = ROWS && GH == 4;
   __shared__ int s_prog[PRIO ? 8 : 1];
   if constexpr (PRIO) {
@@ -961,6 +961,16 @@ __global__ __launch_bounds__(ROWS ? 512 : kThreads, ROWS ? 1 : 2) void wave_kern
   for (int t = t_first; t < t_end; t += TS) {
     const int n0 = t * BN;
     const int len = min(BN, L_valid - n0);
+    if constexpr (ROWS && GH == 8) {
+      // no LDS for the checkpoint counts: the favour alternates by tile
+      // parity instead (waves 4-7 on even tiles, 0-3 on odd ones), so that
+      // neither SIMD partner keeps the lead the issue order gives it
+      if ((t + (wave >> 2)) & 1) {
+        __builtin_amdgcn_s_setprio(1);
+      } else {
+        __builtin_amdgcn_s_setprio(0);
+      }
+    }
     balance(3 * (t - t_first));
 
     // ---- scores of the four sub-blocks -------------------------------------
