@@ -308,7 +308,7 @@ def run_cfg5(args, dev):
                    "global_batch": B, "seq_len": L, "S": S, "parallelism": "single GPU"},
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                      "frac": achieved / HBM_PEAK_GBPS, "traffic": None,
-                     "kernel": "santa::flash::wave_kernel (block_n 256, GH 8)", "kernel_us": ms_kernel * 1e3,
+                     "kernel": "santa::flash::wave_kernel (block_n 256, GH 8, rows layout)", "kernel_us": ms_kernel * 1e3,
                      "bytes_alg_per_launch": bytes_alg, "emitted_v_rows": v_rows,
                      "step_achieved_GBps": bytes_alg / (ms_step * 1e-3) / 1e9},
         "wall_s_timed": wall,
