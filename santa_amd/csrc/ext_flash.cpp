@@ -101,12 +101,31 @@ at::Tensor aligned_q(const at::Tensor& q_h) {
 // Small per-call metadata (lengths, budgets) to the device without a host
 // synchronisation: staged in pinned memory from torch's caching host
 // allocator, which keeps the buffer until the copy on the current stream has
-// run, then copied asynchronously.
+// run, then copied asynchronously.  The last few uploads are kept per
+// (device, stream) and reused when the contents are equal: a decode step
+// calls the attention of every layer with the same lengths.  A reuse on the
+// stream the copy was made on is ordered after that copy, and an entry is
+// never written again, so kernels still reading it are unaffected.  (The
+// cache is never destroyed: tensors freed at process exit could outlive the
+// HIP runtime.)
 at::Tensor to_device_async(const std::vector<int32_t>& host, const at::Device& dev) {
+  struct Entry {
+    int device;
+    hipStream_t stream;
+    std::vector<int32_t> host;
+    at::Tensor t;
+  };
+  static auto* cache = new std::vector<Entry>();  // callers hold the GIL
+  const hipStream_t stream = c10::hip::getCurrentHIPStream(dev.index()).stream();
+  for (const Entry& e : *cache)
+    if (e.device == dev.index() && e.stream == stream && e.host == host) return e.t;
   at::Tensor pinned = at::empty({static_cast<int64_t>(host.size())},
                                 at::TensorOptions().dtype(at::kInt).pinned_memory(true));
   std::copy(host.begin(), host.end(), pinned.data_ptr<int32_t>());
-  return pinned.to(dev, /*non_blocking=*/true);
+  at::Tensor t = pinned.to(dev, /*non_blocking=*/true);
+  if (cache->size() >= 8) cache->erase(cache->begin());
+  cache->push_back(Entry{dev.index(), stream, host, t});
+  return t;
 }
 
 hipStream_t current_stream(const at::Tensor& t) {
