@@ -211,6 +211,29 @@ int santa_prop_decode_paged(const void* q, const void* K_pages, const void* V_pa
                             int pass1_path, uint64_t seed, void* out, float* m_star, int* vrows, void* workspace,
                             size_t workspace_bytes, hipStream_t stream);
 
+/* ------------------------------------------------- model-level decode */
+
+/* Fused elementwise steps of the model-level decode loop
+ * (santa_amd/runtime.py); the reference runs them as separate torch
+ * kernels inside the HF decoder layer (tutorial_code/runtime_common.py:
+ * 501-571).  bf16 tensors, rows contiguous.
+ *
+ * santa_rt_add_rms_norm: per row of h [rows, hidden], h = bf16(h + a) when a
+ * is not null, then x = bf16(float(h) * rsqrt(mean(float(h)^2) + eps) *
+ * float(w)).
+ * santa_rt_rope_write: qkv [B, H + 2 KVH, D] (the fused projection's
+ * output); q heads rotated into q_out [B, H, D], k heads rotated into
+ * k_cache[b, pos] and v heads copied into v_cache[b, pos] of caches
+ * [B, storage, KVH, D]; RoPE in the rotate-half convention with cos, sin
+ * [D] and bf16 rounding of each product and of the sum.
+ * santa_rt_silu_mul: out [rows, inter] = bf16(bf16(silu(gate)) * up), gate
+ * and up the two halves of gu [rows, 2 inter]. */
+int santa_rt_add_rms_norm(void* h, const void* a, const void* w, void* x, int rows, int hidden, float eps,
+                          hipStream_t stream);
+int santa_rt_rope_write(const void* qkv, const void* cos_, const void* sin_, void* q_out, void* k_cache, void* v_cache,
+                        int B, int H, int KVH, int D, long long storage, int pos, hipStream_t stream);
+int santa_rt_silu_mul(const void* gu, void* out, int rows, int inter, hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

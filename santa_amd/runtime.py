@@ -16,7 +16,9 @@ the NHD caches directly, and the greedy loop keeps the tokens on the device
 """
 from __future__ import annotations
 
+import ctypes
 import math
+import os
 import time
 from dataclasses import dataclass
 from typing import Dict, List, Optional
@@ -53,6 +55,74 @@ def _rms_norm(x: torch.Tensor, w: torch.Tensor, eps: float) -> torch.Tensor:
     xf = x.float()
     xf = xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + eps)
     return (xf * w.float()).to(x.dtype)
+
+
+class _FusedOps:
+    """The library's fused decode-step kernels (santa_rt_* in santa_amd.h):
+    residual add + RMSNorm, RoPE of q and k with the cache write, SwiGLU.
+    Used for tensors on a GPU; the torch expressions above stay the CPU path
+    and the prefill's.  A GPU decode step fails loudly if the library is not
+    built."""
+
+    _lib = None
+
+    @classmethod
+    def lib(cls):
+        if cls._lib is None:
+            path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libsanta_amd.so")
+            if not os.path.exists(path):
+                raise RuntimeError("santa_amd/libsanta_amd.so is not built (run __graft_entry__.build())")
+            L = ctypes.CDLL(path)
+            L.santa_last_error.restype = ctypes.c_char_p
+            L.santa_rt_add_rms_norm.argtypes = [ctypes.c_void_p] * 4 + [ctypes.c_int, ctypes.c_int, ctypes.c_float,
+                                                                         ctypes.c_void_p]
+            L.santa_rt_rope_write.argtypes = [ctypes.c_void_p] * 6 + [ctypes.c_int] * 4 + [
+                ctypes.c_longlong, ctypes.c_int, ctypes.c_void_p]
+            L.santa_rt_silu_mul.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int, ctypes.c_int,
+                                            ctypes.c_void_p]
+            cls._lib = L
+        return cls._lib
+
+    @classmethod
+    def _check(cls, rc):
+        if rc != 0:
+            raise RuntimeError(cls.lib().santa_last_error().decode())
+
+    @staticmethod
+    def _stream(t: torch.Tensor):
+        return torch.cuda.current_stream(t.device).cuda_stream
+
+    @classmethod
+    def add_rms_norm(cls, h: torch.Tensor, a: Optional[torch.Tensor], w: torch.Tensor, eps: float) -> torch.Tensor:
+        """h += a (in place, bf16) when a is given; returns rms_norm(h) * w."""
+        assert h.is_contiguous() and h.dtype == torch.bfloat16 and (a is None or a.is_contiguous())
+        x = torch.empty_like(h)
+        rows, hidden = h.numel() // h.shape[-1], h.shape[-1]
+        cls._check(cls.lib().santa_rt_add_rms_norm(h.data_ptr(), a.data_ptr() if a is not None else None,
+                                                   w.data_ptr(), x.data_ptr(), rows, hidden, eps, cls._stream(h)))
+        return x
+
+    @classmethod
+    def rope_write(cls, qkv: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor, cache: "NHDCache", layer: int,
+                   pos: int, heads: int, kv_heads: int, head_dim: int) -> torch.Tensor:
+        """q rotated ([B, H, D]); k rotated and v written to the caches at pos."""
+        assert qkv.is_contiguous() and cos.is_contiguous() and sin.is_contiguous()
+        B = qkv.shape[0]
+        q = torch.empty(B, heads, head_dim, dtype=qkv.dtype, device=qkv.device)
+        kc, vc = cache.k[layer], cache.v[layer]
+        cls._check(cls.lib().santa_rt_rope_write(qkv.data_ptr(), cos.data_ptr(), sin.data_ptr(), q.data_ptr(),
+                                                 kc.data_ptr(), vc.data_ptr(), B, heads, kv_heads, head_dim,
+                                                 kc.shape[1], pos, cls._stream(qkv)))
+        return q
+
+    @classmethod
+    def silu_mul(cls, gu: torch.Tensor) -> torch.Tensor:
+        assert gu.is_contiguous()
+        inter = gu.shape[-1] // 2
+        rows = gu.numel() // gu.shape[-1]
+        out = torch.empty(*gu.shape[:-1], inter, dtype=gu.dtype, device=gu.device)
+        cls._check(cls.lib().santa_rt_silu_mul(gu.data_ptr(), out.data_ptr(), rows, inter, cls._stream(gu)))
+        return out
 
 
 def _rope_cos_sin(positions: torch.Tensor, head_dim: int, theta: float, dtype: torch.dtype):
@@ -234,6 +304,9 @@ class RandomLlama:
         B = token.shape[0]
         cos, sin = _rope_cos_sin(torch.tensor([pos], device=self.device), D, s.rope_theta, self.dtype)
         h = self.embed[token]  # [B, hidden]
+        if self.device.type == "cuda" and self.dtype == torch.bfloat16:
+            return self._decode_step_fused(h, cos.reshape(D).contiguous(), sin.reshape(D).contiguous(), pos, cache,
+                                           backend)
         for li, L in enumerate(self.layers):
             x = _rms_norm(h, L["ln1"], s.rms_eps)
             q, k, v = self._qkv(L, x)
@@ -244,6 +317,26 @@ class RandomLlama:
             h = h + F.linear(a.reshape(B, s.heads * D), L["wo"])
             h = h + self._mlp(L, _rms_norm(h, L["ln2"], s.rms_eps))
         return F.linear(_rms_norm(h, self.norm, s.rms_eps), self.lm_head).float()
+
+    def _decode_step_fused(self, h, cos, sin, pos, cache, backend):
+        """decode_step on the GPU: per layer four fused kernels (add + norm
+        twice, RoPE with the cache write, SwiGLU) around the four weight
+        products and the backend's attention; the same arithmetic as the
+        torch expressions, in the torch expressions' bf16 roundings."""
+        s, D = self.shape, self.shape.head_dim
+        B = h.shape[0]
+        h = h.contiguous()
+        x = _FusedOps.add_rms_norm(h, None, self.layers[0]["ln1"], s.rms_eps)
+        for li, L in enumerate(self.layers):
+            qkv = F.linear(x, L["wqkv"])
+            q = _FusedOps.rope_write(qkv, cos, sin, cache, li, pos, s.heads, s.kv_heads, D)
+            a = backend.decode(q, cache.k[li], cache.v[li], pos + 1)
+            o = F.linear(a.reshape(B, s.heads * D), L["wo"])
+            x = _FusedOps.add_rms_norm(h, o, L["ln2"], s.rms_eps)  # h += o
+            m = F.linear(_FusedOps.silu_mul(F.linear(x, L["wgu"])), L["wd"])
+            nxt = self.layers[li + 1]["ln1"] if li + 1 < len(self.layers) else self.norm
+            x = _FusedOps.add_rms_norm(h, m, nxt, s.rms_eps)  # h += m, then the next layer's (or final) norm
+        return F.linear(x, self.lm_head).float()
 
 
 @torch.inference_mode()

@@ -1,0 +1,84 @@
+"""GPU checks of the fused decode-step kernels (santa_rt_* in santa_amd.h)
+against the torch expressions of santa_amd/runtime.py they replace.
+
+* RoPE with the cache write: bit-exact (each product and the sum are one
+  IEEE float operation rounded to bf16, as in torch's bf16 arithmetic);
+  rows of the caches other than the written position are untouched.
+* add + RMSNorm: the residual sum bit-exact; the norm to one bf16 unit in
+  the last place (the float32 sum of squares is reduced in another order).
+* SwiGLU: to one bf16 unit in the last place (exp is this library's).
+
+Every case prints its name and shape before touching the GPU.
+"""
+import numpy as np
+import pytest
+import torch
+import torch.nn.functional as F
+
+from santa_amd.runtime import NHDCache, LlamaShape, _FusedOps, _apply_rope, _rms_norm, _rope_cos_sin
+
+pytestmark = pytest.mark.gpu
+
+DEV = torch.device("cuda:0")
+
+
+def _ulp_close(got: torch.Tensor, ref: torch.Tensor, ulps: int = 1):
+    a = got.view(torch.int16).cpu().numpy().astype(np.int32)
+    b = ref.view(torch.int16).cpu().numpy().astype(np.int32)
+    # bf16 bit patterns of same-sign values are ordered like the values
+    assert np.abs(a - b).max() <= ulps, np.abs(a - b).max()
+
+
+@pytest.mark.parametrize("rows,hidden", [(1, 4096), (4, 4096), (3, 1000)])
+def test_add_rms_norm(rows, hidden):
+    print(f"\n[case] add_rms_norm rows={rows} hidden={hidden}", flush=True)
+    g = torch.Generator(device=DEV).manual_seed(rows * 7 + hidden)
+    h = torch.randn(rows, hidden, device=DEV, generator=g).to(torch.bfloat16)
+    a = torch.randn(rows, hidden, device=DEV, generator=g).to(torch.bfloat16)
+    w = (1.0 + 0.1 * torch.randn(hidden, device=DEV, generator=g)).to(torch.bfloat16)
+    ref_h = h + a
+    ref_x = _rms_norm(ref_h, w, 1e-5)
+    h2 = h.clone()
+    x = _FusedOps.add_rms_norm(h2, a, w, 1e-5)
+    x0 = _FusedOps.add_rms_norm(h.clone(), None, w, 1e-5)
+    torch.cuda.synchronize()
+    assert torch.equal(h2.view(torch.int16), ref_h.view(torch.int16))
+    _ulp_close(x, ref_x)
+    _ulp_close(x0, _rms_norm(h, w, 1e-5))
+
+
+@pytest.mark.parametrize("B,H,KVH,pos", [(4, 32, 8, 37), (2, 64, 8, 0), (1, 16, 2, 99)])
+def test_rope_write(B, H, KVH, pos):
+    D = 128
+    print(f"\n[case] rope_write B={B} H={H} KVH={KVH} pos={pos}", flush=True)
+    shape = LlamaShape(hidden=H * D, intermediate=256, heads=H, kv_heads=KVH, layers=1, vocab=16)
+    cache = NHDCache(shape, B, 128, torch.bfloat16, DEV)
+    g = torch.Generator(device=DEV).manual_seed(B * 100 + pos)
+    for t in (cache.k[0], cache.v[0]):
+        t.copy_(torch.randn(t.shape, device=DEV, generator=g).to(torch.bfloat16))
+    k_before, v_before = cache.k[0].clone(), cache.v[0].clone()
+    qkv = torch.randn(B, (H + 2 * KVH) * D, device=DEV, generator=g).to(torch.bfloat16)
+    cos, sin = _rope_cos_sin(torch.tensor([pos], device=DEV), D, 500000.0, torch.bfloat16)
+    q = _FusedOps.rope_write(qkv, cos.reshape(D).contiguous(), sin.reshape(D).contiguous(), cache, 0, pos, H, KVH, D)
+    torch.cuda.synchronize()
+    q_ref, k_ref, v_ref = qkv.split([H * D, KVH * D, KVH * D], dim=-1)
+    q_ref = _apply_rope(q_ref.view(B, H, D), cos, sin)
+    k_ref = _apply_rope(k_ref.view(B, KVH, D), cos, sin)
+    assert torch.equal(q.view(torch.int16), q_ref.view(torch.int16))
+    assert torch.equal(cache.k[0][:, pos].view(torch.int16), k_ref.view(torch.int16))
+    assert torch.equal(cache.v[0][:, pos].view(torch.int16), v_ref.reshape(B, KVH, D).view(torch.int16))
+    mask = torch.ones(128, dtype=torch.bool)
+    mask[pos] = False
+    assert torch.equal(cache.k[0][:, mask], k_before[:, mask]) and torch.equal(cache.v[0][:, mask], v_before[:, mask])
+
+
+@pytest.mark.parametrize("rows,inter", [(4, 14336), (1, 300)])
+def test_silu_mul(rows, inter):
+    print(f"\n[case] silu_mul rows={rows} inter={inter}", flush=True)
+    g = torch.Generator(device=DEV).manual_seed(rows + inter)
+    gu = (3.0 * torch.randn(rows, 2 * inter, device=DEV, generator=g)).to(torch.bfloat16)
+    out = _FusedOps.silu_mul(gu)
+    gate, up = gu.chunk(2, dim=-1)
+    ref = F.silu(gate) * up
+    torch.cuda.synchronize()
+    _ulp_close(out, ref)
