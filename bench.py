@@ -456,12 +456,14 @@ def main():
         "vs_baseline": None,
         "dtype": "bf16",
         "data": "synthetic",
-        "config": {"workload": "santa_flash decode, Llama-3.1-8B attention shape (32q/8kv, d=128), B=8, "
-                               "32768 cached tokens, S=256, seed 1690, K/V ~ N(0,1) + rank-4 key bias 0.5",
+        "config": {"workload": f"santa_flash decode, Llama-3.1-8B attention shape (32q/8kv, d=128), B={B}, "
+                               f"{L} cached tokens, S={S}, seed {seed}, K/V ~ N(0,1) + rank-4 key bias 0.5",
                    "global_batch": B, "seq_len": L, "S": S, "parallelism": "single GPU"},
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                      "frac": achieved / HBM_PEAK_GBPS, "traffic": traffic,
-                     "kernel": "santa::flash::wave_kernel (block_n 256, GH 4, rows layout)", "kernel_us": ms_kernel * 1e3,
+                     "kernel": ("santa::flash::tile_kernel (block_n 256, online)" if B * T_c * KVH <= 2048
+                                else "santa::flash::wave_kernel (block_n 256, GH 4, rows layout)"),
+                     "kernel_us": ms_kernel * 1e3,
                      "bytes_alg_per_launch": bytes_alg, "emitted_v_rows": v_rows,
                      "step_achieved_GBps": bytes_alg / (ms_step * 1e-3) / 1e9},
         "wall_s_timed": wall,

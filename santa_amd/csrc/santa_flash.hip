@@ -1777,6 +1777,16 @@ void plan_chunks(int B, int KVH, int T_c, int* cs, int* cpg) { chunk_plan(B, KVH
 bool rows_layout(int KVH) { return KVH == 8; }
 int rows_per_round() { return 4 * resident_workgroups(); }
 
+// Little K to read (at most one resident round of single-wave items: B = 1
+// up to 64k tokens, B = 8 up to 8k): the block_n = 256 tile pass runs on the
+// tile kernel, four waves per tile, whose per-tile latency chain is a
+// quarter of a wave's (B = 1, 4k tokens: 13.0 against 31.2 us per step; B =
+// 1, 32k: 26.5 against 36.2 us).  Above it the wave kernel is faster (B = 4,
+// 32k: 60.9 against 63.9 us).
+static bool small_pass(int B, int KVH, int T_c) {
+  return static_cast<long long>(B) * KVH * T_c <= rows_per_round();
+}
+
 // Ragged batches: chunks small enough for about eight resident rounds over
 // all (kv, tile) items, so the hardware's workgroup dispatch evens out the
 // uneven chunks (each sequence adds at most one partial chunk per KV head;
@@ -1903,7 +1913,8 @@ struct FlashWs {
 };
 FlashWs flash_ws_layout(int B, int H, int KVH, int T_c) {
   FlashWs w{};
-  flash::chunk_plan(B, KVH, T_c, &w.cs, &w.cpg, flash::rows_layout(KVH) ? flash::rows_per_round() : 0);
+  const bool rows = flash::rows_layout(KVH) && !flash::small_pass(B, KVH, T_c);
+  flash::chunk_plan(B, KVH, T_c, &w.cs, &w.cpg, rows ? flash::rows_per_round() : 0);
   const size_t chunks = static_cast<size_t>(B) * KVH * w.cpg;
   const int GH = H / KVH;
   size_t off = 0;
@@ -1958,8 +1969,9 @@ extern "C" int santa_flash_decode_tiles(const void* q, const void* K, const void
   flash::Args a{q, K, V, B, H, KVH, L_valid, L_storage, T_c, S_per_tile, seed, nullptr, nullptr, nullptr, nullptr,
                 nullptr, reinterpret_cast<float*>(base + w.part), reinterpret_cast<int*>(base + w.emit), w.cs, w.cpg,
                 nullptr};
-  const hipError_t e = (block_n == 256) ? flash::launch_wave(dtype, H / KVH, a, nullptr, nullptr, nullptr, stream)
-                                         : flash::launch_tiles<flash::kOnline>(dtype, H / KVH, block_n, a, stream);
+  const bool wave = block_n == 256 && !flash::small_pass(B, KVH, T_c);
+  const hipError_t e = wave ? flash::launch_wave(dtype, H / KVH, a, nullptr, nullptr, nullptr, stream)
+                            : flash::launch_tiles<flash::kOnline>(dtype, H / KVH, block_n, a, stream);
   if (e != hipSuccess) return set_error(SANTA_ERR_HIP, "tile launch failed: %s", hipGetErrorString(e));
   return clear_error();
 }
