@@ -1727,6 +1727,11 @@ hipError_t launch_prop_pass1(const void* q, const void* K, int dtype, int B, int
     // rows form, with a plan of its own (pass 1 writes no chunk partials, so
     // it need not share pass 2's chunking)
     const float q_scale = 1.0f / sqrtf(static_cast<float>(kD));
+    // little K to read and the [L, H] stash: four waves per tile, as for flash
+    const long long kv_tiles = (a.seq_lens ? total_tiles : static_cast<long long>(a.B) * a.T_c) * a.KVH;
+    if (stash_ld == 0 && !a.pt.table && (!a.seq_lens || total_tiles >= 0) && small_prop_pass(kv_tiles))
+      return (dtype == SANTA_BF16) ? launch_bn<true, 4, kPass1Vec>(256, a, stream)
+                                   : launch_bn<false, 4, kPass1Vec>(256, a, stream);
     const bool rows = rows_layout(a.KVH) && (!a.seq_lens || total_tiles >= 0);
     if (rows) {
       if (a.seq_lens) {
@@ -1783,9 +1788,14 @@ int rows_per_round() { return 4 * resident_workgroups(); }
 // quarter of a wave's (B = 1, 4k tokens: 13.0 against 31.2 us per step; B =
 // 1, 32k: 26.5 against 36.2 us).  Above it the wave kernel is faster (B = 4,
 // 32k: 60.9 against 63.9 us).
-static bool small_pass(int B, int KVH, int T_c) {
-  return static_cast<long long>(B) * KVH * T_c <= rows_per_round();
-}
+bool small_pass(long long kv_tiles) { return kv_tiles <= rows_per_round(); }
+// santa_prop's vec pass 1 takes the tile kernel below a quarter of that: the
+// [L, H] stash it writes costs pass 2 four 2-byte loads per lane and row pair
+// where the head-major one costs one, which outweighs the shorter pass 1 from
+// about 32k tokens of one sequence (per call: 4k 30.8 -> 19.7 us, 16k 38.5 ->
+// 31.3 us; 32k 44.0 -> 45.8 us, 64k 54.3 -> 64.5 us).
+bool small_prop_pass(long long kv_tiles) { return kv_tiles <= rows_per_round() / 4; }
+static bool small_pass(int B, int KVH, int T_c) { return small_pass(static_cast<long long>(B) * KVH * T_c); }
 
 // Ragged batches: chunks small enough for about eight resident rounds over
 // all (kv, tile) items, so the hardware's workgroup dispatch evens out the

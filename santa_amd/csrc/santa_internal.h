@@ -54,6 +54,11 @@ void plan_ragged(int B, int KVH, long long total_tiles, int max_tiles, int* cs, 
 // The flash tile pass's layout: one wave per KV head (ROWS) for KVH = 8, its
 // chunks planned for rows_per_round() items per round.
 bool rows_layout(int KVH);
+// A tile pass with at most one resident round of (kv, tile) items runs four
+// waves per tile (tile_kernel) rather than one (wave_kernel); for santa_prop's
+// vec pass 1 that also means the [L, H] stash layout.
+bool small_pass(long long kv_tiles);
+bool small_prop_pass(long long kv_tiles);
 int rows_per_round();
 // The block_n = 256 online tile pass (the wave kernel) with its per-tile
 // statistics m, ell [B, H, T_c] and counts [B, H, T_c, 256] written out

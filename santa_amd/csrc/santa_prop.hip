@@ -918,8 +918,11 @@ extern "C" int santa_prop_decode(const void* q, const void* K, const void* V, in
   float* inv = reinterpret_cast<float*>(base + w.inv);
   float* a0 = reinterpret_cast<float*>(base + w.a0);
   uint16_t* stash = reinterpret_cast<uint16_t*>(base + w.stash);
-  // the vec path keeps the stash head-major between its two passes
-  const int sld = (pass1_path == 0) ? prop::stash_ld(L) : 0;
+  // the vec path keeps the stash head-major between its two passes, except
+  // for a small pass, whose pass 1 runs four waves per tile with the [L, H]
+  // stash
+  const bool small = flash::small_prop_pass(static_cast<long long>(T_c) * KVH);
+  const int sld = (pass1_path == 0 && !small) ? prop::stash_ld(L) : 0;
   hipError_t e = flash::launch_prop_pass1(q, K, dtype, 1, H, KVH, L, L, block_n, pass1_path, m_tiles, ell_tiles,
                                           stash, nullptr, 0, 0, sld, stream);
   if (e != hipSuccess) return set_error(SANTA_ERR_HIP, "pass-1 launch failed: %s", hipGetErrorString(e));
@@ -968,7 +971,8 @@ static int prop_decode_batched(const void* q, const void* K, const void* V, int 
   float* inv = reinterpret_cast<float*>(base + w.inv);
   float* a0 = reinterpret_cast<float*>(base + w.a0);
   uint16_t* stash = reinterpret_cast<uint16_t*>(base + w.stash);
-  const int sld = (pass1_path == 0) ? prop::stash_ld(L_storage) : 0;
+  const bool small = !pt.table && flash::small_prop_pass(total_tiles * KVH);  // as in the scalar call
+  const int sld = (pass1_path == 0 && !small) ? prop::stash_ld(L_storage) : 0;
   hipError_t e = flash::launch_prop_pass1(q, K, dtype, B, H, KVH, max_len, L_storage, block_n, pass1_path, m_tiles,
                                           ell_tiles, stash, seq_lens, w.cs, w.n_wg, sld, stream, pt, total_tiles);
   if (e != hipSuccess) return set_error(SANTA_ERR_HIP, "pass-1 launch failed: %s", hipGetErrorString(e));
