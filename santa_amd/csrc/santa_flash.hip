@@ -238,7 +238,10 @@ __global__ __launch_bounds__(kThreads, 2) void tile_kernel(
 
   __shared__ float s_sc[BN * GH];          // scores, [row][head]
   __shared__ uint16_t s_ub[GH * BN];       // 16-bit u, [head][row]
-  __shared__ int s_wmax[4 * GH];           // wave maxima as order keys
+  // wave maxima as order keys, double-buffered by tile parity: a wave may
+  // write the next tile's maxima (phase B, before that tile's first barrier)
+  // while another still reads this tile's (phases C-D, after its last one)
+  __shared__ int s_wmax2[2][4 * GH];
   __shared__ float s_W[NWS * GH];
   __shared__ uint64_t s_mask[GH * NPAIR * 2];
 
@@ -396,6 +399,7 @@ __global__ __launch_bounds__(kThreads, 2) void tile_kernel(
   for (int t = t_begin; t < t_end; ++t) {
     const int n0 = t * BN;
     const int len = min(BN, L_valid - n0);
+    int* const s_wmax = s_wmax2[(t - t_begin) & 1];
 
     // ---- A: scores -----------------------------------------------------------
     float lmax[GH];
@@ -1542,7 +1546,7 @@ static hipError_t launch_tk(const Args& a, hipStream_t stream) {
 template <bool BF16, int GH, int BN, int MODE>
 static hipError_t launch_t(const Args& a, hipStream_t stream) {
   if (a.pt.table) {
-    if constexpr ((MODE == kOnline && BN != 256) || MODE == kPass1Gen) return launch_tk<BF16, GH, BN, MODE, true>(a, stream);
+    if constexpr (MODE == kOnline || MODE == kPass1Gen) return launch_tk<BF16, GH, BN, MODE, true>(a, stream);
     return hipErrorInvalidValue;
   }
   return launch_tk<BF16, GH, BN, MODE, false>(a, stream);
@@ -2022,9 +2026,11 @@ struct RaggedWs {
   size_t part, emit, total;
   int cs, n_wg;
 };
-RaggedWs ragged_ws_layout(int B, int H, int KVH, long long total_tiles, int max_tiles) {
+// small: the tile kernel takes the pass (flash::small_pass), with the
+// four-wave plan
+RaggedWs ragged_ws_layout(int B, int H, int KVH, long long total_tiles, int max_tiles, bool small = false) {
   RaggedWs w{};
-  const bool rows = flash::rows_layout(KVH);
+  const bool rows = flash::rows_layout(KVH) && !small;
   flash::plan_ragged(B, KVH, total_tiles, max_tiles, &w.cs, &w.n_wg, rows ? flash::rows_per_round() : 0,
                      rows ? 1 : 4);
   const size_t chunks = static_cast<size_t>(w.n_wg);
@@ -2042,7 +2048,12 @@ extern "C" size_t santa_flash_ragged_workspace_size(int B, int H, int KVH, int D
                                                     long long total_tiles) {
   (void)D;
   if (B <= 0 || H <= 0 || KVH <= 0 || H % KVH != 0 || max_tiles <= 0 || total_tiles < 0) return 0;
-  return ragged_ws_layout(B, H, KVH, total_tiles, max_tiles).total;
+  // both plans a call may take (the small one only at block_n 256, which
+  // this size does not know about)
+  size_t bytes = ragged_ws_layout(B, H, KVH, total_tiles, max_tiles).total;
+  if (flash::small_pass(total_tiles * KVH))
+    bytes = std::max(bytes, ragged_ws_layout(B, H, KVH, total_tiles, max_tiles, true).total);
+  return bytes;
 }
 
 // The ragged decode over a contiguous [B, L_storage, KVH, D] cache or, with
@@ -2057,7 +2068,10 @@ static int flash_decode_ragged(const void* q, const void* K, const void* V, int 
   const int T_c = (max_len + block_n - 1) / block_n;
   if (total_tiles < 0 || total_tiles > static_cast<long long>(B) * T_c)
     return set_error(SANTA_ERR_INVALID, "total_tiles out of range");
-  const RaggedWs w = ragged_ws_layout(B, H, KVH, total_tiles, T_c);
+  // little K: the tile kernel, for contiguous and paged caches alike (so that
+  // the two stay bit-identical)
+  const bool small = block_n == 256 && flash::small_pass(total_tiles * KVH);
+  const RaggedWs w = ragged_ws_layout(B, H, KVH, total_tiles, T_c, small);
   if (!workspace || workspace_bytes < w.total)
     return set_error(SANTA_ERR_WORKSPACE, "workspace too small: need %zu bytes, got %zu", w.total, workspace_bytes);
   char* base = static_cast<char*>(workspace);
@@ -2065,8 +2079,8 @@ static int flash_decode_ragged(const void* q, const void* K, const void* V, int 
   int* pe = reinterpret_cast<int*>(base + w.emit);
   flash::Args a{q, K, V, B, H, KVH, max_len, L_storage, T_c, 0, seed, nullptr, nullptr, nullptr, nullptr, nullptr,
                 part, pe, w.cs, 0, nullptr, seq_lens, w.n_wg, static_cast<long long>(S), pt};
-  hipError_t e = (block_n == 256) ? flash::launch_wave(dtype, H / KVH, a, nullptr, nullptr, nullptr, stream)
-                                  : flash::launch_tiles<flash::kOnline>(dtype, H / KVH, block_n, a, stream);
+  hipError_t e = (block_n == 256 && !small) ? flash::launch_wave(dtype, H / KVH, a, nullptr, nullptr, nullptr, stream)
+                                            : flash::launch_tiles<flash::kOnline>(dtype, H / KVH, block_n, a, stream);
   if (e != hipSuccess) return set_error(SANTA_ERR_HIP, "tile launch failed: %s", hipGetErrorString(e));
   e = flash::launch_merge(part, pe, dtype, B, H, KVH, 0, 0, out, m_star, vrows, seq_lens, block_n, w.cs, max_len,
                           w.n_wg, static_cast<long long>(S), stream);
