@@ -7,10 +7,22 @@ K/V ~ N(0,1) plus a per-head rank-4 key bias (scale 0.5), S = 256, seed 1690.
 One step = one single-layer decode call (santa_flash_batch_cuda.
 decode_systematic_batched) over inputs already resident in HBM.
 
-Prints ONE JSON line (rank 0).  `value` is tokens/s = B / t_step; the
-µs/step is `ms_per_step` * 1000; the roofline block reports algorithmic HBM
-bytes (all valid K rows + emitted V rows + q + out + m_star) over the fused
-tile kernel's average duration measured with HIP events on its stream.
+Timing.  The warm-up runs --warmup calls and then keeps calling until at
+least --warmup-ms of wall time has passed (the GPU's clocks settle), whatever
+--warmup says.  Then exactly --steps calls are timed in one window between
+HIP events on torch's current stream (the stream every launch goes on),
+bracketed by device synchronisations: ms_per_step and value come from that
+window.  Then windows of the whole step and of the dominant kernel alone
+(the flash tile pass, the step minus its merge launch) alternate, several of
+each, and their medians give kernel_us and us_per_step_median: the tile pass
+is part of the step, so kernel_us <= us_per_step_median.
+
+Prints ONE JSON line.  `value` is tokens/s = B / t_step; `roofline.achieved`
+is the algorithmic HBM bytes (all valid K rows + emitted V rows + q + out +
+m_star) over the tile pass's median duration; `roofline.step_frac` uses the
+whole step instead.  `cpu_baseline` is the vectorized PyTorch CPU
+restatement of the same estimator (oracle/torch_ref.py) on the host cores,
+with the C oracle's time beside it.
 """
 from __future__ import annotations
 
@@ -18,6 +30,8 @@ import argparse
 import json
 import math
 import os
+import statistics
+import subprocess
 import sys
 import time
 
@@ -26,6 +40,7 @@ if REPO not in sys.path:
     sys.path.insert(0, REPO)
 
 HBM_PEAK_GBPS = 8000.0  # MI355X published HBM3E bandwidth, 8 TB/s
+METRIC = "sampled-attn decode µs/step + achieved HBM TB/s (B=8, 32k ctx, S=256); tokens/s"
 
 
 def parse_args():
@@ -33,16 +48,22 @@ def parse_args():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=1000)
     ap.add_argument("--warmup", type=int, default=50)
+    ap.add_argument("--warmup-ms", type=float, default=400.0,
+                    help="minimum wall time of warm-up decode calls before timing")
+    ap.add_argument("--windows", type=int, default=5,
+                    help="alternating windows of the step and of the tile pass alone (medians reported)")
     ap.add_argument("--batch", type=int, default=8)
     ap.add_argument("--ctx", type=int, default=32768)
     ap.add_argument("--S", type=int, default=256)
     ap.add_argument("--seed", type=int, default=1690)
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--workload", choices=("cfg2", "cfg3", "cfg4", "cfg5"), default="cfg2",
+    ap.add_argument("--workload", choices=("cfg2", "cfg3", "cfg4", "cfg5", "cfg5p", "single"), default="cfg2",
                     help="cfg2: the headline (flash, B=8, 32k); cfg3: batched ragged santa_prop (B=16, "
                          "L_b in [8192, 131072], S_b = L_b // 64); cfg4: model-level decode, random-init "
                          "Llama-3.1-8B shape, B=4, 32768-token prompt, 64 greedy steps, santa_flash S=256 vs exact; "
-                         "cfg5: flash stress (B=32, 64q/8kv, 128k, S=512)")
+                         "cfg5: flash stress (B=32, 64q/8kv, 128k, S=512); cfg5p: santa_prop at cfg5's shape with "
+                         "S=512 per sequence; single: one sequence of --ctx tokens through santa_flash (S=256) "
+                         "and santa_prop (S=L/64)")
     ap.add_argument("--cpu-sample-seqs", type=int, default=8, help="sequences timed for the CPU baseline")
     ap.add_argument("--page-size", type=int, default=0,
                     help="cfg2 / cfg3 through the paged-KV entry point: the same tokens scattered over a pool of "
@@ -83,29 +104,66 @@ def make_inputs(B, L, H=32, KVH=8, D=128, seed=1690):
     return q.bfloat16(), K.bfloat16(), V.bfloat16()
 
 
-def cpu_baseline(q, K, V, S, seed, n_seq, min_wall_s=2.0, max_reps=20):
-    """The oracle (C restatement of the reference algorithm) on the host cores:
-    whole decode steps over the first n_seq sequences of the same workload,
-    repeated until min_wall_s of wall time (at 16 threads about 30 s of CPU
-    work), median step time."""
-    import statistics
+def host_threads():
+    """The host cores this process may use (the GPU box grants a share of the
+    machine, which os.cpu_count() does not show)."""
+    return int(os.environ.get("OMP_NUM_THREADS") or 0) or len(os.sched_getaffinity(0))
+
+
+def cpu_model():
+    try:
+        out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10).stdout
+        for line in out.splitlines():
+            if line.startswith("Model name:"):
+                return line.split(":", 1)[1].strip()
+    except (OSError, subprocess.SubprocessError):
+        pass
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def cpu_baseline(q, K, V, S, seed, n_seq, min_wall_s=2.0, min_steps=5, max_steps=20):
+    """The reference algorithm's PyTorch CPU path (oracle/torch_ref.py, a
+    vectorized restatement of the same estimator) on the host cores: whole
+    decode steps of the first n_seq sequences, repeated for at least
+    min_wall_s and min_steps, median step time.  Beside it, the C oracle
+    (OpenMP over tiles) on the same sample."""
+    import torch
 
     import oracle
+    from oracle import torch_ref
 
-    # the host cores this process may use (the GPU box grants a share of them)
-    threads = int(os.environ.get("OMP_NUM_THREADS") or 0) or len(os.sched_getaffinity(0))
+    threads = host_threads()
+    torch.set_num_threads(threads)
     qs, Ks, Vs = q[:n_seq].contiguous(), K[:n_seq].contiguous(), V[:n_seq].contiguous()
-    oracle.flash_decode(qs, Ks[:, :4096].contiguous(), Vs[:, :4096].contiguous(), S, seed=seed, nthreads=threads)
-    times = []
-    t_start = time.perf_counter()
-    while len(times) < max_reps and (time.perf_counter() - t_start < min_wall_s or len(times) < 3):
-        t0 = time.perf_counter()
-        oracle.flash_decode(qs, Ks, Vs, S, seed=seed, nthreads=threads)
-        times.append(time.perf_counter() - t0)
-    dt = statistics.median(times)
+
+    def timed(fn, min_steps, max_steps, min_wall):
+        fn()  # first call: allocations, thread pools
+        times = []
+        t_start = time.perf_counter()
+        while len(times) < max_steps and (time.perf_counter() - t_start < min_wall or len(times) < min_steps):
+            t0 = time.perf_counter()
+            fn()
+            times.append(time.perf_counter() - t0)
+        return statistics.median(times), len(times)
+
+    dt, n = timed(lambda: torch_ref.flash_decode(qs, Ks, Vs, S, seed=seed), min_steps, max_steps, min_wall_s)
+    dt_c, n_c = timed(lambda: oracle.flash_decode(qs, Ks, Vs, S, seed=seed, nthreads=threads), 3, 10, 1.0)
     return {"value": n_seq / dt, "unit": "tokens/s", "cores": threads, "kind": "port",
+            "impl": "vectorized PyTorch CPU restatement (oracle/torch_ref.py)",
             "sample": f"{n_seq} of {q.shape[0]} sequences x 1 decode step (L={K.shape[1]}, S={S}); "
-                      f"median of {len(times)} steps, {dt:.3f} s each; C oracle, OpenMP over tiles"}
+                      f"median of {n} steps, {dt:.3f} s each",
+            "torch_num_threads": torch.get_num_threads(), "os_cpu_count": os.cpu_count(),
+            "cpu_model": cpu_model(),
+            "c_oracle": {"value": n_seq / dt_c, "unit": "tokens/s", "cores": threads,
+                         "sample": f"same sample, median of {n_c} steps, {dt_c:.3f} s each; "
+                                   "C restatement (oracle/santa_oracle.c), OpenMP over tiles"}}
 
 
 def device_inputs(B, L, H, KVH, D, seed, dev, keys="bias"):
@@ -160,23 +218,138 @@ def to_pages(K, V, P, seed):
     return pools[0], pools[1], perm.view(B, n).to(torch.int32).contiguous()
 
 
-def time_steps(step, args):
-    """Mean ms per call of step() over args.steps calls after args.warmup,
-    with HIP events on torch's current stream; also the host wall time."""
-    import torch
+class Timing:
+    """Warm-up by time, the official window of exactly `steps` calls, then
+    alternating windows of the step and of the dominant kernel alone."""
 
-    for _ in range(args.warmup):
-        step()
-    stream = torch.cuda.current_stream()
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    def __init__(self, args):
+        self.args = args
+
+    def _window(self, fn, n):
+        import torch
+
+        stream = torch.cuda.current_stream()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        e0.record(stream)
+        for _ in range(n):
+            fn()
+        e1.record(stream)
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / n, time.perf_counter() - t0
+
+    def run(self, step, kernel=None):
+        import torch
+
+        a = self.args
+        t0 = time.perf_counter()
+        calls = 0
+        for _ in range(a.warmup):
+            step()
+            calls += 1
+        torch.cuda.synchronize()
+        while time.perf_counter() - t0 < a.warmup_ms * 1e-3:
+            for _ in range(20):
+                step()
+            calls += 20
+            torch.cuda.synchronize()
+        res = {"warmup_calls": calls, "warmup_s": time.perf_counter() - t0}
+        # the official window: exactly `steps` calls
+        res["ms_per_step"], res["wall_s_timed"] = self._window(step, a.steps)
+        per = max(a.steps, 50)
+        steps_w, kern_w = [], []
+        for _ in range(max(1, a.windows)):
+            steps_w.append(self._window(step, per)[0])
+            if kernel is not None:
+                kern_w.append(self._window(kernel, per)[0])
+        res["step_windows_ms"] = steps_w
+        res["ms_per_step_median"] = statistics.median(steps_w)
+        if kernel is not None:
+            res["kernel_windows_ms"] = kern_w
+            res["kernel_ms"] = statistics.median(kern_w)
+        res["window_calls"] = per
+        return res
+
+
+def base_line(metric, B, tm, args, dtype="bf16"):
+    ms = tm["ms_per_step"]
+    return {
+        "metric": metric, "value": B / (ms * 1e-3), "unit": "tokens/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": ms, "us_per_step": ms * 1e3,
+        "us_per_step_median": tm["ms_per_step_median"] * 1e3, "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": dtype, "data": "synthetic",
+    }
+
+
+def timing_keys(tm):
+    return {"warmup_s": tm["warmup_s"], "warmup_calls": tm["warmup_calls"], "wall_s_timed": tm["wall_s_timed"],
+            "windows": {"calls_each": tm["window_calls"],
+                        "step_us": [round(x * 1e3, 2) for x in tm["step_windows_ms"]],
+                        "kernel_us": [round(x * 1e3, 2) for x in tm.get("kernel_windows_ms", [])]}}
+
+
+def roofline(bytes_alg, tm, kernel_name, traffic=None, v_rows=None):
+    """Roofline block: achieved = algorithmic bytes / the dominant kernel's
+    median duration (the whole step when there is no kernel timing)."""
+    k_ms = tm.get("kernel_ms", tm["ms_per_step_median"])
+    achieved = bytes_alg / (k_ms * 1e-3) / 1e9
+    step_gbps = bytes_alg / (tm["ms_per_step"] * 1e-3) / 1e9
+    r = {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+         "frac": achieved / HBM_PEAK_GBPS, "traffic": traffic, "kernel": kernel_name, "kernel_us": k_ms * 1e3,
+         "bytes_alg_per_launch": bytes_alg, "step_achieved_GBps": step_gbps, "step_frac": step_gbps / HBM_PEAK_GBPS,
+         "kernel_le_step": k_ms <= tm["ms_per_step_median"]}
+    if v_rows is not None:
+        r["emitted_v_rows"] = v_rows
+    return r
+
+
+def flash_bytes(lens, KVH, H, B, v_rows, D=128):
+    return sum(lens) * KVH * D * 2 + v_rows * D * 2 + B * H * D * 2 * 2 + B * H * 4
+
+
+def run_cfg2(args, dev):
+    import torch
+    import santa_flash_batch_cuda as flash
+
+    if args.copy_calibration_mib > 0:
+        n = args.copy_calibration_mib << 20
+        src = torch.ones(n // 2, dtype=torch.bfloat16, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(5):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
+    B, L, S, seed = args.batch, args.ctx, args.S, args.seed
+    H, KVH, D = 32, 8, 128
+    q_c, K_c, V_c = make_inputs(B, L, H, KVH, D, seed)
+    q, K, V = q_c.to(dev), K_c.to(dev), V_c.to(dev)
     torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    e0.record(stream)
-    for _ in range(args.steps):
-        step()
-    e1.record(stream)
-    torch.cuda.synchronize()
-    return e0.elapsed_time(e1) / args.steps, time.perf_counter() - t0
+    # untimed: emitted V rows for the algorithmic byte count
+    _, _, vrows = flash.decode_systematic_batched(q, K, V, S, seed=seed, want_vrows=True)
+    v_rows = int(vrows.sum().item())
+    bytes_alg = flash_bytes([L] * B, KVH, H, B, v_rows)
+    T_c = (L + 255) // 256
+    ws = torch.empty(flash._workspace_bytes(B, H, KVH, D, T_c), dtype=torch.uint8, device=dev)
+
+    def step():
+        flash.decode_systematic_batched(q, K, V, S, seed=seed)
+
+    def tiles():  # the step's dominant launch alone: the flash tile pass
+        flash._decode_tiles_only(q, K, V, S, seed, 0, -1, ws)
+
+    tm = Timing(args).run(step, tiles)
+    default_workload = (B, L, S, seed) == (8, 32768, 256, 1690)
+    line = base_line(METRIC, B, tm, args)
+    line["config"] = {"workload": f"santa_flash decode, Llama-3.1-8B attention shape (32q/8kv, d=128), B={B}, "
+                                  f"{L} cached tokens, S={S}, seed {seed}, K/V ~ N(0,1) + rank-4 key bias 0.5",
+                      "global_batch": B, "seq_len": L, "S": S, "parallelism": "single GPU"}
+    line["roofline"] = roofline(bytes_alg, tm, flash._tile_pass_kernel(B, H, KVH, T_c, 256),
+                                measured_traffic() if default_workload else None, v_rows)
+    line.update(timing_keys(tm))
+    if not args.no_cpu_baseline:
+        line["cpu_baseline"] = cpu_baseline(q_c, K_c, V_c, S, seed, args.cpu_sample_seqs)
+    return line
 
 
 def run_cfg2_paged(args, dev):
@@ -198,24 +371,16 @@ def run_cfg2_paged(args, dev):
 
     _, _, vrows = step(True)
     v_rows = int(vrows.sum().item())
-    bytes_alg = B * L * KVH * D * 2 + v_rows * D * 2 + B * H * D * 2 * 2 + B * H * 4
-    ms_step, wall = time_steps(step, args)
-    achieved = bytes_alg / (ms_step * 1e-3) / 1e9
-    return {
-        "metric": "sampled-attn decode µs/step + achieved HBM TB/s (B=8, 32k ctx, S=256); tokens/s (paged KV)",
-        "value": B / (ms_step * 1e-3), "unit": "tokens/s", "n_gpus": 1, "steps": args.steps,
-        "warmup": args.warmup, "ms_per_step": ms_step, "us_per_step": ms_step * 1e3, "higher_is_better": True,
-        "scaling": "weak", "vs_baseline": None, "dtype": "bf16", "data": "synthetic",
-        "config": {"workload": f"santa_flash decode, Llama-3.1-8B attention shape (32q/8kv, d=128), B={B}, {L} "
-                               f"cached tokens in {P}-token pages (seeded random page order), S={S}, seed {seed}, "
-                               "K/V ~ N(0,1) + rank-4 key bias 0.5",
-                   "global_batch": B, "seq_len": L, "S": S, "page_size": P, "parallelism": "single GPU"},
-        "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBPS, "unit": "GB/s",
-                     "frac": achieved / HBM_PEAK_GBPS, "traffic": None,
-                     "kernel": "whole paged decode step (wave kernel + merge)", "kernel_us": ms_step * 1e3,
-                     "bytes_alg_per_launch": bytes_alg, "emitted_v_rows": v_rows},
-        "wall_s_timed": wall,
-    }
+    tm = Timing(args).run(step)
+    line = base_line(METRIC + " (paged KV)", B, tm, args)
+    line["config"] = {"workload": f"santa_flash decode, Llama-3.1-8B attention shape (32q/8kv, d=128), B={B}, {L} "
+                                  f"cached tokens in {P}-token pages (seeded random page order), S={S}, seed {seed}, "
+                                  "K/V ~ N(0,1) + rank-4 key bias 0.5",
+                      "global_batch": B, "seq_len": L, "S": S, "page_size": P, "parallelism": "single GPU"}
+    line["roofline"] = roofline(flash_bytes(lens, KVH, H, B, v_rows), tm,
+                                "whole paged decode step (tile pass + merge)", None, v_rows)
+    line.update(timing_keys(tm))
+    return line
 
 
 def run_cfg3(args, dev):
@@ -243,24 +408,17 @@ def run_cfg3(args, dev):
             return prop.decode_systematic_batched(q, K, V, Ss, seed=seed, want_vrows=want_vrows, valid_len=lens)
     _, _, vrows = step(True)
     v_rows = int(vrows.sum().item())
-    bytes_alg = sum(lens) * KVH * D * 2 + v_rows * D * 2 + B * H * D * 2 * 2 + B * H * 4
-    ms_step, wall = time_steps(step, args)
-    achieved = bytes_alg / (ms_step * 1e-3) / 1e9
-    return {
-        "metric": "sampled-attn decode µs/step + achieved HBM TB/s; tokens/s (cfg3: batched ragged santa_prop)",
-        "value": B / (ms_step * 1e-3), "unit": "tokens/s", "n_gpus": 1, "steps": args.steps,
-        "warmup": args.warmup, "ms_per_step": ms_step, "us_per_step": ms_step * 1e3, "higher_is_better": True,
-        "scaling": "weak", "vs_baseline": None, "dtype": "bf16", "data": "synthetic",
-        "config": {"workload": f"santa_prop batched ragged decode, 32q/8kv, d=128, B={B}, L_b seeded U[8192, 131072] "
-                               f"(sum {sum(lens)}), S_b = L_b // 64, seed {seed}, K/V ~ N(0,1) + rank-4 key bias 0.5"
-                               + (f", paged KV ({P}-token pages in a seeded random order)" if P else ""),
-                   "global_batch": B, "seq_len": lens, "S": Ss, "parallelism": "single GPU"},
-        "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBPS, "unit": "GB/s",
-                     "frac": achieved / HBM_PEAK_GBPS, "traffic": None,
-                     "kernel": "whole prop step (pass 1 + budgets + pass 2 + finalize)", "kernel_us": ms_step * 1e3,
-                     "bytes_alg_per_launch": bytes_alg, "emitted_v_rows": v_rows},
-        "wall_s_timed": wall,
-    }
+    tm = Timing(args).run(step)
+    line = base_line("sampled-attn decode µs/step + achieved HBM TB/s; tokens/s (cfg3: batched ragged santa_prop)",
+                     B, tm, args)
+    line["config"] = {"workload": f"santa_prop batched ragged decode, 32q/8kv, d=128, B={B}, L_b seeded U[8192, "
+                                  f"131072] (sum {sum(lens)}), S_b = L_b // 64, seed {seed}, K/V ~ N(0,1) + rank-4 key "
+                                  "bias 0.5" + (f", paged KV ({P}-token pages in a seeded random order)" if P else ""),
+                      "global_batch": B, "seq_len": lens, "S": Ss, "parallelism": "single GPU"}
+    line["roofline"] = roofline(flash_bytes(lens, KVH, H, B, v_rows), tm,
+                                "whole prop step (pass 1 + budgets + pass 2 + finalize)", None, v_rows)
+    line.update(timing_keys(tm))
+    return line
 
 
 def run_cfg5(args, dev):
@@ -274,45 +432,91 @@ def run_cfg5(args, dev):
     torch.cuda.synchronize()
     _, _, vrows = flash.decode_systematic_batched(q, K, V, S, seed=seed, want_vrows=True)
     v_rows = int(vrows.sum().item())
-    bytes_alg = B * L * KVH * D * 2 + v_rows * D * 2 + B * H * D * 2 * 2 + B * H * 4
-    for _ in range(args.warmup):
-        flash.decode_systematic_batched(q, K, V, S, seed=seed)
-    stream = torch.cuda.current_stream()
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    e0.record(stream)
-    for _ in range(args.steps):
-        flash.decode_systematic_batched(q, K, V, S, seed=seed)
-    e1.record(stream)
-    torch.cuda.synchronize()
-    wall = time.perf_counter() - t0
-    ms_step = e0.elapsed_time(e1) / args.steps
     T_c = (L + 255) // 256
     ws = torch.empty(flash._workspace_bytes(B, H, KVH, D, T_c), dtype=torch.uint8, device=dev)
-    k0, k1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    k0.record(stream)
-    for _ in range(args.steps):
+
+    def step():
+        flash.decode_systematic_batched(q, K, V, S, seed=seed)
+
+    def tiles():
         flash._decode_tiles_only(q, K, V, S, seed, 0, -1, ws)
-    k1.record(stream)
+
+    tm = Timing(args).run(step, tiles)
+    line = base_line("sampled-attn decode µs/step + achieved HBM TB/s; tokens/s (cfg5: flash stress)", B, tm, args)
+    line["config"] = {"workload": f"santa_flash decode, 64q/8kv (GH 8), d=128, B={B}, {L} cached tokens, S={S}, "
+                                  f"seed {seed}, Student-t(3) keys with 16 planted needles per KV head",
+                      "global_batch": B, "seq_len": L, "S": S, "parallelism": "single GPU"}
+    line["roofline"] = roofline(flash_bytes([L] * B, KVH, H, B, v_rows), tm,
+                                flash._tile_pass_kernel(B, H, KVH, T_c, 256), None, v_rows)
+    line.update(timing_keys(tm))
+    return line
+
+
+def run_cfg5p(args, dev):
+    """santa_prop at cfg5's shape: B=32, 64q/8kv (GH 8: the general pass 1),
+    L=131072, S=512 per sequence (the flash leg's budget), Student-t(3) keys
+    with planted needles; one batched call per step."""
+    import torch
+    import santa_prop_batch_cuda as prop
+
+    B, L, H, KVH, D, S, seed = 32, 131072, 64, 8, 128, 512, args.seed
+    q, K, V = device_inputs(B, L, H, KVH, D, seed, dev, keys="needles")
     torch.cuda.synchronize()
-    ms_kernel = k0.elapsed_time(k1) / args.steps
-    achieved = bytes_alg / (ms_kernel * 1e-3) / 1e9
-    return {
-        "metric": "sampled-attn decode µs/step + achieved HBM TB/s; tokens/s (cfg5: flash stress)",
-        "value": B / (ms_step * 1e-3), "unit": "tokens/s", "n_gpus": 1, "steps": args.steps,
-        "warmup": args.warmup, "ms_per_step": ms_step, "us_per_step": ms_step * 1e3, "higher_is_better": True,
-        "scaling": "weak", "vs_baseline": None, "dtype": "bf16", "data": "synthetic",
-        "config": {"workload": f"santa_flash decode, 64q/8kv (GH 8), d=128, B={B}, {L} cached tokens, S={S}, "
-                               f"seed {seed}, Student-t(3) keys with 16 planted needles per KV head",
-                   "global_batch": B, "seq_len": L, "S": S, "parallelism": "single GPU"},
-        "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBPS, "unit": "GB/s",
-                     "frac": achieved / HBM_PEAK_GBPS, "traffic": None,
-                     "kernel": "santa::flash::wave_kernel (block_n 256, GH 8, rows layout)", "kernel_us": ms_kernel * 1e3,
-                     "bytes_alg_per_launch": bytes_alg, "emitted_v_rows": v_rows,
-                     "step_achieved_GBps": bytes_alg / (ms_step * 1e-3) / 1e9},
-        "wall_s_timed": wall,
-    }
+
+    def step(want_vrows=False):
+        return prop.decode_systematic_batched(q, K, V, S, seed=seed, want_vrows=want_vrows)
+
+    _, _, vrows = step(True)
+    v_rows = int(vrows.sum().item())
+    tm = Timing(args).run(step)
+    line = base_line("sampled-attn decode µs/step + achieved HBM TB/s; tokens/s (cfg5: santa_prop leg)", B, tm, args)
+    line["config"] = {"workload": f"santa_prop batched decode, 64q/8kv (GH 8), d=128, B={B}, {L} cached tokens, "
+                                  f"S={S} per sequence, seed {seed}, Student-t(3) keys with 16 planted needles per "
+                                  "KV head",
+                      "global_batch": B, "seq_len": L, "S": S, "parallelism": "single GPU"}
+    line["roofline"] = roofline(flash_bytes([L] * B, KVH, H, B, v_rows), tm,
+                                "whole prop step (pass 1 + budgets + pass 2 + finalize)", None, v_rows)
+    line.update(timing_keys(tm))
+    return line
+
+
+def run_single(args, dev):
+    """One sequence of --ctx tokens (32q/8kv, d=128, bf16, N(0,1) from the
+    seeded device generator): santa_flash decode_systematic_batched at B=1
+    (S=256) and santa_prop decode_systematic_scalar (S = L // 64), the
+    short-call regime of a single request."""
+    import torch
+    import santa_flash_batch_cuda as flash
+    import santa_prop_batch_cuda as prop
+
+    L, H, KVH, D, seed = args.ctx, 32, 8, 128, args.seed
+    g = torch.Generator(device=dev).manual_seed(seed)
+    q = torch.randn(1, H, D, device=dev, generator=g).bfloat16()
+    K = torch.randn(1, L, KVH, D, device=dev, generator=g).bfloat16()
+    V = torch.randn(1, L, KVH, D, device=dev, generator=g).bfloat16()
+    q1, K1, V1 = q[0].contiguous(), K[0].contiguous(), V[0].contiguous()
+    S_f, S_p = 256, max(1, L // 64)
+    _, _, vr = flash.decode_systematic_batched(q, K, V, S_f, seed=seed, want_vrows=True)
+    _, _, vr_p = prop.decode_systematic_scalar(q1, K1, V1, S_p, seed=seed, want_vrows=True)
+    v_rows, v_rows_p = int(vr.sum().item()), int(vr_p.sum().item())
+    bn = 256 if L > 3072 else (64 if L > 1536 else 32)
+    T_c = (L + bn - 1) // bn
+    ws = torch.empty(flash._workspace_bytes(1, H, KVH, D, T_c), dtype=torch.uint8, device=dev)
+    tm = Timing(args).run(lambda: flash.decode_systematic_batched(q, K, V, S_f, seed=seed),
+                          lambda: flash._decode_tiles_only(q, K, V, S_f, seed, 0, -1, ws))
+    tp = Timing(args).run(lambda: prop.decode_systematic_scalar(q1, K1, V1, S_p, seed=seed))
+    line = base_line(f"sampled-attn decode µs/step + achieved HBM TB/s; tokens/s (single sequence, {L} tokens)",
+                     1, tm, args)
+    line["config"] = {"workload": f"one sequence, 32q/8kv, d=128, {L} cached tokens, N(0,1) keys and values, "
+                                  f"seed {seed}: santa_flash S={S_f} (timed) and santa_prop S={S_p} (prop_leg)",
+                      "global_batch": 1, "seq_len": L, "S": S_f, "parallelism": "single GPU"}
+    line["roofline"] = roofline(flash_bytes([L], KVH, H, 1, v_rows), tm,
+                                flash._tile_pass_kernel(1, H, KVH, T_c, bn), None, v_rows)
+    line["prop_leg"] = {"us_per_step": tp["ms_per_step"] * 1e3, "us_per_step_median": tp["ms_per_step_median"] * 1e3,
+                        "S": S_p, "roofline": roofline(flash_bytes([L], KVH, H, 1, v_rows_p), tp,
+                                                       "whole prop step", None, v_rows_p)}
+    line.update(timing_keys(tm))
+    return line
 
 
 def run_cfg4(args, dev):
@@ -379,97 +583,12 @@ def main():
         return 2
     import torch
 
-    if args.workload != "cfg2" or args.page_size:
-        dev = torch.device("cuda:0")
-        if args.workload == "cfg2":
-            print(json.dumps(run_cfg2_paged(args, dev)))
-            return 0
-        line = {"cfg3": run_cfg3, "cfg4": run_cfg4, "cfg5": run_cfg5}[args.workload](args, dev)
-        print(json.dumps(line))
-        return 0
-    import santa_flash_batch_cuda as flash
-
     dev = torch.device("cuda:0")
-    if args.copy_calibration_mib > 0:
-        n = args.copy_calibration_mib << 20
-        src = torch.ones(n // 2, dtype=torch.bfloat16, device=dev)
-        dst = torch.empty_like(src)
-        for _ in range(5):
-            dst.copy_(src)
-        torch.cuda.synchronize()
-        del src, dst
-    B, L, S, seed = args.batch, args.ctx, args.S, args.seed
-    H, KVH, D = 32, 8, 128
-    q_c, K_c, V_c = make_inputs(B, L, H, KVH, D, seed)
-    q, K, V = q_c.to(dev), K_c.to(dev), V_c.to(dev)
-    torch.cuda.synchronize()
-
-    # untimed: emitted V rows for the algorithmic byte count
-    _, _, vrows = flash.decode_systematic_batched(q, K, V, S, seed=seed, want_vrows=True)
-    v_rows = int(vrows.sum().item())
-    bytes_alg = B * L * KVH * D * 2 + v_rows * D * 2 + B * H * D * 2 * 2 + B * H * 4
-
-    for _ in range(args.warmup):
-        flash.decode_systematic_batched(q, K, V, S, seed=seed)
-    torch.cuda.synchronize()
-    stream = torch.cuda.current_stream()
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    e0.record(stream)
-    for _ in range(args.steps):
-        flash.decode_systematic_batched(q, K, V, S, seed=seed)
-    e1.record(stream)
-    torch.cuda.synchronize()
-    wall = time.perf_counter() - t0
-    ms_step = e0.elapsed_time(e1) / args.steps
-
-    # the dominant kernel (the tile pass) alone, timed with HIP events on the
-    # stream it is launched on (torch's current stream)
-    T_c = (L + 255) // 256
-    ws = torch.empty(flash._workspace_bytes(B, H, KVH, D, T_c), dtype=torch.uint8, device=dev)
-    for _ in range(5):
-        flash._decode_tiles_only(q, K, V, S, seed, 0, -1, ws)
-    torch.cuda.synchronize()
-    k0, k1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    k0.record(stream)
-    for _ in range(args.steps):
-        flash._decode_tiles_only(q, K, V, S, seed, 0, -1, ws)
-    k1.record(stream)
-    torch.cuda.synchronize()
-    ms_kernel = k0.elapsed_time(k1) / args.steps
-
-    achieved = bytes_alg / (ms_kernel * 1e-3) / 1e9
-    default_workload = (B, L, S, seed) == (8, 32768, 256, 1690)
-    traffic = measured_traffic() if default_workload else None
-    line = {
-        "metric": "sampled-attn decode µs/step + achieved HBM TB/s (B=8, 32k ctx, S=256); tokens/s",
-        "value": B / (ms_step * 1e-3),
-        "unit": "tokens/s",
-        "n_gpus": 1,
-        "steps": args.steps,
-        "warmup": args.warmup,
-        "ms_per_step": ms_step,
-        "us_per_step": ms_step * 1e3,
-        "higher_is_better": True,
-        "scaling": "weak",
-        "vs_baseline": None,
-        "dtype": "bf16",
-        "data": "synthetic",
-        "config": {"workload": f"santa_flash decode, Llama-3.1-8B attention shape (32q/8kv, d=128), B={B}, "
-                               f"{L} cached tokens, S={S}, seed {seed}, K/V ~ N(0,1) + rank-4 key bias 0.5",
-                   "global_batch": B, "seq_len": L, "S": S, "parallelism": "single GPU"},
-        "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBPS, "unit": "GB/s",
-                     "frac": achieved / HBM_PEAK_GBPS, "traffic": traffic,
-                     "kernel": ("santa::flash::tile_kernel (block_n 256, online)" if B * T_c * KVH <= 2048
-                                else "santa::flash::wave_kernel (block_n 256, GH 4, rows layout)"),
-                     "kernel_us": ms_kernel * 1e3,
-                     "bytes_alg_per_launch": bytes_alg, "emitted_v_rows": v_rows,
-                     "step_achieved_GBps": bytes_alg / (ms_step * 1e-3) / 1e9},
-        "wall_s_timed": wall,
-    }
-    if not args.no_cpu_baseline:
-        line["cpu_baseline"] = cpu_baseline(q_c, K_c, V_c, S, seed, args.cpu_sample_seqs)
+    if args.workload == "cfg2":
+        line = run_cfg2_paged(args, dev) if args.page_size else run_cfg2(args, dev)
+    else:
+        line = {"cfg3": run_cfg3, "cfg4": run_cfg4, "cfg5": run_cfg5, "cfg5p": run_cfg5p,
+                "single": run_single}[args.workload](args, dev)
     print(json.dumps(line))
     return 0
 

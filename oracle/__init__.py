@@ -66,6 +66,9 @@ def lib() -> ctypes.CDLL:
         L.so_flash_decode.restype = i32
         L.so_flash_decode.argtypes = [P, P, P, i32, i32, i32, i32, i32, i32, i32, i32, u64,
                                       P, P, P, P, P, P, P, P, i32]
+        L.so_flash_decode_at.restype = i32
+        L.so_flash_decode_at.argtypes = [P, P, P, i32, i32, i32, i32, i32, i32, i32, i32, u64,
+                                         P, P, P, P, P, P, P, P, i32, i32]
         L.so_f32_to_h16_array.restype = None
         L.so_f32_to_h16_array.argtypes = [P, P, i64, i32]
         L.so_h16_to_f32_array.restype = None
@@ -151,14 +154,17 @@ def flash_s_per_tile(S: int, T_c: int) -> int:
 
 # ---------------------------------------------------------------- flash
 def flash_decode(q, K, V, S: int, seed: int = 42, block_n: int = 0, valid_len: int = -1,
-                 is_bf16: bool = True, debug: bool = False, nthreads: int = 0) -> Dict[str, np.ndarray]:
+                 is_bf16: bool = True, debug: bool = False, nthreads: int = 0,
+                 b_offset: int = 0) -> Dict[str, np.ndarray]:
     """Oracle of santa_flash_batch_cuda.decode_systematic_batched.
 
     q [B,H,128] or [H,128]; K,V [B,L,KVH,128] or [L,KVH,128] as bf16/f16
     tensors or uint16 bit arrays.  Returns a dict with ``out16`` (bits),
     ``out`` (f32 before the cast), ``m_star`` and, with ``debug``, the tile
     statistics ``m_tiles``, ``ell_tiles``, ``counts`` [B,H,T_c,BN],
-    ``out_tiles`` and ``rowmask``."""
+    ``out_tiles`` and ``rowmask``.  ``b_offset``: these B sequences are
+    sequences b_offset .. b_offset+B-1 of a batch (RNG key (b + b_offset)*H + h),
+    e.g. one sequence of a ragged batch decoded on its own length."""
     qb, Kb, Vb = as_bits(q), as_bits(K), as_bits(V)
     single = qb.ndim == 2
     if single:
@@ -182,11 +188,11 @@ def flash_decode(q, K, V, S: int, seed: int = 42, block_n: int = 0, valid_len: i
         res["counts"] = np.zeros((B, H, T_c, bn), np.int16)
         res["out_tiles"] = np.zeros((B, H, T_c, D), np.float32)
         res["rowmask"] = np.zeros((B, KVH, L), np.int32)
-    rc = lib().so_flash_decode(
+    rc = lib().so_flash_decode_at(
         _ptr(qb), _ptr(Kb), _ptr(Vb), int(is_bf16), B, H, KVH, L, L_st, bn, S_pt, seed & 0xFFFFFFFFFFFFFFFF,
         _ptr(res["out"]), _ptr(res["out16"]), _ptr(res["m_star"]), _ptr(res.get("m_tiles")),
         _ptr(res.get("ell_tiles")), _ptr(res.get("counts")), _ptr(res.get("out_tiles")),
-        _ptr(res.get("rowmask")), int(nthreads))
+        _ptr(res.get("rowmask")), int(nthreads), int(b_offset))
     if rc != 0:
         raise RuntimeError(f"so_flash_decode failed: {rc}")
     if debug:

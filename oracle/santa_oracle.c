@@ -324,10 +324,13 @@ static void tile_pv(const int16_t* c_g, const int* emit, int ne, const uint16_t*
 /*   m_tiles, ell_tiles [B,H,T_c]; counts [B,H,T_c*BN] int16;            */
 /*   out_tiles [B,H,T_c,128]; rowmask [B,KVH,L_valid] int32.             */
 /* ------------------------------------------------------------------ */
-int so_flash_decode(const uint16_t* Q, const uint16_t* K, const uint16_t* V, int is_bf16, int B, int H,
-                    int KVH, int L_valid, int L_storage, int BN, int S_pt, uint64_t seed, float* out_f32,
-                    uint16_t* out16, float* m_star, float* m_tiles_o, float* ell_tiles_o, int16_t* counts_o,
-                    float* out_tiles_o, int* rowmask, int nthreads) {
+/* b_offset: sequence b of these inputs is sequence b + b_offset of the     */
+/* batch, so its RNG key is (b + b_offset) * H + h (flash/santa_cuda_       */
+/* kernel.cu:281) -- one sequence of a ragged batch decoded on its own.    */
+int so_flash_decode_at(const uint16_t* Q, const uint16_t* K, const uint16_t* V, int is_bf16, int B, int H,
+                       int KVH, int L_valid, int L_storage, int BN, int S_pt, uint64_t seed, float* out_f32,
+                       uint16_t* out16, float* m_star, float* m_tiles_o, float* ell_tiles_o, int16_t* counts_o,
+                       float* out_tiles_o, int* rowmask, int nthreads, int b_offset) {
   if (KVH <= 0 || H % KVH != 0) return -1;
   const int GH = H / KVH;
   if (GH > SO_MAX_GH || BN > SO_MAX_BN || (BN != 32 && BN != 64 && BN != 256)) return -2;
@@ -371,7 +374,7 @@ int so_flash_decode(const uint16_t* Q, const uint16_t* K, const uint16_t* V, int
     for (int g = 0; g < GH; ++g) {
       const float ell = ts.ell[g];
       const float invdel = (S_pt > 0 && ell > 1e-20f) ? ((float)S_pt / ell) : 0.0f;
-      const float a0 = so_u01(seed, b * H + h0 + g, t);
+      const float a0 = so_u01(seed, (b + b_offset) * H + h0 + g, t);
       tile_counts(ts.ub + g, GH, len, invdel, a0, is_bf16, c + (size_t)g * BN);
     }
     int emit[SO_MAX_BN];
@@ -456,6 +459,14 @@ int so_flash_decode(const uint16_t* Q, const uint16_t* K, const uint16_t* V, int
   free(ell_tiles);
   free(out_tiles);
   return 0;
+}
+
+int so_flash_decode(const uint16_t* Q, const uint16_t* K, const uint16_t* V, int is_bf16, int B, int H,
+                    int KVH, int L_valid, int L_storage, int BN, int S_pt, uint64_t seed, float* out_f32,
+                    uint16_t* out16, float* m_star, float* m_tiles_o, float* ell_tiles_o, int16_t* counts_o,
+                    float* out_tiles_o, int* rowmask, int nthreads) {
+  return so_flash_decode_at(Q, K, V, is_bf16, B, H, KVH, L_valid, L_storage, BN, S_pt, seed, out_f32, out16,
+                            m_star, m_tiles_o, ell_tiles_o, counts_o, out_tiles_o, rowmask, nthreads, 0);
 }
 
 /* ------------------------------------------------------------------ */

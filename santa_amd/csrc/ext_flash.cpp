@@ -9,6 +9,7 @@
 
 #include <cstdint>
 #include <algorithm>
+#include <string>
 #include <tuple>
 #include <vector>
 
@@ -415,6 +416,37 @@ at::Tensor device_expf(at::Tensor x) {
   return y;
 }
 
+// Test-only: the score path's broadcast MFMA and fmaf on the same operands;
+// a, b [n, 64], c [n, 64, 4] float32 CUDA tensors -> (mfma, fma) [n, 16, 64, 4].
+std::tuple<at::Tensor, at::Tensor> mfma_fma_check(at::Tensor a, at::Tensor b, at::Tensor c) {
+  TORCH_CHECK(a.is_cuda() && a.scalar_type() == at::kFloat && a.dim() == 2 && a.size(1) == 64,
+              "a must be a CUDA float32 tensor [n, 64]");
+  TORCH_CHECK(b.is_cuda() && b.scalar_type() == at::kFloat && b.sizes() == a.sizes(), "b must match a");
+  TORCH_CHECK(c.is_cuda() && c.scalar_type() == at::kFloat && c.dim() == 3 && c.size(0) == a.size(0) &&
+                  c.size(1) == 64 && c.size(2) == 4,
+              "c must be a CUDA float32 tensor [n, 64, 4]");
+  c10::DeviceGuard guard(a.device());
+  const at::Tensor ac = a.contiguous(), bc = b.contiguous(), cc = c.contiguous();
+  at::Tensor mo = at::empty({a.size(0), 16, 64, 4}, a.options());
+  at::Tensor fo = at::empty_like(mo);
+  const hipError_t e = santa::flash::launch_mfma_check(ac.data_ptr<float>(), bc.data_ptr<float>(),
+                                                       cc.data_ptr<float>(), mo.data_ptr<float>(),
+                                                       fo.data_ptr<float>(), static_cast<int>(a.size(0)),
+                                                       current_stream(ac));
+  TORCH_CHECK(e == hipSuccess, "mfma check launch failed: ", hipGetErrorString(e));
+  return {mo, fo};
+}
+
+// The kernel santa_flash_decode_tiles runs for this shape (bench label).
+std::string tile_pass_kernel(int64_t B, int64_t H, int64_t KVH, int64_t T_c, int64_t block_n) {
+  TORCH_CHECK(B > 0 && H > 0 && KVH > 0 && H % KVH == 0 && T_c > 0, "bad shape");
+  const std::string gh = "GH " + std::to_string(H / KVH);
+  if (block_n == 256 && !santa::flash::small_pass(B * KVH * T_c))
+    return "santa::flash::wave_kernel (block_n 256, " + gh +
+           (santa::flash::rows_layout(static_cast<int>(KVH)) ? ", rows layout)" : ", four-wave layout)");
+  return "santa::flash::tile_kernel (block_n " + std::to_string(block_n) + ", " + gh + ", online)";
+}
+
 int64_t workspace_bytes(int64_t B, int64_t H, int64_t KVH, int64_t D, int64_t T_c) {
   return static_cast<int64_t>(santa_flash_workspace_size(static_cast<int>(B), static_cast<int>(H),
                                                          static_cast<int>(KVH), static_cast<int>(D),
@@ -444,6 +476,9 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
   m.def("_decode_tiles_only", &decode_tiles_only, py::arg("q_h"), py::arg("K_g"), py::arg("V_g"), py::arg("S"),
         py::arg("seed"), py::arg("block_n"), py::arg("valid_len"), py::arg("ws"));
   m.def("_workspace_bytes", &workspace_bytes);
+  m.def("_tile_pass_kernel", &tile_pass_kernel, py::arg("B"), py::arg("H"), py::arg("KVH"), py::arg("T_c"),
+        py::arg("block_n"));
   m.def("_device_expf", &device_expf, py::arg("x"));
+  m.def("_mfma_fma_check", &mfma_fma_check, py::arg("a"), py::arg("b"), py::arg("c"));
   m.def("_library_version", []() { return std::string(santa_version()); });
 }

@@ -49,6 +49,7 @@
 
 #include <algorithm>
 #include <type_traits>
+#include <utility>
 
 namespace santa {
 namespace flash {
@@ -1706,6 +1707,47 @@ hipError_t launch_expf(const float* x, float* y, size_t n, hipStream_t stream) {
   const size_t blocks = (n + kThreads - 1) / kThreads;
   hipLaunchKernelGGL(expf_kernel, dim3(static_cast<unsigned>(blocks < 65536 ? blocks : 65536)), dim3(kThreads), 0,
                      stream, x, y, n);
+  return hipGetLastError();
+}
+
+// The score path's K=1 MFMA against fmaf on the same operands (test hook,
+// declared in santa_internal.h).  Wave n reads a[64n + l], b[64n + l] and
+// c[4(64n + l) + i] at lane l; for every broadcast block J it writes
+// mfma_out / fma_out[((16n + J) * 64 + l) * 4 + i] =
+// a[64n + 4J + i] * b[64n + l] + c[4(64n + l) + i], once through
+// v_mfma_f32_4x4x1f32 with the A operand of block J broadcast (the form
+// score_chunk issues) and once through fmaf.
+template <int J>
+__device__ __forceinline__ void mfma_fma_block(float a, float b, f32x4 c, int lane, size_t base, float* mo,
+                                               float* fo) {
+  const f32x4 d = mfma_bcast<J>(a, b, c);
+  const size_t o = (base + static_cast<size_t>(J) * 64 + lane) * 4;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const float ai = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(a), 4 * J + i));
+    mo[o + i] = d[i];
+    fo[o + i] = fmaf(ai, b, c[i]);
+  }
+}
+template <int... J>
+__device__ __forceinline__ void mfma_fma_blocks(std::integer_sequence<int, J...>, float a, float b, f32x4 c,
+                                                int lane, size_t base, float* mo, float* fo) {
+  (mfma_fma_block<J>(a, b, c, lane, base, mo, fo), ...);
+}
+__global__ __launch_bounds__(64) void mfma_fma_kernel(const float* __restrict__ a, const float* __restrict__ b,
+                                                      const float* __restrict__ c, float* __restrict__ mo,
+                                                      float* __restrict__ fo) {
+  const int lane = static_cast<int>(threadIdx.x);
+  const size_t n = blockIdx.x;
+  const size_t i = n * 64 + lane;
+  const f32x4 cv = {c[4 * i], c[4 * i + 1], c[4 * i + 2], c[4 * i + 3]};
+  mfma_fma_blocks(std::make_integer_sequence<int, 16>{}, a[i], b[i], cv, lane, n * 16 * 64, mo, fo);
+}
+hipError_t launch_mfma_check(const float* a, const float* b, const float* c, float* mfma_out, float* fma_out,
+                             int n_waves, hipStream_t stream) {
+  if (n_waves <= 0) return hipSuccess;
+  hipLaunchKernelGGL(mfma_fma_kernel, dim3(static_cast<unsigned>(n_waves)), dim3(64), 0, stream, a, b, c, mfma_out,
+                     fma_out);
   return hipGetLastError();
 }
 

@@ -68,6 +68,11 @@ hipError_t launch_wave_debug(const void* q, const void* K, const void* V, int dt
                              float* ell_tiles, int16_t* counts, hipStream_t stream);
 // y[i] = santa_expf(x[i]) on the device (test hook for the exponential).
 hipError_t launch_expf(const float* x, float* y, size_t n, hipStream_t stream);
+// The score path's broadcast K=1 MFMA and fmaf on the same operands (test
+// hook): n_waves waves; a, b [64 n_waves], c [4 * 64 n_waves]; outputs
+// [n_waves, 16 blocks, 64 lanes, 4].
+hipError_t launch_mfma_check(const float* a, const float* b, const float* c, float* mfma_out, float* fma_out,
+                             int n_waves, hipStream_t stream);
 // Chunks of cs tiles per workgroup, cpg chunks per (b, kv) group, sized to
 // about one resident round of 256-thread workgroups on the current device.
 void plan_chunks(int B, int KVH, int T_c, int* cs, int* cpg);

@@ -25,6 +25,8 @@ from ._C import (  # noqa: F401
     _decode_tiles_only,
     _device_expf,
     _library_version,
+    _mfma_fma_check,
+    _tile_pass_kernel,
     _workspace_bytes,
     decode_systematic_batched,
     decode_systematic_paged,

@@ -56,3 +56,19 @@ def tol_check(got: np.ndarray, ref: np.ndarray, max_abs=2e-2, mean_rel=1e-3):
     mabs = float(err.max()) if err.size else 0.0
     mrel = float(err.sum() / max(np.abs(ref).sum(), 1e-30)) if err.size else 0.0
     return mabs <= max_abs and mrel <= mean_rel, mabs, mrel
+
+
+def flash_oracle_sequence(q, K, V, b, Lb, S, bn, seed=SEED, is_bf16=True):
+    """The oracle of sequence b of a ragged flash batch on its own (CPU
+    tensors): its first Lb tokens, S_per_tile from its own tile count, RNG
+    key b*H + h -- what the ragged call does for that sequence."""
+    import oracle
+
+    return oracle.flash_decode(q[b:b + 1], K[b:b + 1, :Lb], V[b:b + 1, :Lb], S, seed=seed, block_n=bn,
+                               is_bf16=is_bf16, debug=True, b_offset=b)
+
+
+def seeded_lens(B, lo, hi, seed):
+    """B lengths drawn uniformly from [lo, hi] by a seeded CPU generator."""
+    g = torch.Generator().manual_seed(seed)
+    return torch.randint(lo, hi + 1, (B,), generator=g).tolist()

@@ -260,3 +260,34 @@ def test_cfg5_shape_parity():
     np.testing.assert_array_equal(vr.cpu().numpy(), exp["vrows"], err_msg="vrows")
     ok, mabs, mrel = tol_check(h16_to_f32(bits16(out)), h16_to_f32(exp["out16"]))
     assert ok, ("vs oracle", mabs, mrel)
+
+
+@pytest.mark.parametrize("valid_len", [32769, 32832])
+def test_cfg4_attention_shape_parity(valid_len):
+    """The attention call of cfg4's decode loop (tutorial_code/runtime_common.py:
+    553-557): B=4, 32q/8kv, a 32832-token cache of which the first valid_len
+    are valid (32769 at the first decode step, 32832 at the last), S=256, so
+    block_n 256, T_c = 129 and S_per_tile = 1, with a last tile of 1 or 64
+    rows.  The production wave kernel's tile max, tile mass and every count
+    bit-exact to the oracle, m* and vrows exact, the output within the bf16
+    tolerance."""
+    B, H, KVH, L_st, S = 4, 32, 8, 32832, 256
+    _announce(f"cfg4 attention shape B={B} H={H} KVH={KVH} L_storage={L_st} valid_len={valid_len} S={S}")
+    m = _mod()
+    q, K, V = gen_qkv(B, H, KVH, L_st, seed=SEED + valid_len, lowrank=0.5)
+    dev = torch.device("cuda:0")
+    qd, Kd, Vd = q.to(dev), K.to(dev), V.to(dev)
+    mt, lt, cnt = m._debug_wave(qd, Kd, Vd, S, seed=SEED, valid_len=valid_len)
+    out, ms, vr = m.decode_systematic_batched(qd, Kd, Vd, S, seed=SEED, want_vrows=True, valid_len=valid_len)
+    torch.cuda.synchronize()
+    exp = oracle.flash_decode(q, K, V, S, seed=SEED, valid_len=valid_len, is_bf16=True, debug=True)
+    assert (exp["block_n"], exp["T_c"], exp["S_per_tile"]) == (256, 129, 1)
+    np.testing.assert_array_equal(mt.cpu().numpy().view(np.uint32), exp["m_tiles"].view(np.uint32), err_msg="m_tiles")
+    np.testing.assert_array_equal(lt.cpu().numpy().view(np.uint32), exp["ell_tiles"].view(np.uint32),
+                                  err_msg="ell_tiles")
+    c_gpu = cnt.cpu().numpy()
+    assert np.array_equal(c_gpu, exp["counts"]), f"counts differ at {np.argwhere(c_gpu != exp['counts'])[:8]}"
+    np.testing.assert_array_equal(ms.cpu().numpy().view(np.uint32), exp["m_star"].view(np.uint32), err_msg="m_star")
+    np.testing.assert_array_equal(vr.cpu().numpy(), exp["vrows"], err_msg="vrows")
+    ok, mabs, mrel = tol_check(h16_to_f32(bits16(out)), h16_to_f32(exp["out16"]))
+    assert ok, ("vs oracle", mabs, mrel)

@@ -15,8 +15,7 @@ import numpy as np
 import pytest
 import torch
 
-import oracle
-from helpers import SEED, bits16, gen_qkv, h16_to_f32, tol_check
+from helpers import SEED, bits16, flash_oracle_sequence, gen_qkv, h16_to_f32, seeded_lens, tol_check
 
 pytestmark = pytest.mark.gpu
 
@@ -58,19 +57,19 @@ def _run(H, KVH, lens, S, block_n, dtype=torch.bfloat16, L_st=None, as_tensor=Fa
         if S <= 0:
             assert not got.any(), f"b={b}: S <= 0 must give a zero output"
         if oracle_check:
-            exp = oracle.flash_decode(q, K, V, S, seed=SEED, block_n=bn, valid_len=Lb, is_bf16=is_bf16, debug=True)
-            np.testing.assert_array_equal(ms[b].cpu().numpy().view(np.uint32), exp["m_star"][b].view(np.uint32))
-            np.testing.assert_array_equal(vr[b].cpu().numpy(), exp["vrows"][b])
-            ok, mabs, mrel = tol_check(got, h16_to_f32(exp["out16"][b], is_bf16))
+            exp = flash_oracle_sequence(q, K, V, b, Lb, S, bn, is_bf16=is_bf16)
+            np.testing.assert_array_equal(ms[b].cpu().numpy().view(np.uint32), exp["m_star"][0].view(np.uint32))
+            np.testing.assert_array_equal(vr[b].cpu().numpy(), exp["vrows"][0])
+            ok, mabs, mrel = tol_check(got, h16_to_f32(exp["out16"][0], is_bf16))
             assert ok, (f"b={b} vs oracle", mabs, mrel)
 
 
 @pytest.mark.parametrize(
     "H,KVH,lens,S,block_n",
     [
-        (32, 8, [9000, 3100, 5000, 4097], 256, 0),   # wave kernel, ragged grid
+        (32, 8, [9000, 3100, 5000, 4097], 256, 0),   # block_n 256, few tiles: tile kernel, ragged grid
         (32, 8, [9000, 1, 257, 8999, 6000], 300, 0),  # one-token and one-row tiles
-        (64, 8, [5000, 300, 7000], 512, 256),       # GH=8
+        (64, 8, [5000, 300, 7000], 512, 256),       # GH=8 (tile kernel)
         (32, 8, [1000, 200, 33, 1500], 64, 0),      # block_n 32 (tile kernel, ragged grid)
         (32, 8, [2000, 3000, 1700], 96, 0),         # block_n 64
         (32, 8, [6000, 4000], 0, 0),                # S = 0
@@ -82,6 +81,19 @@ def test_flash_ragged_parity(H, KVH, lens, S, block_n):
 
 def test_flash_ragged_against_oracle():
     _run(32, 8, [4096, 3500, 300], 128, 256, L_st=4096, as_tensor=True, oracle_check=True)
+
+
+@pytest.mark.parametrize("H,S", [(32, 256), (64, 512)])
+def test_flash_ragged_wave_kernel_against_oracle(H, S):
+    """The production ragged wave kernel (GH 4 and GH 8): every sequence's m*
+    and vrows exact against the oracle, the output within the bf16
+    tolerance, and against the uniform call per sequence."""
+    # lengths in [9000, 40000]: more (kv, tile) items than one resident
+    # round, so the ragged grid runs the production wave kernel (rows
+    # layout, ragged chunk plan)
+    lens = seeded_lens(8, 9000, 40000, SEED + H)
+    assert sum((l + 255) // 256 for l in lens) * 8 > 2048
+    _run(H, 8, lens, S, 0, oracle_check=True)
 
 
 def test_flash_ragged_f16():

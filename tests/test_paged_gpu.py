@@ -5,7 +5,8 @@ int32 block table.  It runs the same kernels, chunk plan and merge as the
 contiguous call on the same tokens (ragged flash, batched prop); only the
 row addressing differs.  So its results must be bit-identical to that call,
 which is itself pinned to the oracle (tests/test_flash_ragged_gpu.py,
-tests/test_prop_batched_gpu.py).  The one exception is a prop batch whose
+tests/test_prop_batched_gpu.py); the production-sized cases are also
+compared with the oracle directly, sequence by sequence.  The one exception is a prop batch whose
 sequences plan to different block sizes: it is decoded one paged launch per
 sequence, while the contiguous call runs the scalar path per sequence.
 There m* and vrows must be identical, and the output must agree to the
@@ -22,7 +23,8 @@ import numpy as np
 import pytest
 import torch
 
-from helpers import SEED, bits16, gen_qkv, h16_to_f32, tol_check
+import oracle
+from helpers import SEED, bits16, flash_oracle_sequence, gen_qkv, h16_to_f32, seeded_lens, tol_check
 
 pytestmark = pytest.mark.gpu
 
@@ -76,7 +78,7 @@ def _inputs(B, H, KVH, lens, page_size, dtype, seed):
 @pytest.mark.parametrize(
     "H,KVH,lens,S,page_size,block_n,dtype",
     [
-        (32, 8, [9000, 3100, 5000, 4097], 256, 16, 0, torch.bfloat16),  # wave kernel, 16-token pages
+        (32, 8, [9000, 3100, 5000, 4097], 256, 16, 0, torch.bfloat16),  # few tiles: tile kernel, 16-token pages
         (32, 8, [9000, 1, 257, 8999], 300, 8, 0, torch.bfloat16),       # 8-token pages, a one-token sequence
         (32, 8, [7000, 6000, 5000], 256, 256, 0, torch.bfloat16),       # one page per tile
         (32, 8, [7000, 6000], 256, 1024, 0, torch.bfloat16),            # tiles inside pages
@@ -128,6 +130,64 @@ def test_prop_paged_matches_contiguous(H, KVH, lens, Ss, page_size, block_n, env
     ref = m.decode_systematic_batched(q, K, V, Ss, seed=SEED, block_n=block_n, want_vrows=True, valid_len=lens)
     torch.cuda.synchronize()
     _check(got, ref, exact, True, "paged vs contiguous")
+
+
+def _oracle_checks(got, q, K, V, lens, what, oracle_of):
+    """Per sequence: m* bit-exact and vrows exact against the oracle, the
+    output within the bf16 tolerance."""
+    out, ms, vr = (t.cpu() for t in got)
+    qc, Kc, Vc = q.cpu(), K.cpu(), V.cpu()
+    for b, Lb in enumerate(lens):
+        exp = oracle_of(qc, Kc, Vc, b, Lb)
+        np.testing.assert_array_equal(ms[b].numpy().view(np.uint32), exp["m_star"].reshape(-1).view(np.uint32),
+                                      err_msg=f"{what}: m_star b={b}")
+        np.testing.assert_array_equal(vr[b].numpy(), exp["vrows"].reshape(-1), err_msg=f"{what}: vrows b={b}")
+        ok, mabs, mrel = tol_check(h16_to_f32(bits16(out[b])), h16_to_f32(exp["out16"].reshape(out[b].shape)))
+        assert ok, (f"{what}: b={b} vs oracle", mabs, mrel)
+
+
+@pytest.mark.parametrize("H,S,page_size", [(32, 256, 16), (32, 256, 256), (64, 512, 16), (64, 512, 256)])
+def test_flash_paged_wave_kernel_against_oracle(H, S, page_size):
+    """The production paged wave kernel (lengths in [9000, 40000]: more
+    (kv, tile) items than one resident round; GH 4 and 8; pages of 16 and
+    256 tokens): bit-identical to the contiguous ragged call, and every
+    sequence's m* and vrows exact against the oracle, its output within the
+    bf16 tolerance."""
+    import santa_flash_batch_cuda as m
+
+    lens = seeded_lens(8, 9000, 40000, SEED + H + page_size)
+    assert sum((l + 255) // 256 for l in lens) * 8 > 2048
+    seed = SEED + 13 * H + page_size
+    print(f"\n[case] flash paged wave kernel vs oracle H={H} lens={lens} S={S} page_size={page_size} seed={seed}",
+          flush=True)
+    q, K, V, Kp, Vp, table = _inputs(len(lens), H, 8, lens, page_size, torch.bfloat16, seed)
+    got = m.decode_systematic_paged(q, Kp, Vp, table, lens, S, seed=SEED, want_vrows=True)
+    ref = m.decode_systematic_batched(q, K, V, S, seed=SEED, want_vrows=True, valid_len=lens)
+    torch.cuda.synchronize()
+    _check(got, ref, True, True, "paged vs contiguous")
+    _oracle_checks(got, q, K, V, lens, "flash paged",
+                   lambda qc, Kc, Vc, b, Lb: flash_oracle_sequence(qc, Kc, Vc, b, Lb, S, 256))
+
+
+@pytest.mark.parametrize("H,page_size", [(32, 16), (64, 256)])
+def test_prop_paged_against_oracle(H, page_size, monkeypatch):
+    """Paged batched santa_prop on lengths in [9000, 40000] with S_b = L_b // 64
+    (GH 4: the vec pass 1 on the wave kernel; GH 8: the general pass 1):
+    every sequence's m* and vrows exact against the oracle of the
+    per-sequence call, its output within the bf16 tolerance."""
+    import santa_prop_batch_cuda as m
+
+    monkeypatch.delenv("SANTA_PASS1", raising=False)
+    lens = seeded_lens(6, 9000, 40000, SEED + 2 * H + page_size)
+    Ss = [l // 64 for l in lens]
+    seed = SEED + 17 * H + page_size
+    print(f"\n[case] prop paged vs oracle H={H} lens={lens} S={Ss} page_size={page_size} seed={seed}", flush=True)
+    q, K, V, Kp, Vp, table = _inputs(len(lens), H, 8, lens, page_size, torch.bfloat16, seed)
+    got = m.decode_systematic_paged(q, Kp, Vp, table, lens, Ss, seed=SEED, want_vrows=True)
+    torch.cuda.synchronize()
+    _oracle_checks(got, q, K, V, lens, "prop paged",
+                   lambda qc, Kc, Vc, b, Lb: oracle.prop_decode(qc[b], Kc[b, :Lb], Vc[b, :Lb], Ss[b], seed=SEED,
+                                                                debug=True))
 
 
 def test_paged_argument_errors():

@@ -160,3 +160,42 @@ def test_cfg3_workload_parity():
         np.testing.assert_array_equal(vr[b].cpu().numpy(), exp["vrows"], err_msg=f"vrows b={b}")
         ok, mabs, mrel = tol_check(h16_to_f32(bits16(out[b])), h16_to_f32(exp["out16"]))
         assert ok, (f"b={b} vs oracle", mabs, mrel)
+
+
+def test_cfg5_prop_leg_parity():
+    """cfg5's santa_prop leg (bench.py --workload cfg5p): 64q/8kv (GH 8, the
+    general pass 1), L=131072, Student-t(3) keys with planted needles, S=512
+    per sequence (the flash leg's budget), on 2 sequences of the batched call:
+    m* and vrows exact against the oracle, the output within the bf16
+    tolerance; for sequence 0 also the stage outputs -- tile max and mass, the
+    u stash, the budgets S_t, invdelta_t, a0_t and every sampled count --
+    bit-exact."""
+    import bench
+    import santa_prop_batch_cuda as m
+
+    B, H, KVH, L, S = 2, 64, 8, 131072, 512
+    print(f"\n[case] prop cfg5 leg B={B} H={H} KVH={KVH} L={L} S={S} needles seed={SEED}", flush=True)
+    dev = torch.device("cuda:0")
+    q, K, V = bench.device_inputs(B, L, H, KVH, 128, SEED, dev, keys="needles")
+    out, ms, vr = m.decode_systematic_batched(q, K, V, S, seed=SEED, want_vrows=True)
+    dbg = m._debug_pass(q[0].contiguous(), K[0].contiguous(), V[0].contiguous(), S, seed=SEED)
+    torch.cuda.synchronize()
+    mt, lt, mstar, St, inv, a0, stash, cnt, out_d, vr_d = [t.cpu() for t in dbg]
+    qc, Kc, Vc = q.cpu(), K.cpu(), V.cpu()
+    del K, V
+    for b in range(B):
+        exp = oracle.prop_decode(qc[b], Kc[b], Vc[b], S, seed=SEED, debug=True)
+        assert exp["pass1_mode"] == 1 and exp["T_c"] == 512
+        np.testing.assert_array_equal(ms[b].cpu().numpy().view(np.uint32), exp["m_star"].view(np.uint32),
+                                      err_msg=f"m_star b={b}")
+        np.testing.assert_array_equal(vr[b].cpu().numpy(), exp["vrows"], err_msg=f"vrows b={b}")
+        ok, mabs, mrel = tol_check(h16_to_f32(bits16(out[b])), h16_to_f32(exp["out16"]))
+        assert ok, (f"b={b} vs oracle", mabs, mrel)
+        if b == 0:
+            for name, got in (("m_tiles", mt), ("ell_tiles", lt), ("invdelta", inv), ("a0", a0)):
+                np.testing.assert_array_equal(got.numpy().view(np.uint32), exp[name].view(np.uint32), err_msg=name)
+            np.testing.assert_array_equal(St.numpy(), exp["S_tiles"], err_msg="S_tiles")
+            assert (St.sum(dim=1) == S).all()
+            np.testing.assert_array_equal(bits16(stash), exp["u_stash"], err_msg="u_stash")
+            assert np.array_equal(cnt.numpy(), exp["counts"]), "counts"
+            np.testing.assert_array_equal(vr_d.numpy(), exp["vrows"], err_msg="vrows (stages)")
