@@ -112,6 +112,22 @@ int santa_flash_decode_tiles(const void* q, const void* K, const void* V, int dt
 int santa_flash_decode_merge(const void* workspace, size_t workspace_bytes, int dtype, int B, int H, int KVH, int D,
                              int T_c, int S_per_tile, void* out, float* m_star, int* vrows, hipStream_t stream);
 
+/* santa_flash_decode without a workspace argument, for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving
+ * loops, harnesses that forbid hipMalloc).  No counterpart in the reference.
+ * The workspace lives in a static device array of 16 MiB (16,777,216
+ * bytes) that each device holds until the process ends; shapes whose
+ * santa_flash_workspace_size exceeds it are rejected with
+ * SANTA_ERR_WORKSPACE before anything is launched.  The call makes no hipMalloc / hipFree or other allocation.
+ * The array needs no initialisation (every kernel writes what a later one
+ * reads).  Every call on a device shares that device's array: calls that
+ * overlap on one device (different streams, or host threads) race and must
+ * be ordered by the caller.  Results are bit-identical to santa_flash_decode
+ * on the same arguments. */
+int santa_flash_decode_noalloc(const void* q, const void* K, const void* V, int dtype, int B, int H, int KVH, int D,
+                               int L_valid, int L_storage, int block_n, int S_per_tile, uint64_t seed, void* out,
+                               float* m_star, int* vrows, hipStream_t stream);
+
 /* Ragged flash (no counterpart in the reference, whose batched call takes
  * one valid_len for every sequence, flash/santa_cuda.cpp:188): sequence b of
  * a [B, L_storage, KVH, D] cache is decoded on its first seq_lens[b] tokens

@@ -50,6 +50,7 @@
 #include <algorithm>
 #include <type_traits>
 #include <utility>
+#include <mutex>
 
 namespace santa {
 namespace flash {
@@ -2060,6 +2061,70 @@ extern "C" int santa_flash_decode(const void* q, const void* K, const void* V, i
   if (st != SANTA_OK) return st;
   return santa_flash_decode_merge(workspace, workspace_bytes, dtype, B, H, KVH, D, (L_valid + block_n - 1) / block_n,
                                   S_per_tile, out, m_star, vrows, stream);
+}
+
+// ------------------------------------------------- allocation-free decode
+// santa_flash_decode with its workspace (the chunk partials and per-chunk
+// emitted-row counts) in this file-scope device array instead of caller or
+// allocator memory.  Each device holds its own copy for the life of the
+// process.  Host code never passes the array's name to a kernel or a copy:
+// the name is a host-side stand-in, not a device address.  Its address on a
+// device comes from hipGetSymbolAddress, taken once per device with that
+// device current and kept in s_scratch_ptr.
+namespace {
+constexpr size_t kScratchBytes = size_t{16} << 20;
+constexpr int kMaxDevices = 64;
+__device__ __align__(256) unsigned char scratch[kScratchBytes];
+std::mutex s_scratch_mu;
+void* s_scratch_ptr[kMaxDevices];
+
+// The scratch array's address on the current device (nullptr and the
+// error recorded on failure).
+void* scratch_on_current_device(int* status) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) {
+    *status = set_error(SANTA_ERR_HIP, "hipGetDevice failed: %s", hipGetErrorString(e));
+    return nullptr;
+  }
+  if (dev < 0 || dev >= kMaxDevices) {
+    *status = set_error(SANTA_ERR_UNSUPPORTED, "device %d: at most %d devices are supported", dev, kMaxDevices);
+    return nullptr;
+  }
+  std::lock_guard<std::mutex> lock(s_scratch_mu);
+  if (!s_scratch_ptr[dev]) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p) {
+      *status = set_error(SANTA_ERR_HIP, "hipGetSymbolAddress(scratch) failed on device %d: %s", dev,
+                          hipGetErrorString(e));
+      return nullptr;
+    }
+    s_scratch_ptr[dev] = p;
+  }
+  *status = SANTA_OK;
+  return s_scratch_ptr[dev];
+}
+}  // namespace
+
+extern "C" int santa_flash_decode_noalloc(const void* q, const void* K, const void* V, int dtype, int B, int H,
+                                          int KVH, int D, int L_valid, int L_storage, int block_n, int S_per_tile,
+                                          uint64_t seed, void* out, float* m_star, int* vrows, hipStream_t stream) {
+  int st = check_flash_shape(dtype, B, H, KVH, D, L_valid, L_storage, block_n);
+  if (st != SANTA_OK) return st;
+  if (!q || !K || !V || !out) return set_error(SANTA_ERR_INVALID, "null pointer argument");
+  const int T_c = (L_valid + block_n - 1) / block_n;
+  // checked before any HIP call: a shape beyond the scratch array launches nothing
+  const size_t need = flash_ws_layout(B, H, KVH, T_c).total;
+  if (need > kScratchBytes)
+    return set_error(SANTA_ERR_WORKSPACE,
+                     "santa_flash_decode_noalloc: this shape needs %zu bytes of scratch; the static scratch holds "
+                     "%zu (use santa_flash_decode with a workspace)",
+                     need, kScratchBytes);
+  void* ws = scratch_on_current_device(&st);
+  if (!ws) return st;
+  return santa_flash_decode(q, K, V, dtype, B, H, KVH, D, L_valid, L_storage, block_n, S_per_tile, seed, out, m_star,
+                            vrows, ws, kScratchBytes, stream);
 }
 
 // ------------------------------------------------------------ ragged flash

@@ -204,3 +204,25 @@ def test_extension_surfaces():
     with pytest.raises(TypeError):
         flash.decode_systematic_scalar(q, K, K, 8, seed=-1)
     assert "gfx950" in flash._library_version() and "gfx950" in prop._library_version()
+
+
+def test_noalloc_rejects_shapes_beyond_its_scratch(lib):
+    """santa_flash_decode_noalloc checks the workspace its shape needs against
+    its 16 MiB static scratch before any HIP call (so this runs without a
+    GPU; the pointers are never dereferenced): B=1024, 64q/8kv, one 256-row
+    tile each needs 8192 chunk partials of 8 heads, about 34 MB."""
+    P, I, U64 = ctypes.c_void_p, ctypes.c_int, ctypes.c_uint64
+    lib.santa_flash_decode_noalloc.argtypes = [P, P, P] + [I] * 9 + [U64, P, P, P, P]
+    lib.santa_flash_workspace_size.restype = ctypes.c_size_t
+    need = lib.santa_flash_workspace_size(1024, 64, 8, 128, 1)
+    assert need > 16 << 20
+    dummy = ctypes.c_void_p(0x1000)
+    rc = lib.santa_flash_decode_noalloc(dummy, dummy, dummy, 0, 1024, 64, 8, 128, 256, 256, 256, 1, 1690, dummy, None,
+                                        None, None)
+    assert rc == ERR_WORKSPACE
+    msg = lib.santa_last_error().decode()
+    assert "needs" in msg and str(16 << 20) in msg and str(need) in msg, msg
+    # argument errors come first, as in santa_flash_decode
+    rc = lib.santa_flash_decode_noalloc(dummy, dummy, dummy, 0, 1, 32, 8, 64, 256, 256, 256, 1, 1690, dummy, None,
+                                        None, None)
+    assert rc == ERR_UNSUPPORTED and "D=128" in lib.santa_last_error().decode()
