@@ -78,6 +78,9 @@ def lib() -> ctypes.CDLL:
         L.so_prop_decode.restype = i32
         L.so_prop_decode.argtypes = [P, P, P, i32, i32, i32, i32, i32, i32, u64, i32,
                                      P, P, P, P, P, P, P, P, P, P, P]
+        L.so_prop_decode_d.restype = i32
+        L.so_prop_decode_d.argtypes = [P, P, P, i32, i32, i32, i32, i32, i32, i32, u64, i32,
+                                       P, P, P, P, P, P, P, P, P, P, P]
         _lib = L
     return _lib
 
@@ -232,7 +235,8 @@ def prop_pass1_mode(GH: int, D: int, bn: int, env: Optional[str] = None) -> int:
 def prop_decode(q, K, V, S: int, seed: int = 42, block_n: int = 0, is_bf16: bool = True,
                 pass1_mode: Optional[int] = None, debug: bool = False) -> Dict[str, np.ndarray]:
     """Oracle of santa_prop_batch_cuda.decode_systematic_scalar for one sequence:
-    q [H,128]; K,V [L,KVH,128]."""
+    q [H,D]; K,V [L,KVH,D] (D a multiple of 16 up to 256; block_n a multiple
+    of 16 up to 512)."""
     qb, Kb, Vb = as_bits(q), as_bits(K), as_bits(V)
     H, D = qb.shape
     L, KVH = Kb.shape[0], Kb.shape[1]
@@ -254,8 +258,8 @@ def prop_decode(q, K, V, S: int, seed: int = 42, block_n: int = 0, is_bf16: bool
         res["u_stash"] = np.zeros((L, H), np.uint16)
         res["counts"] = np.zeros((H, T_c, bn), np.int16)
         res["rowmask"] = np.zeros((KVH, L), np.int32)
-    rc = lib().so_prop_decode(
-        _ptr(qb), _ptr(Kb), _ptr(Vb), int(is_bf16), H, KVH, L, bn, int(S), seed & 0xFFFFFFFFFFFFFFFF, mode,
+    rc = lib().so_prop_decode_d(
+        _ptr(qb), _ptr(Kb), _ptr(Vb), int(is_bf16), H, KVH, D, L, bn, int(S), seed & 0xFFFFFFFFFFFFFFFF, mode,
         _ptr(res["out"]), _ptr(res["out16"]), _ptr(res["m_star"]), _ptr(res.get("m_tiles")),
         _ptr(res.get("ell_tiles")), _ptr(res.get("S_tiles")), _ptr(res.get("invdelta")), _ptr(res.get("a0")),
         _ptr(res.get("u_stash")), _ptr(res.get("counts")), _ptr(res.get("rowmask")))

@@ -36,9 +36,10 @@
 #include <omp.h>
 #endif
 
-#define SO_D 128
+#define SO_D 128      /* flash: the reference's only head_dim */
+#define SO_MAX_D 256  /* prop: any multiple of 16 up to this */
 #define SO_MAX_GH 16
-#define SO_MAX_BN 256
+#define SO_MAX_BN 512
 #define SO_LANES 32
 
 /* ------------------------------------------------------------------ */
@@ -302,15 +303,15 @@ static int tile_emit(const int16_t* c /*[GH][BN]*/, int BN, int GH, int len, int
  * zero counts, one fma per element.  flash/santa_cuda_kernel.cu:347-379
  * (prop/...kernel.cu:843-857 with its a*b+c contracted to fma). */
 static void tile_pv(const int16_t* c_g, const int* emit, int ne, const uint16_t* V, size_t v_row0,
-                    size_t row_stride, int is_bf16, float* acc /*[128]*/) {
-  for (int d = 0; d < SO_D; ++d) acc[d] = 0.0f;
+                    size_t row_stride, int D, int is_bf16, float* acc /*[D]*/) {
+  for (int d = 0; d < D; ++d) acc[d] = 0.0f;
   for (int i = 0; i < ne; ++i) {
     const int r = emit[i];
     const int cc = (int)c_g[r];
     if (cc == 0) continue;
     const float cf = (float)cc;
     const uint16_t* vrow = V + v_row0 + (size_t)r * row_stride;
-    for (int d = 0; d < SO_D; ++d) acc[d] = fmaf(cf, ld16(vrow, (size_t)d, is_bf16), acc[d]);
+    for (int d = 0; d < D; ++d) acc[d] = fmaf(cf, ld16(vrow, (size_t)d, is_bf16), acc[d]);
   }
 }
 
@@ -393,7 +394,7 @@ int so_flash_decode_at(const uint16_t* Q, const uint16_t* K, const uint16_t* V, 
       } else {
         m_tiles[mt] = ts.m[g];
         ell_tiles[mt] = ts.ell[g];
-        tile_pv(c + (size_t)g * BN, emit, ne, V, row0, row_stride, is_bf16, acc);
+        tile_pv(c + (size_t)g * BN, emit, ne, V, row0, row_stride, SO_D, is_bf16, acc);
       }
       if (counts_o) {
         int16_t* dst = counts_o + (((size_t)b * H + h) * T_c + t) * BN;
@@ -476,38 +477,45 @@ int so_flash_decode(const uint16_t* Q, const uint16_t* K, const uint16_t* V, int
 /* Pass-1 of the general ("WMMA") path, prop/santa_cuda_kernel.cu:87-267:
  * q' = TK(f32(q) * scale) (:121-140).  The reference's scores come from a
  * 16x16x16 MMA whose internal association is unspecified; this build fixes
- * it to the vec path's (4-element fma chains per virtual lane and the
- * 32-lane tree, A.2) so that the GPU kernel and this restatement agree bit
+ * it: for D = 128 to the vec path's (4-element fma chains per virtual lane
+ * and the 32-lane tree, A.2), for any other D (a multiple of 16) to one fma
+ * chain over d ascending -- the GPU kernels and this restatement agree bit
  * for bit.  ell: per 16-row slab a sequential sum (:229-246), then a
  * sequential sum over slabs (:257-259). */
 static void tile_stats_general(const uint16_t* Qh /*[GH][D] raw*/, const uint16_t* K, size_t row0_off,
-                               size_t row_stride, int len, int BN, int GH, int is_bf16, float q_scale,
+                               size_t row_stride, int len, int BN, int GH, int D, int is_bf16, float q_scale,
                                tile_stats_t* ts, float* scores) {
   ts->len = len;
-  float qr[SO_MAX_GH * SO_D];
+  float qr[SO_MAX_GH * SO_MAX_D];
   for (int g = 0; g < GH; ++g)
-    for (int d = 0; d < SO_D; ++d) {
-      const float qv = ld16(Qh, (size_t)g * SO_D + d, is_bf16) * q_scale;
+    for (int d = 0; d < D; ++d) {
+      const float qv = ld16(Qh, (size_t)g * D + d, is_bf16) * q_scale;
       const uint16_t qb = st16(qv, is_bf16);
-      qr[g * SO_D + d] = ld16(&qb, 0, is_bf16);
+      qr[g * D + d] = ld16(&qb, 0, is_bf16);
     }
   for (int g = 0; g < GH; ++g) ts->m[g] = -INFINITY;
   for (int r = 0; r < len; ++r) {
     const uint16_t* krow = K + row0_off + (size_t)r * row_stride;
-    float kf[SO_D];
-    for (int d = 0; d < SO_D; ++d) kf[d] = ld16(krow, (size_t)d, is_bf16);
+    float kf[SO_MAX_D];
+    for (int d = 0; d < D; ++d) kf[d] = ld16(krow, (size_t)d, is_bf16);
     for (int g = 0; g < GH; ++g) {
-      const float* q = qr + (size_t)g * SO_D;
-      float lanes[SO_LANES];
-      for (int l = 0; l < SO_LANES; ++l) {
-        float sl = 0.0f;
-        sl = fmaf(q[4 * l + 0], kf[4 * l + 0], sl);
-        sl = fmaf(q[4 * l + 1], kf[4 * l + 1], sl);
-        sl = fmaf(q[4 * l + 2], kf[4 * l + 2], sl);
-        sl = fmaf(q[4 * l + 3], kf[4 * l + 3], sl);
-        lanes[l] = sl;
+      const float* q = qr + (size_t)g * D;
+      float sf;
+      if (D == SO_D) {
+        float lanes[SO_LANES];
+        for (int l = 0; l < SO_LANES; ++l) {
+          float sl = 0.0f;
+          sl = fmaf(q[4 * l + 0], kf[4 * l + 0], sl);
+          sl = fmaf(q[4 * l + 1], kf[4 * l + 1], sl);
+          sl = fmaf(q[4 * l + 2], kf[4 * l + 2], sl);
+          sl = fmaf(q[4 * l + 3], kf[4 * l + 3], sl);
+          lanes[l] = sl;
+        }
+        sf = lane_tree_down(lanes);
+      } else {
+        sf = 0.0f;
+        for (int d = 0; d < D; ++d) sf = fmaf(q[d], kf[d], sf);
       }
-      const float sf = lane_tree_down(lanes);
       scores[r * GH + g] = sf;
       ts->m[g] = fmaxf(ts->m[g], sf);
     }
@@ -623,21 +631,23 @@ void so_prop_budgets(const float* m_tiles, const float* ell_tiles, int T_c, int 
  * pass1_mode: 0 = vec path (GH=4, D=128, BN=256),
  *             1 = general path (q rounded to the storage dtype after scaling,
  *                 per-slab ell; see tile_stats_general).
- * Layouts: q [H,128]; K,V [L,KVH,128]. Optional outputs may be NULL:
+ * D: a multiple of 16 up to 256; BN: a multiple of 16 up to 512; GH <= 16.
+ * Layouts: q [H,D]; K,V [L,KVH,D]. Optional outputs may be NULL:
  *   m_tiles, ell_tiles, invdelta, a0 [H,T_c]; S_tiles [H,T_c] int32;
  *   u_stash [L,H] 16-bit; counts [H,T_c*BN] int16; rowmask [KVH,L]. */
-int so_prop_decode(const uint16_t* Q, const uint16_t* K, const uint16_t* V, int is_bf16, int H, int KVH, int L,
-                   int BN, int S, uint64_t seed, int pass1_mode, float* out_f32, uint16_t* out16,
-                   float* m_star, float* m_tiles_o, float* ell_tiles_o, int* S_tiles_o, float* invdelta_o,
-                   float* a0_o, uint16_t* u_stash_o, int16_t* counts_o, int* rowmask) {
+int so_prop_decode_d(const uint16_t* Q, const uint16_t* K, const uint16_t* V, int is_bf16, int H, int KVH, int D,
+                     int L, int BN, int S, uint64_t seed, int pass1_mode, float* out_f32, uint16_t* out16,
+                     float* m_star, float* m_tiles_o, float* ell_tiles_o, int* S_tiles_o, float* invdelta_o,
+                     float* a0_o, uint16_t* u_stash_o, int16_t* counts_o, int* rowmask) {
   if (KVH <= 0 || H % KVH != 0) return -1;
   const int GH = H / KVH;
   if (GH > SO_MAX_GH || BN > SO_MAX_BN || BN <= 0 || (BN % 16) != 0) return -2;
-  if (pass1_mode == 0 && !(GH == 4 && BN == 256)) return -5;
+  if (D <= 0 || D > SO_MAX_D || (D % 16) != 0) return -6;
+  if (pass1_mode == 0 && !(GH == 4 && BN == 256 && D == SO_D)) return -5;
   const int T_c = (L + BN - 1) / BN;
   const size_t TT = (size_t)(T_c > 0 ? T_c : 1);
-  const float q_scale = so_q_scale(SO_D);
-  const size_t row_stride = (size_t)KVH * SO_D;
+  const float q_scale = so_q_scale(D);
+  const size_t row_stride = (size_t)KVH * D;
 
   float* m_tiles = (float*)calloc((size_t)H * TT, sizeof(float));
   float* ell_tiles = (float*)calloc((size_t)H * TT, sizeof(float));
@@ -645,24 +655,25 @@ int so_prop_decode(const uint16_t* Q, const uint16_t* K, const uint16_t* V, int 
   int* S_tiles = (int*)calloc((size_t)H * TT, sizeof(int));
   float* invdelta = (float*)calloc((size_t)H * TT, sizeof(float));
   float* a0 = (float*)calloc((size_t)H * TT, sizeof(float));
-  float* out_acc = (float*)calloc((size_t)H * SO_D, sizeof(float));
+  float* out_acc = (float*)calloc((size_t)H * D, sizeof(float));
 
   /* pass 1 */
   for (int kv = 0; kv < KVH; ++kv) {
     const int h0 = kv * GH;
     float qf[SO_MAX_GH * SO_D];
-    for (int g = 0; g < GH; ++g)
-      for (int d = 0; d < SO_D; ++d) qf[g * SO_D + d] = ld16(Q, (size_t)(h0 + g) * SO_D + d, is_bf16) * q_scale;
+    if (pass1_mode == 0)
+      for (int g = 0; g < GH; ++g)
+        for (int d = 0; d < SO_D; ++d) qf[g * SO_D + d] = ld16(Q, (size_t)(h0 + g) * SO_D + d, is_bf16) * q_scale;
     for (int t = 0; t < T_c; ++t) {
       const int n0 = t * BN;
       const int len = (n0 + BN < L ? n0 + BN : L) - n0;
       tile_stats_t ts;
       float scores[SO_MAX_BN * SO_MAX_GH];
-      const size_t row0 = (size_t)n0 * row_stride + (size_t)kv * SO_D;
+      const size_t row0 = (size_t)n0 * row_stride + (size_t)kv * D;
       if (pass1_mode == 0)
         tile_stats_vec(qf, K, row0, row_stride, len, GH, 256, is_bf16, &ts, scores);
       else
-        tile_stats_general(Q + (size_t)h0 * SO_D, K, row0, row_stride, len, BN, GH, is_bf16, q_scale, &ts, scores);
+        tile_stats_general(Q + (size_t)h0 * D, K, row0, row_stride, len, BN, GH, D, is_bf16, q_scale, &ts, scores);
       for (int g = 0; g < GH; ++g) {
         m_tiles[(size_t)(h0 + g) * T_c + t] = ts.m[g];
         ell_tiles[(size_t)(h0 + g) * T_c + t] = ts.ell[g];
@@ -701,16 +712,16 @@ int so_prop_decode(const uint16_t* Q, const uint16_t* K, const uint16_t* V, int 
           for (int r = 0; r < BN; ++r) dst[r] = (r < len) ? c[(size_t)g * BN + r] : 0;
         }
         if (ne == 0) continue;
-        float acc[SO_D];
-        tile_pv(c + (size_t)g * BN, emit, ne, V, (size_t)n0 * row_stride + (size_t)kv * SO_D, row_stride, is_bf16,
+        float acc[SO_MAX_D];
+        tile_pv(c + (size_t)g * BN, emit, ne, V, (size_t)n0 * row_stride + (size_t)kv * D, row_stride, D, is_bf16,
                 acc);
-        for (int d = 0; d < SO_D; ++d) out_acc[(size_t)h * SO_D + d] += acc[d];
+        for (int d = 0; d < D; ++d) out_acc[(size_t)h * D + d] += acc[d];
       }
     }
   }
   /* cast + scale: prop/santa_cuda.cpp:333, prop/santa_cuda_kernel.cu:976-985 */
   const float scale_out = (S > 0) ? (1.0f / (float)S) : 0.0f;
-  for (int i = 0; i < H * SO_D; ++i) {
+  for (int i = 0; i < H * D; ++i) {
     const float y = out_acc[i] * scale_out;
     if (out_f32) out_f32[i] = y;
     if (out16) out16[i] = st16(y, is_bf16);
@@ -729,6 +740,14 @@ int so_prop_decode(const uint16_t* Q, const uint16_t* K, const uint16_t* V, int 
   free(a0);
   free(out_acc);
   return 0;
+}
+
+int so_prop_decode(const uint16_t* Q, const uint16_t* K, const uint16_t* V, int is_bf16, int H, int KVH, int L,
+                   int BN, int S, uint64_t seed, int pass1_mode, float* out_f32, uint16_t* out16,
+                   float* m_star, float* m_tiles_o, float* ell_tiles_o, int* S_tiles_o, float* invdelta_o,
+                   float* a0_o, uint16_t* u_stash_o, int16_t* counts_o, int* rowmask) {
+  return so_prop_decode_d(Q, K, V, is_bf16, H, KVH, SO_D, L, BN, S, seed, pass1_mode, out_f32, out16, m_star,
+                          m_tiles_o, ell_tiles_o, S_tiles_o, invdelta_o, a0_o, u_stash_o, counts_o, rowmask);
 }
 
 /* Element-wise helpers exported for the known-answer tests. */

@@ -34,7 +34,7 @@ ROCM = os.environ.get("ROCM_PATH", "/opt/rocm")
 HIPCC = os.path.join(ROCM, "bin", "hipcc")
 ARCH = "gfx950"
 
-HIP_SOURCES = ["santa_flash.hip", "santa_prop.hip", "santa_runtime.hip"]
+HIP_SOURCES = ["santa_flash.hip", "santa_prop.hip", "santa_prop_gen.hip", "santa_runtime.hip"]
 CXX_SOURCES = ["santa_common.cpp"]
 EXTENSIONS = {"santa_flash_batch_cuda": "ext_flash.cpp", "santa_prop_batch_cuda": "ext_prop.cpp"}
 

@@ -78,4 +78,32 @@ hipError_t launch_mfma_check(const float* a, const float* b, const float* c, flo
 void plan_chunks(int B, int KVH, int T_c, int* cs, int* cpg);
 }  // namespace flash
 
+namespace propgen {
+// santa_prop's shapes outside the tuned kernels (santa_prop_gen.hip): any
+// GH <= 16, D a multiple of 16 up to 256, block_n a multiple of 16 up to 512.
+// generic_shape: the shape is not one the tuned kernels take (D = 128, GH 4
+// or 8, block_n 32 / 64 / 256); shape_supported: the generic kernels take it.
+bool generic_shape(int GH, int D, int block_n);
+bool shape_supported(int GH, int D, int block_n);
+// Pass 1 (general numerics): m, ell [B, H, T_c] and the stash [B, L_storage,
+// H]; ragged with seq_lens (L the longest) over total_tiles tiles.
+hipError_t launch_pass1(const void* q, const void* K, int dtype, int B, int H, int KVH, int D, int L, int L_storage,
+                        int BN, float* m_tiles, float* ell_tiles, uint16_t* u_stash, const int* seq_lens,
+                        long long total_tiles, PageTable pt, hipStream_t stream);
+// The budgets for any tile count (one workgroup per (b, h), BH of them).
+hipError_t launch_budgets_big(const float* m_tiles, const float* ell_tiles, int BH, int H, int T_c, int S,
+                              uint64_t seed, float* m_star, int* S_tiles, float* invdelta, float* a0,
+                              const int* seq_lens, const int* seq_S, int BN, hipStream_t stream);
+// Pass 2 over the [B, L_storage, H] stash into per-chunk partials
+// [chunks, GH, D] (the chunk grid of flash::plan_chunks / plan_ragged), and
+// the finalize that sums them.
+hipError_t launch_pass2(const void* V, const uint16_t* u_stash, int dtype, int B, int H, int KVH, int D, int L,
+                        int L_storage, int BN, int T_c, int cs, int cpg, int n_wg, const float* invdelta,
+                        const float* a0, int16_t* counts, float* part, int* part_emit, int want_emit,
+                        const int* seq_lens, PageTable pt, hipStream_t stream);
+hipError_t launch_finalize(const float* part, const int* part_emit, int dtype, int B, int H, int KVH, int D, int cpg,
+                           float scale_out, void* out, int* vrows, const int* seq_lens, const int* seq_S, int BN,
+                           int cs, int max_rows, int n_wg, hipStream_t stream);
+}  // namespace propgen
+
 }  // namespace santa

@@ -672,7 +672,7 @@ struct PropWs {
   size_t m, ell, st, inv, a0, stash, part, emit, total;
   int cs, cpg, n_wg;
 };
-static PropWs prop_ws_layout(int B, int H, int KVH, int L_storage, int T_c, long long total_tiles = -1) {
+static PropWs prop_ws_layout(int B, int H, int KVH, int D, int L_storage, int T_c, long long total_tiles = -1) {
   PropWs w{};
   size_t chunks;
   if (total_tiles >= 0) {
@@ -697,8 +697,8 @@ static PropWs prop_ws_layout(int B, int H, int KVH, int L_storage, int T_c, long
   off = align_up(off + bht * sizeof(float));
   w.stash = off;  // [B, L_storage, H] or head-major [B, H, stash_ld(L_storage)]
   off = align_up(off + static_cast<size_t>(B) * stash_ld(L_storage) * H * sizeof(uint16_t));
-  w.part = off;
-  off = align_up(off + chunks * (H / KVH) * kD * sizeof(float));
+  w.part = off;  // [chunks, GH, D]
+  off = align_up(off + chunks * (H / KVH) * static_cast<size_t>(D) * sizeof(float));
   w.emit = off;
   off = align_up(off + chunks * sizeof(int));
   w.total = off;
@@ -719,25 +719,29 @@ static int pass1_mode(const char* env) {
   return 0;
 }
 
+// D = 128 with GH 4 or 8 runs the tuned kernels at block_n 32 / 64 / 256;
+// every other shape with D a multiple of 16 up to 256, GH up to 16 and
+// block_n a multiple of 16 up to 512 runs the generic ones
+// (santa_prop_gen.hip).
 static int check_common(int dtype, int H, int KVH, int D) {
   if (dtype != SANTA_BF16 && dtype != SANTA_F16) return set_error(SANTA_ERR_INVALID, "q_h must be bf16 or f16");
   if (H <= 0 || KVH <= 0) return set_error(SANTA_ERR_INVALID, "empty head dimension");
   if (H % KVH != 0)
     return set_error(SANTA_ERR_INVALID, "H must be divisible by KVH (expected KVH == K_g.size(1) for NHD)");
-  if (D != kD) return set_error(SANTA_ERR_UNSUPPORTED, "This build supports only D=128. Got D=%d", D);
+  if (D < 16 || D > 256 || D % 16 != 0)
+    return set_error(SANTA_ERR_UNSUPPORTED, "This build supports D a multiple of 16 up to 256 for santa_prop. Got D=%d",
+                     D);
   const int GH = H / KVH;
-  if (GH != 4 && GH != 8)
-    return set_error(SANTA_ERR_UNSUPPORTED, "This build supports only GH=4 or GH=8 (H/KVH). Got GH=%d (H=%d KVH=%d)",
+  if (GH > 16)
+    return set_error(SANTA_ERR_UNSUPPORTED, "This build supports GH (H/KVH) up to 16 for santa_prop. Got GH=%d (H=%d KVH=%d)",
                      GH, H, KVH);
   return SANTA_OK;
 }
 
-static int check_bn(int block_n, int T_c) {
-  if (!(block_n == 32 || block_n == 64 || block_n == 256))
-    return set_error(SANTA_ERR_UNSUPPORTED, "This build supports block_n in {32,64,256} for santa_prop. Got block_n=%d",
-                     block_n);
-  if (T_c > kMaxTiles)
-    return set_error(SANTA_ERR_UNSUPPORTED, "too many tiles per sequence: T_c=%d (max %d)", T_c, kMaxTiles);
+static int check_bn(int block_n, int GH, int D) {
+  if (!propgen::shape_supported(GH, D, block_n))
+    return set_error(SANTA_ERR_UNSUPPORTED,
+                     "This build supports block_n a multiple of 16 up to 512 for santa_prop. Got block_n=%d", block_n);
   return SANTA_OK;
 }
 
@@ -774,14 +778,17 @@ extern "C" int santa_prop_pass1(const void* q, const void* K, int dtype, int H, 
   int st = prop::check_common(dtype, H, KVH, D);
   if (st != SANTA_OK) return st;
   if (L <= 0) return set_error(SANTA_ERR_INVALID, "empty KV cache: L=%d", L);
-  const int T_c = (L + block_n - 1) / block_n;
-  if ((st = prop::check_bn(block_n, T_c)) != SANTA_OK) return st;
-  if (pass1_path == 0 && !(H / KVH == 4 && block_n == 256))
+  if ((st = prop::check_bn(block_n, H / KVH, D)) != SANTA_OK) return st;
+  if (pass1_path == 0 && !(H / KVH == 4 && D == 128 && block_n == 256))
     return set_error(SANTA_ERR_INVALID, "SANTA_PASS1=vec requires GH=4, D=128, block_n=256. Got GH=%d D=%d block_n=%d",
                      H / KVH, D, block_n);
   if (!q || !K || !m_tiles || !ell_tiles || !u_stash) return set_error(SANTA_ERR_INVALID, "null pointer argument");
-  const hipError_t e = flash::launch_prop_pass1(q, K, dtype, 1, H, KVH, L, L, block_n, pass1_path, m_tiles, ell_tiles,
-                                                static_cast<uint16_t*>(u_stash), nullptr, 0, 0, 0, stream);
+  const hipError_t e =
+      propgen::generic_shape(H / KVH, D, block_n)
+          ? propgen::launch_pass1(q, K, dtype, 1, H, KVH, D, L, L, block_n, m_tiles, ell_tiles,
+                                  static_cast<uint16_t*>(u_stash), nullptr, -1, PageTable{nullptr, 0, 3, 1}, stream)
+          : flash::launch_prop_pass1(q, K, dtype, 1, H, KVH, L, L, block_n, pass1_path, m_tiles, ell_tiles,
+                                     static_cast<uint16_t*>(u_stash), nullptr, 0, 0, 0, stream);
   if (e != hipSuccess) return set_error(SANTA_ERR_HIP, "pass-1 launch failed: %s", hipGetErrorString(e));
   return clear_error();
 }
@@ -790,6 +797,13 @@ static int prop_budgets_launch(const float* m_tiles, const float* ell_tiles, int
                                uint64_t seed, float* m_star, int* S_tiles, float* invdelta, float* a0,
                                hipStream_t stream, const int* seq_lens = nullptr, const int* seq_S = nullptr,
                                int block_n = 0) {
+  if (T_c > prop::kMaxTiles) {
+    // more tiles than the register network holds: the network in memory
+    const hipError_t e = propgen::launch_budgets_big(m_tiles, ell_tiles, BH, H, T_c, S, seed, m_star, S_tiles,
+                                                     invdelta, a0, seq_lens, seq_S, block_n, stream);
+    if (e != hipSuccess) return set_error(SANTA_ERR_HIP, "budget launch failed: %s", hipGetErrorString(e));
+    return SANTA_OK;
+  }
   // waves per (b, h) and registers per thread for every tile of the longest
   // sequence (T_c <= kMaxTiles): two registers a thread, up to 16 waves
   int N = 1;
@@ -805,8 +819,7 @@ static int prop_budgets_launch(const float* m_tiles, const float* ell_tiles, int
   else if (NW == 4 && R == 2) SANTA_BUDGETS(4, 2);
   else if (NW == 8 && R == 2) SANTA_BUDGETS(8, 2);
   else if (NW == 16 && R == 2) SANTA_BUDGETS(16, 2);
-  else if (NW == 16 && R == 4) SANTA_BUDGETS(16, 4);
-  else return set_error(SANTA_ERR_UNSUPPORTED, "too many tiles per sequence: T_c=%d (max %d)", T_c, prop::kMaxTiles);
+  else SANTA_BUDGETS(16, 4);
 #undef SANTA_BUDGETS
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess) return set_error(SANTA_ERR_HIP, "budget launch failed: %s", hipGetErrorString(e));
@@ -817,8 +830,6 @@ extern "C" int santa_prop_tile_budgets(const float* m_tiles, const float* ell_ti
                                        uint64_t seed, float* m_star, int* S_tiles, float* invdelta, float* a0,
                                        hipStream_t stream) {
   if (H <= 0 || T_c <= 0) return set_error(SANTA_ERR_INVALID, "bad budget shape: H=%d T_c=%d", H, T_c);
-  if (T_c > prop::kMaxTiles)
-    return set_error(SANTA_ERR_UNSUPPORTED, "too many tiles per sequence: T_c=%d (max %d)", T_c, prop::kMaxTiles);
   if (!m_tiles || !ell_tiles || !S_tiles || !invdelta || !a0)
     return set_error(SANTA_ERR_INVALID, "null pointer argument");
   const int st = prop_budgets_launch(m_tiles, ell_tiles, H, H, T_c, S, seed, m_star, S_tiles, invdelta, a0, stream);
@@ -826,18 +837,28 @@ extern "C" int santa_prop_tile_budgets(const float* m_tiles, const float* ell_ti
   return clear_error();
 }
 
-static int prop_pass2_launch(const void* V, const uint16_t* u_stash, int dtype, int B, int H, int KVH, int L,
+static int prop_pass2_launch(const void* V, const uint16_t* u_stash, int dtype, int B, int H, int KVH, int D, int L,
                              int L_storage, int block_n, int T_c, int S, const float* invdelta, const float* a0,
                              int16_t* counts, void* out, int* vrows, const prop::PropWs& w, char* base,
                              hipStream_t stream, const int* seq_lens = nullptr, const int* seq_S = nullptr,
                              int stash_ld = 0, PageTable pt = PageTable{nullptr, 0, 3, 1}) {
-  const prop::Pass2Grid rg{seq_lens, w.n_wg, stash_ld, pt};
   float* part = reinterpret_cast<float*>(base + w.part);
   int* pe = reinterpret_cast<int*>(base + w.emit);
   const int GH = H / KVH;
-  const uint16_t* Vh = static_cast<const uint16_t*>(V);
-  hipError_t e;
   const int want_emit = vrows ? 1 : 0;
+  const float scale_out = (S > 0) ? (1.0f / static_cast<float>(S)) : 0.0f;
+  hipError_t e;
+  if (propgen::generic_shape(GH, D, block_n)) {
+    e = propgen::launch_pass2(V, u_stash, dtype, B, H, KVH, D, L, L_storage, block_n, T_c, w.cs, w.cpg, w.n_wg,
+                              invdelta, a0, counts, part, pe, want_emit, seq_lens, pt, stream);
+    if (e != hipSuccess) return set_error(SANTA_ERR_HIP, "pass-2 launch failed: %s", hipGetErrorString(e));
+    e = propgen::launch_finalize(part, pe, dtype, B, H, KVH, D, w.cpg, scale_out, out, vrows, seq_lens, seq_S,
+                                 block_n, w.cs, L, w.n_wg, stream);
+    if (e != hipSuccess) return set_error(SANTA_ERR_HIP, "finalize launch failed: %s", hipGetErrorString(e));
+    return SANTA_OK;
+  }
+  const prop::Pass2Grid rg{seq_lens, w.n_wg, stash_ld, pt};
+  const uint16_t* Vh = static_cast<const uint16_t*>(V);
   if (dtype == SANTA_BF16)
     e = (GH == 4) ? prop::launch_pass2_bn<true, 4>(block_n, Vh, u_stash, B, H, KVH, L, L_storage, T_c, w.cs, w.cpg,
                                                    invdelta, a0, counts, part, pe, want_emit, rg, stream)
@@ -849,7 +870,6 @@ static int prop_pass2_launch(const void* V, const uint16_t* u_stash, int dtype, 
                   : prop::launch_pass2_bn<false, 8>(block_n, Vh, u_stash, B, H, KVH, L, L_storage, T_c, w.cs, w.cpg,
                                                     invdelta, a0, counts, part, pe, want_emit, rg, stream);
   if (e != hipSuccess) return set_error(SANTA_ERR_HIP, "pass-2 launch failed: %s", hipGetErrorString(e));
-  const float scale_out = (S > 0) ? (1.0f / static_cast<float>(S)) : 0.0f;
   const unsigned grid = static_cast<unsigned>(B) * static_cast<unsigned>(H);
   uint16_t* o = static_cast<uint16_t*>(out);
   if (dtype == SANTA_BF16) {
@@ -873,9 +893,8 @@ static int prop_pass2_launch(const void* V, const uint16_t* u_stash, int dtype, 
 }
 
 extern "C" size_t santa_prop_workspace_size(int H, int KVH, int D, int L, int T_c) {
-  (void)D;
-  if (H <= 0 || KVH <= 0 || H % KVH != 0 || L <= 0 || T_c <= 0) return 0;
-  return prop::prop_ws_layout(1, H, KVH, L, T_c).total;
+  if (H <= 0 || KVH <= 0 || H % KVH != 0 || D <= 0 || L <= 0 || T_c <= 0) return 0;
+  return prop::prop_ws_layout(1, H, KVH, D, L, T_c).total;
 }
 
 extern "C" int santa_prop_pass2(const void* V, const void* u_stash, int dtype, int H, int KVH, int D, int L,
@@ -885,13 +904,13 @@ extern "C" int santa_prop_pass2(const void* V, const void* u_stash, int dtype, i
   if (st != SANTA_OK) return st;
   if (L <= 0) return set_error(SANTA_ERR_INVALID, "empty KV cache: L=%d", L);
   const int T_c = (L + block_n - 1) / block_n;
-  if ((st = prop::check_bn(block_n, T_c)) != SANTA_OK) return st;
+  if ((st = prop::check_bn(block_n, H / KVH, D)) != SANTA_OK) return st;
   if (!V || !u_stash || !invdelta || !a0 || !out) return set_error(SANTA_ERR_INVALID, "null pointer argument");
-  const prop::PropWs w = prop::prop_ws_layout(1, H, KVH, L, T_c);
+  const prop::PropWs w = prop::prop_ws_layout(1, H, KVH, D, L, T_c);
   if (!workspace || workspace_bytes < w.total)
     return set_error(SANTA_ERR_WORKSPACE, "workspace too small: need %zu bytes, got %zu", w.total, workspace_bytes);
-  st = prop_pass2_launch(V, static_cast<const uint16_t*>(u_stash), dtype, 1, H, KVH, L, L, block_n, T_c, S, invdelta,
-                         a0, counts, out, vrows, w, static_cast<char*>(workspace), stream);
+  st = prop_pass2_launch(V, static_cast<const uint16_t*>(u_stash), dtype, 1, H, KVH, D, L, L, block_n, T_c, S,
+                         invdelta, a0, counts, out, vrows, w, static_cast<char*>(workspace), stream);
   if (st != SANTA_OK) return st;
   return clear_error();
 }
@@ -903,12 +922,12 @@ extern "C" int santa_prop_decode(const void* q, const void* K, const void* V, in
   if (st != SANTA_OK) return st;
   if (L <= 0) return set_error(SANTA_ERR_INVALID, "empty KV cache: L=%d", L);
   const int T_c = (L + block_n - 1) / block_n;
-  if ((st = prop::check_bn(block_n, T_c)) != SANTA_OK) return st;
-  if (pass1_path == 0 && !(H / KVH == 4 && block_n == 256))
+  if ((st = prop::check_bn(block_n, H / KVH, D)) != SANTA_OK) return st;
+  if (pass1_path == 0 && !(H / KVH == 4 && D == 128 && block_n == 256))
     return set_error(SANTA_ERR_INVALID, "SANTA_PASS1=vec requires GH=4, D=128, block_n=256. Got GH=%d D=%d block_n=%d",
                      H / KVH, D, block_n);
   if (!q || !K || !V || !out) return set_error(SANTA_ERR_INVALID, "null pointer argument");
-  const prop::PropWs w = prop::prop_ws_layout(1, H, KVH, L, T_c);
+  const prop::PropWs w = prop::prop_ws_layout(1, H, KVH, D, L, T_c);
   if (!workspace || workspace_bytes < w.total)
     return set_error(SANTA_ERR_WORKSPACE, "workspace too small: need %zu bytes, got %zu", w.total, workspace_bytes);
   char* base = static_cast<char*>(workspace);
@@ -918,27 +937,30 @@ extern "C" int santa_prop_decode(const void* q, const void* K, const void* V, in
   float* inv = reinterpret_cast<float*>(base + w.inv);
   float* a0 = reinterpret_cast<float*>(base + w.a0);
   uint16_t* stash = reinterpret_cast<uint16_t*>(base + w.stash);
+  const bool gen = propgen::generic_shape(H / KVH, D, block_n);
   // the vec path keeps the stash head-major between its two passes, except
   // for a small pass, whose pass 1 runs four waves per tile with the [L, H]
   // stash
   const bool small = flash::small_prop_pass(static_cast<long long>(T_c) * KVH);
   const int sld = (pass1_path == 0 && !small) ? prop::stash_ld(L) : 0;
-  hipError_t e = flash::launch_prop_pass1(q, K, dtype, 1, H, KVH, L, L, block_n, pass1_path, m_tiles, ell_tiles,
-                                          stash, nullptr, 0, 0, sld, stream);
+  hipError_t e = gen ? propgen::launch_pass1(q, K, dtype, 1, H, KVH, D, L, L, block_n, m_tiles, ell_tiles, stash,
+                                             nullptr, -1, PageTable{nullptr, 0, 3, 1}, stream)
+                     : flash::launch_prop_pass1(q, K, dtype, 1, H, KVH, L, L, block_n, pass1_path, m_tiles, ell_tiles,
+                                                stash, nullptr, 0, 0, sld, stream);
   if (e != hipSuccess) return set_error(SANTA_ERR_HIP, "pass-1 launch failed: %s", hipGetErrorString(e));
   if ((st = prop_budgets_launch(m_tiles, ell_tiles, H, H, T_c, S, seed, m_star, S_tiles, inv, a0, stream)) != SANTA_OK)
     return st;
-  if ((st = prop_pass2_launch(V, stash, dtype, 1, H, KVH, L, L, block_n, T_c, S, inv, a0, nullptr, out, vrows, w, base,
-                              stream, nullptr, nullptr, sld)) != SANTA_OK)
+  if ((st = prop_pass2_launch(V, stash, dtype, 1, H, KVH, D, L, L, block_n, T_c, S, inv, a0, nullptr, out, vrows, w,
+                              base, stream, nullptr, nullptr, sld)) != SANTA_OK)
     return st;
   return clear_error();
 }
 
 extern "C" size_t santa_prop_batched_workspace_size(int B, int H, int KVH, int D, int L_storage, int max_tiles,
                                                     long long total_tiles) {
-  (void)D;
-  if (B <= 0 || H <= 0 || KVH <= 0 || H % KVH != 0 || L_storage <= 0 || max_tiles <= 0 || total_tiles < 0) return 0;
-  return prop::prop_ws_layout(B, H, KVH, L_storage, max_tiles, total_tiles).total;
+  if (B <= 0 || H <= 0 || KVH <= 0 || H % KVH != 0 || D <= 0 || L_storage <= 0 || max_tiles <= 0 || total_tiles < 0)
+    return 0;
+  return prop::prop_ws_layout(B, H, KVH, D, L_storage, max_tiles, total_tiles).total;
 }
 
 // The batched decode over a contiguous [B, L_storage, KVH, D] cache or, with
@@ -954,14 +976,14 @@ static int prop_decode_batched(const void* q, const void* K, const void* V, int 
   if (max_len <= 0 || max_len > L_storage)
     return set_error(SANTA_ERR_INVALID, "max_len must be in [1, L_storage]: max_len=%d L_storage=%d", max_len, L_storage);
   const int T_c = (max_len + block_n - 1) / block_n;
-  if ((st = prop::check_bn(block_n, T_c)) != SANTA_OK) return st;
+  if ((st = prop::check_bn(block_n, H / KVH, D)) != SANTA_OK) return st;
   if (total_tiles < 0 || total_tiles > static_cast<long long>(B) * T_c)
     return set_error(SANTA_ERR_INVALID, "total_tiles out of range");
-  if (pass1_path == 0 && !(H / KVH == 4 && block_n == 256))
+  if (pass1_path == 0 && !(H / KVH == 4 && D == 128 && block_n == 256))
     return set_error(SANTA_ERR_INVALID, "SANTA_PASS1=vec requires GH=4, D=128, block_n=256. Got GH=%d D=%d block_n=%d",
                      H / KVH, D, block_n);
   if (!q || !K || !V || !out || !seq_lens || !seq_S) return set_error(SANTA_ERR_INVALID, "null pointer argument");
-  const prop::PropWs w = prop::prop_ws_layout(B, H, KVH, L_storage, T_c, total_tiles);
+  const prop::PropWs w = prop::prop_ws_layout(B, H, KVH, D, L_storage, T_c, total_tiles);
   if (!workspace || workspace_bytes < w.total)
     return set_error(SANTA_ERR_WORKSPACE, "workspace too small: need %zu bytes, got %zu", w.total, workspace_bytes);
   char* base = static_cast<char*>(workspace);
@@ -971,16 +993,20 @@ static int prop_decode_batched(const void* q, const void* K, const void* V, int 
   float* inv = reinterpret_cast<float*>(base + w.inv);
   float* a0 = reinterpret_cast<float*>(base + w.a0);
   uint16_t* stash = reinterpret_cast<uint16_t*>(base + w.stash);
+  const bool gen = propgen::generic_shape(H / KVH, D, block_n);
   const bool small = !pt.table && flash::small_prop_pass(total_tiles * KVH);  // as in the scalar call
   const int sld = (pass1_path == 0 && !small) ? prop::stash_ld(L_storage) : 0;
-  hipError_t e = flash::launch_prop_pass1(q, K, dtype, B, H, KVH, max_len, L_storage, block_n, pass1_path, m_tiles,
-                                          ell_tiles, stash, seq_lens, w.cs, w.n_wg, sld, stream, pt, total_tiles);
+  hipError_t e = gen ? propgen::launch_pass1(q, K, dtype, B, H, KVH, D, max_len, L_storage, block_n, m_tiles,
+                                             ell_tiles, stash, seq_lens, total_tiles, pt, stream)
+                     : flash::launch_prop_pass1(q, K, dtype, B, H, KVH, max_len, L_storage, block_n, pass1_path,
+                                                m_tiles, ell_tiles, stash, seq_lens, w.cs, w.n_wg, sld, stream, pt,
+                                                total_tiles);
   if (e != hipSuccess) return set_error(SANTA_ERR_HIP, "pass-1 launch failed: %s", hipGetErrorString(e));
   if ((st = prop_budgets_launch(m_tiles, ell_tiles, B * H, H, T_c, 0, seed, m_star, S_tiles, inv, a0, stream, seq_lens,
                                 seq_S, block_n)) != SANTA_OK)
     return st;
-  if ((st = prop_pass2_launch(V, stash, dtype, B, H, KVH, max_len, L_storage, block_n, T_c, 0, inv, a0, nullptr, out,
-                              vrows, w, base, stream, seq_lens, seq_S, sld, pt)) != SANTA_OK)
+  if ((st = prop_pass2_launch(V, stash, dtype, B, H, KVH, D, max_len, L_storage, block_n, T_c, 0, inv, a0, nullptr,
+                              out, vrows, w, base, stream, seq_lens, seq_S, sld, pt)) != SANTA_OK)
     return st;
   return clear_error();
 }

@@ -1,0 +1,538 @@
+// santa_prop_gen.hip -- santa_prop on the shapes the tuned kernels of
+// santa_flash.hip / santa_prop.hip do not take: any query-group size GH up to
+// 16, head_dim D any multiple of 16 up to 256, block_n any multiple of 16 up
+// to 512 (the reference's general pass 1 takes D % 16 == 0 and
+// block_n % 16 == 0, prop/santa_cuda.cpp:212-259; its pass 2 launches
+// (128, GH) threads, prop/santa_cuda_kernel.cu:917-946), and more than 4096
+// tiles per head in the budgets (the reference sizes that kernel's shared
+// memory at T_c * 8 bytes, prop/santa_cuda_kernel.cu:904-915).
+//
+// Kernels (one decode step, as in santa_prop.hip):
+//  * pass1_kernel: one workgroup per (sequence, KV head, tile).  q' =
+//    TK(f32(q) * scale) (prop/santa_cuda_kernel.cu:121-140); scores in a
+//    fixed association for what the reference leaves to its 16x16x16 MMA:
+//    for D = 128 the vec path's (4-element fma chains per virtual lane, then
+//    the 32-lane shfl_down tree), otherwise one fma chain over d ascending;
+//    m_t, u = exp(s - m_t) and the 16-bit u stash [B, L_storage, H]; ell as
+//    the reference's WMMA kernel sums it: per 16-row slab in row order, then
+//    the slabs in order (:225-262).
+//  * budgets_big_kernel: the largest-remainder budgets of santa_prop.hip's
+//    budgets_kernel (same m*, Z association, bases, jitter and bitonic
+//    network, :577-726) with the network's keys in global memory (the
+//    head's invdelta and a0 rows until their final values), for any number
+//    of tiles.
+//  * pass2_kernel: per (sequence, KV head, chunk of tiles): each head's
+//    systematic counts from the stash (32-row chunks, the reference's
+//    Hillis-Steele scan with a sequential carry, :771-807), its sampled rows
+//    ascending, and their count-weighted V rows summed with fma (:843-857).
+//  * finalize_kernel: out = dtype(sum over chunks * (1/S)) and vrows.
+// These are plain, correct kernels for shapes outside the tuned paths; the
+// shapes of the benchmarks run the tuned kernels.
+#include "santa_device.h"
+#include "santa_amd.h"
+#include "santa_internal.h"
+
+#include <algorithm>
+#include <cfloat>
+
+namespace santa {
+namespace propgen {
+
+constexpr int kThreads = 256;
+constexpr int kMaxD = 256;
+constexpr int kMaxGH = 16;
+constexpr int kMaxBN = 512;
+constexpr int kRowChunk = 64;  // K rows staged in LDS at a time
+
+bool generic_shape(int GH, int D, int block_n) {
+  return !(D == 128 && (GH == 4 || GH == 8) && (block_n == 32 || block_n == 64 || block_n == 256));
+}
+
+bool shape_supported(int GH, int D, int block_n) {
+  return GH >= 1 && GH <= kMaxGH && D >= 16 && D <= kMaxD && D % 16 == 0 && block_n >= 16 &&
+         block_n <= kMaxBN && block_n % 16 == 0;
+}
+
+// Score of one (row, head) from the rounded q' (floats) and the 16-bit K row.
+template <bool BF16, bool VEC128>
+__device__ __forceinline__ float score(const float* __restrict__ q, const uint16_t* __restrict__ k, int D) {
+  if constexpr (VEC128) {
+    float c[32];
+#pragma unroll
+    for (int v = 0; v < 32; ++v) {
+      float s = fmaf(q[4 * v], h16_to_f32<BF16>(k[4 * v]), 0.0f);
+      s = fmaf(q[4 * v + 1], h16_to_f32<BF16>(k[4 * v + 1]), s);
+      s = fmaf(q[4 * v + 2], h16_to_f32<BF16>(k[4 * v + 2]), s);
+      c[v] = fmaf(q[4 * v + 3], h16_to_f32<BF16>(k[4 * v + 3]), s);
+    }
+#pragma unroll
+    for (int off = 16; off > 0; off >>= 1)
+#pragma unroll
+      for (int l = 0; l < off; ++l) c[l] = c[l] + c[l + off];
+    return c[0];
+  } else {
+    float s = 0.0f;
+    for (int d = 0; d < D; ++d) s = fmaf(q[d], h16_to_f32<BF16>(k[d]), s);
+    return s;
+  }
+}
+
+// Element offset of token n of sequence b, KV head kv (contiguous or paged).
+template <bool PAGED>
+__device__ __forceinline__ size_t row_offset(const PageTable& pt, int b, int n, int kv, int KVH, int D,
+                                             int L_storage) {
+  if constexpr (PAGED) {
+    const int page = page_of_row(pt, b, n, true);
+    return ((static_cast<size_t>(page) << pt.shift) + static_cast<size_t>(n & ((1 << pt.shift) - 1))) * KVH * D +
+           static_cast<size_t>(kv) * D;
+  } else {
+    return (static_cast<size_t>(b) * L_storage + n) * KVH * D + static_cast<size_t>(kv) * D;
+  }
+}
+
+// ------------------------------------------------------------------ pass 1
+template <bool BF16, bool VEC128, bool PAGED>
+__global__ __launch_bounds__(kThreads) void pass1_kernel(const uint16_t* __restrict__ Q,
+                                                         const uint16_t* __restrict__ K, int H, int KVH, int D,
+                                                         int BN, int L_valid, int L_storage, int T_c, float q_scale,
+                                                         float* __restrict__ m_tiles, float* __restrict__ ell_tiles,
+                                                         uint16_t* __restrict__ u_stash,
+                                                         const int* __restrict__ seq_lens, int B, PageTable pt) {
+  const int GH = H / KVH;
+  const GridPos gp = grid_pos(static_cast<int>(blockIdx.x), seq_lens, B, KVH, BN, L_valid, T_c, 1, T_c);
+  if (gp.b < 0) return;
+  const int b = gp.b, kv = gp.kv, t = gp.chunk;
+  const int n0 = t * BN;
+  const int len = min(BN, gp.len - n0);
+  const int h0 = kv * GH;
+  const int tid = static_cast<int>(threadIdx.x);
+
+  __shared__ float s_q[kMaxGH * kMaxD];
+  __shared__ uint16_t s_k[kRowChunk * kMaxD];
+  __shared__ float s_sc[kMaxBN * kMaxGH];
+  __shared__ int s_mk[kMaxGH * 16];
+  __shared__ float s_m[kMaxGH];
+  __shared__ float s_part[kMaxGH * (kMaxBN / 16)];
+
+  for (int i = tid; i < GH * D; i += kThreads) {
+    const int g = i / D, d = i - (i / D) * D;
+    const float qv = h16_to_f32<BF16>(Q[(static_cast<size_t>(b) * H + h0 + g) * D + d]) * q_scale;
+    s_q[i] = h16_to_f32<BF16>(f32_to_h16<BF16>(qv));
+  }
+  const int hw = D / 2;  // 4-byte words per row
+  for (int r0 = 0; r0 < len; r0 += kRowChunk) {
+    const int nr = min(kRowChunk, len - r0);
+    __syncthreads();  // q' written; the previous chunk's rows read
+    for (int i = tid; i < nr * hw; i += kThreads) {
+      const int r = i / hw, w = i - (i / hw) * hw;
+      const uint32_t* src =
+          reinterpret_cast<const uint32_t*>(K + row_offset<PAGED>(pt, b, n0 + r0 + r, kv, KVH, D, L_storage));
+      reinterpret_cast<uint32_t*>(s_k)[r * hw + w] = src[w];
+    }
+    __syncthreads();
+    for (int i = tid; i < nr * GH; i += kThreads) {
+      const int r = i / GH, g = i - (i / GH) * GH;
+      s_sc[(r0 + r) * GH + g] = score<BF16, VEC128>(s_q + g * D, s_k + r * D, D);
+    }
+  }
+  __syncthreads();
+  // tile max per head (order keys: exact in any order)
+  if (tid < GH * 16) {
+    const int g = tid / 16, p = tid % 16;
+    int k = -2147483647 - 1;
+    for (int r = p; r < len; r += 16) k = max(k, order_key(s_sc[r * GH + g]));
+    s_mk[g * 16 + p] = k;
+  }
+  __syncthreads();
+  if (tid < GH) {
+    int k = s_mk[tid * 16];
+    for (int p = 1; p < 16; ++p) k = max(k, s_mk[tid * 16 + p]);
+    s_m[tid] = from_order_key(k);
+  }
+  __syncthreads();
+  // u, the 16-bit stash and the slab partials of ell
+  const int nslab = BN / 16;
+  for (int i = tid; i < GH * nslab; i += kThreads) {
+    const int g = i / nslab, w = i - (i / nslab) * nslab;
+    const float mg = s_m[g];
+    float part = 0.0f;
+    for (int j = 0; j < 16; ++j) {
+      const int r = 16 * w + j;
+      if (r < len) {
+        const float u = santa_expf(s_sc[r * GH + g] - mg);
+        part += u;
+        u_stash[(static_cast<size_t>(b) * L_storage + n0 + r) * H + h0 + g] = f32_to_h16<BF16>(u);
+      }
+    }
+    s_part[g * nslab + w] = part;
+  }
+  __syncthreads();
+  if (tid < GH) {
+    float ell = 0.0f;
+    for (int w = 0; w < nslab; ++w) ell += s_part[tid * nslab + w];
+    const size_t mt = (static_cast<size_t>(b) * H + h0 + tid) * T_c + t;
+    m_tiles[mt] = s_m[tid];
+    ell_tiles[mt] = ell;
+  }
+}
+
+// ----------------------------------------------------------------- budgets
+// One workgroup per (sequence, head).  The network only reads and writes
+// positions below the tile count (the rest read as (-inf, -1)), so its
+// (key, index) pairs live in this head's rows of invdelta and a0 (as int
+// bits) until the last phase writes their final values.
+constexpr int kBudgetThreads = 1024;
+
+__global__ __launch_bounds__(kBudgetThreads) void budgets_big_kernel(
+    const float* __restrict__ m_tiles, const float* __restrict__ ell_tiles, int H, int T_c, int S, uint64_t seed,
+    float* __restrict__ m_star, int* __restrict__ S_tiles, float* __restrict__ invdelta, float* __restrict__ a0_tile,
+    const int* __restrict__ seq_lens, const int* __restrict__ seq_S, int BN) {
+  __shared__ float s_red[kBudgetThreads / 64];
+  __shared__ long long s_lred[kBudgetThreads / 64];
+  __shared__ float s_z[128];
+  const int bh = static_cast<int>(blockIdx.x);
+  const int h = bh % H;
+  const int tid = static_cast<int>(threadIdx.x);
+  const int lane = tid & 63, wv = tid >> 6;
+  const size_t off = static_cast<size_t>(bh) * T_c;
+  int T = T_c;
+  if (seq_lens) T = (ragged_len(seq_lens, bh / H, T_c * BN) + BN - 1) / BN;
+  if (seq_S) S = seq_S[bh / H];
+  const float* mt = m_tiles + off;
+  const float* lt = ell_tiles + off;
+  float* f = invdelta + off;
+  int* ix = reinterpret_cast<int*>(a0_tile + off);
+
+  // m* = max_t m_t (exact in any order), from -FLT_MAX as in :597
+  float ms = -FLT_MAX;
+  for (int t = tid; t < T; t += kBudgetThreads) ms = fmaxf(ms, mt[t]);
+  for (int s = 32; s > 0; s >>= 1) ms = fmaxf(ms, __shfl_xor(ms, s, 64));
+  if (lane == 0) s_red[wv] = ms;
+  __syncthreads();
+  ms = s_red[0];
+  for (int i = 1; i < kBudgetThreads / 64; ++i) ms = fmaxf(ms, s_red[i]);
+  if (tid == 0 && m_star) m_star[bh] = ms;
+  // W_t, then Z: 128 partials over tiles tau, tau + 128, ... ascending, then
+  // the pairwise tree red[i] += red[i + s], s = 64 .. 1
+  for (int t = tid; t < T; t += kBudgetThreads) f[t] = santa_expf(mt[t] - ms) * lt[t];
+  __syncthreads();
+  if (tid < 128) {
+    float z = 0.0f;
+    for (int t = tid; t < T; t += 128) z += f[t];
+    s_z[tid] = z;
+  }
+  __syncthreads();
+  for (int s = 64; s > 0; s >>= 1) {
+    if (tid < s) s_z[tid] = s_z[tid] + s_z[tid + s];
+    __syncthreads();
+  }
+  const float Z = s_z[0];
+  if (S <= 0 || !(Z > 0.0f)) {
+    for (int t = tid; t < T; t += kBudgetThreads) {
+      S_tiles[off + t] = 0;
+      invdelta[off + t] = 0.0f;
+      a0_tile[off + t] = u01(seed, h, t);
+    }
+    return;
+  }
+  // integer bases and jittered fractional parts (:662-678)
+  long long base = 0;
+  for (int t = tid; t < T; t += kBudgetThreads) {
+    const float q = static_cast<float>(S) * (f[t] / Z);
+    const float fq = floorf(q);
+    const int bt = (fq != fq) ? 0 : (fq >= 2147483648.0f ? 2147483647 : static_cast<int>(fq));
+    S_tiles[off + t] = bt;
+    base += bt;
+    f[t] = (q - static_cast<float>(bt)) + 1.0e-7f * u01(seed, h, t);
+    ix[t] = t;
+  }
+  for (int s = 32; s > 0; s >>= 1) base += __shfl_xor(base, s, 64);
+  if (lane == 0) s_lred[wv] = base;
+  __syncthreads();
+  base = 0;
+  for (int i = 0; i < kBudgetThreads / 64; ++i) base += s_lred[i];
+  long long rem = static_cast<long long>(S) - base;
+  if (rem < 0) rem = 0;
+  if (rem > T) rem = T;
+  // the bitonic network over N = next power of two >= T (:686-707): the pair
+  // (i, i ^ j) with i the lower position swaps when (a_i > a_j) == (i & k);
+  // positions >= T read as (-inf, -1) and are never written
+  int N = 1;
+  while (N < T) N <<= 1;
+  for (int k = 2; k <= N; k <<= 1) {
+    for (int j = k >> 1; j > 0; j >>= 1) {
+      for (int p = tid; p < N / 2; p += kBudgetThreads) {
+        const int i = (p / j) * 2 * j + (p % j);
+        const int ixj = i + j;
+        const bool up = (i & k) != 0;
+        float ai = (i < T) ? f[i] : -__builtin_inff();
+        float aj = (ixj < T) ? f[ixj] : -__builtin_inff();
+        int ii = (i < T) ? ix[i] : -1;
+        int ij = (ixj < T) ? ix[ixj] : -1;
+        if ((ai > aj) == up) {
+          const float tf = ai;
+          ai = aj;
+          aj = tf;
+          const int ti = ii;
+          ii = ij;
+          ij = ti;
+        }
+        if (i < T) {
+          f[i] = ai;
+          ix[i] = ii;
+        }
+        if (ixj < T) {
+          f[ixj] = aj;
+          ix[ixj] = ij;
+        }
+      }
+      __syncthreads();
+    }
+  }
+  // +1 to the top `rem` (distinct tiles, :710-716)
+  for (int r = tid; r < rem; r += kBudgetThreads) {
+    const int best = ix[r];
+    if (best >= 0) S_tiles[off + best] += 1;
+  }
+  __syncthreads();
+  __syncthreads();  // the pairs' last reads are done before they are overwritten
+  for (int t = tid; t < T; t += kBudgetThreads) {
+    const int s_t = S_tiles[off + t];
+    const float ell = lt[t];
+    invdelta[off + t] = (s_t > 0 && ell > 1e-20f) ? (static_cast<float>(s_t) / ell) : 0.0f;
+    a0_tile[off + t] = u01(seed, h, t);
+  }
+}
+
+// ------------------------------------------------------------------ pass 2
+constexpr int kMaxDimsPerLane = kMaxD / 64;
+constexpr int kMaxHeadsPerWave = kMaxGH / 4;
+
+template <bool BF16, bool PAGED>
+__global__ __launch_bounds__(kThreads) void pass2_kernel(const uint16_t* __restrict__ V,
+                                                         const uint16_t* __restrict__ u_stash, int H, int KVH, int D,
+                                                         int BN, int L, int L_storage, int T_c, int cs, int cpg,
+                                                         const float* __restrict__ invdelta,
+                                                         const float* __restrict__ a0_tile,
+                                                         int16_t* __restrict__ dbg_counts, float* __restrict__ part,
+                                                         int* __restrict__ part_emit, int want_emit,
+                                                         const int* __restrict__ seq_lens, int B, PageTable pt) {
+  const int GH = H / KVH;
+  const int wg = static_cast<int>(blockIdx.x);
+  const GridPos gp = grid_pos(wg, seq_lens, B, KVH, BN, L, T_c, cs, cpg);
+  const int b = gp.b < 0 ? 0 : gp.b;
+  const int kv = gp.kv;
+  const int h0 = kv * GH;
+  L = gp.len;
+  const int t_begin = gp.chunk * cs;
+  const int t_end = (gp.b < 0) ? t_begin : min(gp.n_tiles, t_begin + cs);
+  const int tid = static_cast<int>(threadIdx.x);
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+
+  __shared__ int s_lrow[4][kMaxBN];
+  __shared__ float s_lc[4][kMaxBN];
+  __shared__ int s_flag[kMaxBN];
+  __shared__ int s_nemit;
+
+  float acc[kMaxHeadsPerWave][kMaxDimsPerLane];
+#pragma unroll
+  for (int k = 0; k < kMaxHeadsPerWave; ++k)
+#pragma unroll
+    for (int j = 0; j < kMaxDimsPerLane; ++j) acc[k][j] = 0.0f;
+  int emit_total = 0;
+  const uint16_t* ub = u_stash + static_cast<size_t>(b) * L_storage * H;
+
+  for (int t = t_begin; t < t_end; ++t) {
+    const int n0 = t * BN;
+    const int len = min(BN, L - n0);
+    if (want_emit) {
+      for (int r = tid; r < BN; r += kThreads) s_flag[r] = 0;
+      __syncthreads();
+    }
+#pragma unroll
+    for (int k = 0; k < kMaxHeadsPerWave; ++k) {
+      const int g = wave + 4 * k;
+      if (g >= GH) break;
+      const int h = h0 + g;
+      const size_t ht = (static_cast<size_t>(b) * H + h) * T_c + t;
+      const float inv = invdelta[ht];
+      const float a0 = a0_tile[ht];
+      float carry = 0.0f;
+      int lc = 0;
+      for (int base = 0; base < len; base += 32) {
+        const int r = base + lane;
+        const bool in = lane < 32 && r < len;
+        const float x = (in && inv > 0.0f) ? h16_to_f32<BF16>(ub[static_cast<size_t>(n0 + r) * H + h]) * inv : 0.0f;
+        // Hillis-Steele inclusive scan over 32 lanes, then res - x
+        // (flash/santa_cuda_kernel.cu:60-69)
+        float res = x;
+#pragma unroll
+        for (int off = 1; off < 32; off <<= 1) {
+          const float o = __shfl_up(res, off, 32);
+          res = ((lane & 31) >= off) ? res + o : res;
+        }
+        const float pre = res - x;
+        const float pre_g = carry + pre;
+        const float cum_g = pre_g + x;
+        const int c = in ? count_from_floors(a0, pre_g, cum_g) : 0;
+        const int last = min(31, len - base - 1);
+        const float chunk_total = __shfl(pre + x, last, 64);
+        carry = carry + chunk_total;
+        if (dbg_counts && lane < 32 && r < BN) dbg_counts[ht * BN + r] = static_cast<int16_t>(c);
+        const uint64_t nz = __ballot(c != 0);
+        if (c != 0) {
+          const int pos = lc + __popcll(nz & ((1ull << lane) - 1ull));
+          s_lrow[wave][pos] = n0 + r;
+          s_lc[wave][pos] = static_cast<float>(c);
+          if (want_emit) s_flag[r] = 1;
+        }
+        lc += __popcll(nz);
+      }
+      if (dbg_counts)
+        for (int r = ((len + 31) / 32) * 32 + lane; r < BN; r += 64) dbg_counts[ht * BN + r] = 0;
+      __builtin_amdgcn_wave_barrier();
+      // count-weighted V rows, rows ascending, one fma per element
+      for (int i = 0; i < lc; ++i) {
+        const int row = __builtin_amdgcn_readfirstlane(s_lrow[wave][i]);
+        const float cf = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(s_lc[wave][i])));
+        const uint16_t* vr = V + row_offset<PAGED>(pt, b, row, kv, KVH, D, L_storage);
+#pragma unroll
+        for (int j = 0; j < kMaxDimsPerLane; ++j) {
+          const int d = lane + 64 * j;
+          if (d < D) acc[k][j] = fmaf(cf, h16_to_f32<BF16>(vr[d]), acc[k][j]);
+        }
+      }
+      __builtin_amdgcn_wave_barrier();
+    }
+    if (want_emit) {
+      __syncthreads();
+      if (wave == 0) {
+        int e = 0;
+        for (int r = lane; r < BN; r += 64) e += s_flag[r];
+        for (int s = 32; s > 0; s >>= 1) e += __shfl_xor(e, s, 64);
+        if (lane == 0) s_nemit = e;
+      }
+      __syncthreads();
+      emit_total += s_nemit;
+    }
+  }
+#pragma unroll
+  for (int k = 0; k < kMaxHeadsPerWave; ++k) {
+    const int g = wave + 4 * k;
+    if (g >= GH) break;
+#pragma unroll
+    for (int j = 0; j < kMaxDimsPerLane; ++j) {
+      const int d = lane + 64 * j;
+      if (d < D) part[(static_cast<size_t>(wg) * GH + g) * D + d] = acc[k][j];
+    }
+  }
+  if (tid == 0) part_emit[wg] = emit_total;
+}
+
+// ---------------------------------------------------------------- finalize
+template <bool BF16>
+__global__ __launch_bounds__(kMaxD) void finalize_kernel(const float* __restrict__ part,
+                                                         const int* __restrict__ part_emit, int H, int KVH, int D,
+                                                         int cpg, float scale_out, uint16_t* __restrict__ out,
+                                                         int* __restrict__ vrows, const int* __restrict__ seq_lens,
+                                                         const int* __restrict__ seq_S, int BN, int cs, int max_rows,
+                                                         int n_wg) {
+  const int GH = H / KVH;
+  const int bh = static_cast<int>(blockIdx.x);
+  const int b = bh / H, h = bh % H;
+  const int kv = h / GH, g = h % GH;
+  const int d = static_cast<int>(threadIdx.x);
+  // chunk c of (b, kv) was workgroup base_b + c * KVH + kv
+  int base = b * cpg * KVH;
+  int nch = cpg;
+  if (seq_lens) {
+    base = 0;
+    for (int bb = 0; bb < b; ++bb) base += KVH * (((ragged_len(seq_lens, bb, max_rows) + BN - 1) / BN + cs - 1) / cs);
+    nch = ((ragged_len(seq_lens, b, max_rows) + BN - 1) / BN + cs - 1) / cs;
+    nch = max(0, min(nch, (n_wg - base - kv + KVH - 1) / KVH));
+  }
+  if (seq_S) scale_out = (seq_S[b] > 0) ? (1.0f / static_cast<float>(seq_S[b])) : 0.0f;
+  float s = 0.0f;
+  int e = 0;
+  for (int c = 0; c < nch; ++c) {
+    const size_t slot = static_cast<size_t>(base) + static_cast<size_t>(c) * KVH + kv;
+    if (d < D) s += part[(slot * GH + g) * D + d];
+    if (vrows && g == 0 && d == 0) e += part_emit[slot];
+  }
+  if (d < D) out[static_cast<size_t>(bh) * D + d] = f32_to_h16<BF16>(s * scale_out);
+  if (vrows && g == 0 && d == 0) vrows[static_cast<size_t>(b) * KVH + kv] = e;
+}
+
+// ---------------------------------------------------------------- launchers
+hipError_t launch_pass1(const void* q, const void* K, int dtype, int B, int H, int KVH, int D, int L, int L_storage,
+                        int BN, float* m_tiles, float* ell_tiles, uint16_t* u_stash, const int* seq_lens,
+                        long long total_tiles, PageTable pt, hipStream_t stream) {
+  const int T_c = (L + BN - 1) / BN;
+  const long long grid = seq_lens ? total_tiles * KVH : static_cast<long long>(B) * KVH * T_c;
+  if (grid <= 0) return hipSuccess;
+  const float q_scale = 1.0f / sqrtf(static_cast<float>(D));
+  const uint16_t* Qh = static_cast<const uint16_t*>(q);
+  const uint16_t* Kh = static_cast<const uint16_t*>(K);
+#define SANTA_GP1(BF, V128, PG)                                                                                     \
+  hipLaunchKernelGGL((pass1_kernel<BF, V128, PG>), dim3(static_cast<unsigned>(grid)), dim3(kThreads), 0, stream, Qh, \
+                     Kh, H, KVH, D, BN, L, L_storage, T_c, q_scale, m_tiles, ell_tiles, u_stash, seq_lens, B, pt)
+  const bool bf = dtype == SANTA_BF16, v128 = D == 128, pg = pt.table != nullptr;
+  if (bf) {
+    if (v128) { if (pg) SANTA_GP1(true, true, true); else SANTA_GP1(true, true, false); }
+    else { if (pg) SANTA_GP1(true, false, true); else SANTA_GP1(true, false, false); }
+  } else {
+    if (v128) { if (pg) SANTA_GP1(false, true, true); else SANTA_GP1(false, true, false); }
+    else { if (pg) SANTA_GP1(false, false, true); else SANTA_GP1(false, false, false); }
+  }
+#undef SANTA_GP1
+  return hipGetLastError();
+}
+
+hipError_t launch_budgets_big(const float* m_tiles, const float* ell_tiles, int BH, int H, int T_c, int S,
+                              uint64_t seed, float* m_star, int* S_tiles, float* invdelta, float* a0,
+                              const int* seq_lens, const int* seq_S, int BN, hipStream_t stream) {
+  if (BH <= 0) return hipSuccess;
+  hipLaunchKernelGGL(budgets_big_kernel, dim3(static_cast<unsigned>(BH)), dim3(kBudgetThreads), 0, stream, m_tiles,
+                     ell_tiles, H, T_c, S, seed, m_star, S_tiles, invdelta, a0, seq_lens, seq_S, BN);
+  return hipGetLastError();
+}
+
+hipError_t launch_pass2(const void* V, const uint16_t* u_stash, int dtype, int B, int H, int KVH, int D, int L,
+                        int L_storage, int BN, int T_c, int cs, int cpg, int n_wg, const float* invdelta,
+                        const float* a0, int16_t* counts, float* part, int* part_emit, int want_emit,
+                        const int* seq_lens, PageTable pt, hipStream_t stream) {
+  const long long grid = seq_lens ? n_wg : static_cast<long long>(B) * KVH * cpg;
+  if (grid <= 0) return hipSuccess;
+  const uint16_t* Vh = static_cast<const uint16_t*>(V);
+#define SANTA_GP2(BF, PG)                                                                                          \
+  hipLaunchKernelGGL((pass2_kernel<BF, PG>), dim3(static_cast<unsigned>(grid)), dim3(kThreads), 0, stream, Vh,      \
+                     u_stash, H, KVH, D, BN, L, L_storage, T_c, cs, cpg, invdelta, a0, counts, part, part_emit,     \
+                     want_emit, seq_lens, B, pt)
+  if (dtype == SANTA_BF16) {
+    if (pt.table) SANTA_GP2(true, true); else SANTA_GP2(true, false);
+  } else {
+    if (pt.table) SANTA_GP2(false, true); else SANTA_GP2(false, false);
+  }
+#undef SANTA_GP2
+  return hipGetLastError();
+}
+
+hipError_t launch_finalize(const float* part, const int* part_emit, int dtype, int B, int H, int KVH, int D, int cpg,
+                           float scale_out, void* out, int* vrows, const int* seq_lens, const int* seq_S, int BN,
+                           int cs, int max_rows, int n_wg, hipStream_t stream) {
+  const unsigned grid = static_cast<unsigned>(B) * static_cast<unsigned>(H);
+  if (grid == 0) return hipSuccess;
+  const unsigned threads = static_cast<unsigned>((D + 63) / 64 * 64);
+  uint16_t* o = static_cast<uint16_t*>(out);
+  if (dtype == SANTA_BF16)
+    hipLaunchKernelGGL(finalize_kernel<true>, dim3(grid), dim3(threads), 0, stream, part, part_emit, H, KVH, D, cpg,
+                       scale_out, o, vrows, seq_lens, seq_S, BN, cs, max_rows, n_wg);
+  else
+    hipLaunchKernelGGL(finalize_kernel<false>, dim3(grid), dim3(threads), 0, stream, part, part_emit, H, KVH, D, cpg,
+                       scale_out, o, vrows, seq_lens, seq_S, BN, cs, max_rows, n_wg);
+  return hipGetLastError();
+}
+
+}  // namespace propgen
+}  // namespace santa

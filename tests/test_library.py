@@ -130,10 +130,22 @@ def test_compute_entry_points_validate_before_any_launch(lib):
     rc = lib.santa_flash_fused_tiles(null, null, null, 7, 1, 32, 8, 128, 100, 100, 32, 1, ctypes.c_uint64(1), null,
                                      null, null, null, null, null)
     assert rc == ERR_INVALID
-    # prop: block_n outside the build
-    rc = lib.santa_prop_decode(null, null, null, 0, 32, 8, 128, 1000, 128, 1, 8, ctypes.c_uint64(1), null, null, null,
+    # prop: block_n, D and GH outside the build (any multiple of 16 up to 512,
+    # a multiple of 16 up to 256, at most 16)
+    for bn in (100, 1024):
+        rc = lib.santa_prop_decode(null, null, null, 0, 32, 8, 128, 1000, bn, 1, 8, ctypes.c_uint64(1), null, null,
+                                   null, null, ctypes.c_size_t(0), null)
+        assert rc == ERR_UNSUPPORTED and b"block_n a multiple of 16" in lib.santa_last_error()
+    rc = lib.santa_prop_decode(null, null, null, 0, 32, 8, 40, 1000, 64, 1, 8, ctypes.c_uint64(1), null, null, null,
                                null, ctypes.c_size_t(0), null)
-    assert rc == ERR_UNSUPPORTED and b"block_n" in lib.santa_last_error()
+    assert rc == ERR_UNSUPPORTED and b"D a multiple of 16" in lib.santa_last_error()
+    rc = lib.santa_prop_decode(null, null, null, 0, 64, 2, 128, 1000, 64, 1, 8, ctypes.c_uint64(1), null, null, null,
+                               null, ctypes.c_size_t(0), null)
+    assert rc == ERR_UNSUPPORTED and b"GH=32" in lib.santa_last_error()
+    # prop: a generic shape passes validation and stops at the workspace
+    rc = lib.santa_prop_decode(null, null, null, 0, 12, 4, 80, 1000, 48, 1, 8, ctypes.c_uint64(1), null, null, null,
+                               null, ctypes.c_size_t(0), null)
+    assert rc == ERR_INVALID and b"null pointer" in lib.santa_last_error()
     # prop: vec path with GH 8
     rc = lib.santa_prop_pass1(null, null, 0, 64, 8, 128, 1000, 256, 0, null, null, null, null)
     assert rc == ERR_INVALID and b"SANTA_PASS1=vec" in lib.santa_last_error()

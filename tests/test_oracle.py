@@ -15,7 +15,7 @@ import pytest
 import torch
 
 import oracle
-from helpers import SEED, gen_qkv, tol_check
+from helpers import SEED, gen_qkv, h16_to_f32, tol_check
 
 F32_MAX_EXP = 88.72283935546875
 
@@ -431,4 +431,120 @@ def test_prop_output_given_counts_and_convergence():
     assert oracle.prop_decode(q, K, V, 200_000, seed=SEED, block_n=256, debug=True)["counts"].max() < 32767
     exact = _exact_attention(q[None], K[None], V[None])[0]
     ok, mabs, mrel = tol_check(big["out"], exact, max_abs=2e-2, mean_rel=5e-3)
+    assert ok, (mabs, mrel)
+
+
+# ---------------------------------------------------- prop: general shapes
+def _general_case(H, KVH, D, L, seed):
+    g = torch.Generator().manual_seed(seed)
+    q = torch.randn(H, D, generator=g).bfloat16()
+    K = torch.randn(L, KVH, D, generator=g).bfloat16()
+    V = torch.randn(L, KVH, D, generator=g).bfloat16()
+    return q, K, V
+
+
+@pytest.mark.parametrize("H,KVH,D,BN,L", [
+    (8, 8, 128, 48, 500),     # GH 1, the vec score association (D = 128)
+    (8, 4, 64, 16, 300),      # GH 2
+    (32, 2, 80, 512, 1100),   # GH 16, block_n 512
+    (6, 2, 256, 128, 600),    # GH 3, D 256
+    (32, 8, 48, 256, 800),    # GH 4, D 48
+])
+def test_prop_general_shapes_bruteforce(H, KVH, D, BN, L):
+    """The general pass 1 on shapes outside D = 128 / GH 4, 8 / block_n 32, 64,
+    256: tile max and mass against float64 scores of q rounded to bf16 after
+    scaling by 1/sqrt(D); the stash against exp(s - m_t) to bf16 rounding;
+    the counts sum per tile to the systematic sampler's total, sampled rows
+    are where the counts are, and the output is the float64 estimator given
+    the counts."""
+    q, K, V = _general_case(H, KVH, D, L, SEED + D + H)
+    GH = H // KVH
+    S = 3 * (L // 16)
+    p = oracle.prop_decode(q, K, V, S, seed=SEED, block_n=BN, pass1_mode=1, debug=True)
+    assert p["T_c"] == (L + BN - 1) // BN
+    scale = np.float32(1.0) / np.sqrt(np.float32(D))
+    qr = torch.from_numpy(q.float().numpy() * scale).to(torch.bfloat16).double().numpy()
+    s = np.einsum("hd,lhd->hl", qr, np.repeat(K.double().numpy(), GH, axis=1))
+    u16 = h16_to_f32(p["u_stash"]).astype(np.float64)  # [L, H]
+    for t in range(p["T_c"]):
+        st = s[:, t * BN:(t + 1) * BN]
+        assert np.allclose(p["m_tiles"][:, t], st.max(axis=1), rtol=1e-5, atol=1e-5)
+        e = np.exp(st - p["m_tiles"][:, t, None].astype(np.float64))
+        assert np.allclose(p["ell_tiles"][:, t], e.sum(axis=1), rtol=2e-5)
+        assert np.allclose(u16[t * BN:(t + 1) * BN].T, e, rtol=2 ** -8, atol=1e-6)
+    assert (p["S_tiles"].sum(axis=1) == S).all()
+    cnt = p["counts"].reshape(H, -1)[:, :L].astype(np.float64)
+    # per tile: sum of counts = floor(a0 + X) - floor(a0), X ~ S_t (float32 sums)
+    for t in range(p["T_c"]):
+        tot = cnt[:, t * BN:(t + 1) * BN].sum(axis=1)
+        assert (np.abs(tot - p["S_tiles"][:, t]) <= 1).all()
+    rows = (cnt.reshape(KVH, GH, L) > 0).any(axis=1)
+    assert np.array_equal(p["vrows"], rows.sum(axis=1))
+    y = np.stack([cnt[h] @ V.double().numpy()[:, h // GH] for h in range(H)]) / S
+    assert np.allclose(p["out"], y, rtol=1e-4, atol=2e-5)
+
+
+def test_prop_general_score_exact_on_integer_inputs():
+    """D = 48 with small-integer K and q' a power of two times small integers:
+    every fma of the chain is exact, so the tile max equals the exact integer
+    dot product scaled -- whatever the association (a dropped or repeated term
+    would not)."""
+    H, KVH, D, L = 4, 2, 48, 40
+    rng = np.random.default_rng(7)
+    qi = rng.integers(-3, 4, (H, D))
+    ki = rng.integers(-3, 4, (L, KVH, D))
+    # q' = bf16(q * 1/sqrt(48)); pick q so that q' is exactly qi / 8: q = qi/8 * sqrt(48)
+    scale = np.float32(1.0) / np.sqrt(np.float32(D))
+    qf = (qi / 8.0 / float(scale)).astype(np.float32)
+    q = torch.from_numpy(qf).bfloat16()
+    qr = torch.from_numpy(q.float().numpy() * scale).to(torch.bfloat16).float().numpy()
+    K = torch.from_numpy(ki.astype(np.float32)).bfloat16()
+    p = oracle.prop_decode(q, K, K, 10, seed=SEED, block_n=16, pass1_mode=1, debug=True)
+    # the exact dot products of the rounded q' (small dyadic numbers: exact in float32)
+    s = np.einsum("hd,lhd->hl", qr.astype(np.float64), np.repeat(ki.astype(np.float64), H // KVH, axis=1))
+    for t in range(p["T_c"]):
+        assert np.array_equal(p["m_tiles"][:, t].astype(np.float64), s[:, t * 16:(t + 1) * 16].max(axis=1))
+
+
+@pytest.mark.parametrize("T_c", [4100, 8192])
+def test_prop_budgets_beyond_4096_tiles(T_c):
+    """More tiles than the register network holds: the same invariants (every
+    tile floor(q_t) or floor(q_t) + 1, the budgets add up to S when T_c is a
+    power of two, the +1 on the largest jittered remainders) and, for one
+    budget, the brute-force model of the padded network."""
+    rng = np.random.default_rng(T_c)
+    m = rng.normal(0, 3, T_c).astype(np.float32)
+    ell = rng.uniform(1, 256, T_c).astype(np.float32)
+    W = np.exp(m.astype(np.float64) - m.max()) * ell
+    for S in (T_c // 3, 5 * T_c + 17):
+        res = oracle.prop_budgets(m, ell, S, SEED, h=5)
+        St = res["S_tiles"]
+        qt = S * W / W.sum()
+        assert ((St >= np.floor(qt - 1e-4)) & (St <= np.floor(qt + 1e-4) + 1)).all()
+        assert St.sum() <= S
+        if T_c & (T_c - 1) == 0:
+            assert St.sum() == S
+    S = T_c // 3
+    res = oracle.prop_budgets(m, ell, S, SEED, h=5)
+    fr32 = []
+    for t in range(T_c):
+        q32 = np.float32(S) * np.float32(W[t] / W.sum())
+        fr32.append(float(q32 - np.floor(q32)))
+    ix = _bitonic_model(fr32, T_c)
+    rem = S - int(np.floor(S * W / W.sum()).sum())
+    allowed = {i for i in ix[:max(0, min(rem + 1, T_c))] if i >= 0}
+    plus = set(np.nonzero(res["S_tiles"] > np.floor(S * W / W.sum() + 1e-4))[0].tolist())
+    assert plus <= allowed | set(np.nonzero(np.abs(S * W / W.sum() - np.round(S * W / W.sum())) < 1e-4)[0].tolist())
+
+
+def test_prop_general_shape_converges_to_exact_attention():
+    H, KVH, D, L = 8, 4, 64, 600
+    q, K, V = _general_case(H, KVH, D, L, SEED + 99)
+    big = oracle.prop_decode(q, K, V, 200_000, seed=SEED, block_n=48, pass1_mode=1)
+    qf = q.double().numpy() / math.sqrt(D)
+    s = np.einsum("hd,lhd->hl", qf, np.repeat(K.double().numpy(), H // KVH, axis=1))
+    w = np.exp(s - s.max(axis=1, keepdims=True))
+    w /= w.sum(axis=1, keepdims=True)
+    exact = np.einsum("hl,lhd->hd", w, np.repeat(V.double().numpy(), H // KVH, axis=1))
+    ok, mabs, mrel = tol_check(big["out"], exact, max_abs=2e-2, mean_rel=1e-2)
     assert ok, (mabs, mrel)

@@ -199,3 +199,42 @@ def test_cfg5_prop_leg_parity():
             np.testing.assert_array_equal(bits16(stash), exp["u_stash"], err_msg="u_stash")
             assert np.array_equal(cnt.numpy(), exp["counts"]), "counts"
             np.testing.assert_array_equal(vr_d.numpy(), exp["vrows"], err_msg="vrows (stages)")
+
+
+@pytest.mark.parametrize("H,KVH,D,lens,Ss,block_n,page_size", [
+    (16, 8, 64, [3000, 1700, 2500], [100, 40, 77], 48, 16),
+    (32, 2, 128, [900, 2048, 1333, 64], [30, 64, 0, 5], 32, 256),
+])
+def test_prop_general_batched_and_paged(H, KVH, D, lens, Ss, block_n, page_size, monkeypatch):
+    """The generic kernels in the batched, ragged call (one launch sequence over
+    the batch) and the paged one: every sequence's m* and vrows exact against
+    the oracle of the per-sequence call, the output within the bf16 tolerance,
+    and the paged call bit-identical to the contiguous one."""
+    import santa_prop_batch_cuda as m
+    from test_paged_gpu import make_pool
+
+    monkeypatch.delenv("SANTA_PASS1", raising=False)
+    B, L = len(lens), max(lens)
+    print(f"\n[case] prop general batched H={H} KVH={KVH} D={D} lens={lens} S={Ss} bn={block_n} page={page_size}",
+          flush=True)
+    g = torch.Generator().manual_seed(SEED + D)
+    q = torch.randn(B, H, D, generator=g).bfloat16()
+    K = torch.randn(B, L, KVH, D, generator=g).bfloat16()
+    V = torch.randn(B, L, KVH, D, generator=g).bfloat16()
+    Kp, Vp, table = make_pool(K, V, lens, page_size, SEED + 1)
+    dev = torch.device("cuda:0")
+    qd, Kd, Vd, Kpd, Vpd, td = (t.to(dev) for t in (q, K, V, Kp, Vp, table))
+    out, ms, vr = m.decode_systematic_batched(qd, Kd, Vd, Ss, seed=SEED, block_n=block_n, want_vrows=True,
+                                              valid_len=lens)
+    po, pm, pv = m.decode_systematic_paged(qd, Kpd, Vpd, td, lens, Ss, seed=SEED, block_n=block_n, want_vrows=True)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(bits16(po), bits16(out), err_msg="paged vs contiguous: out")
+    np.testing.assert_array_equal(pm.cpu().numpy().view(np.uint32), ms.cpu().numpy().view(np.uint32))
+    np.testing.assert_array_equal(pv.cpu().numpy(), vr.cpu().numpy())
+    for b, (Lb, Sb) in enumerate(zip(lens, Ss)):
+        exp = oracle.prop_decode(q[b], K[b, :Lb], V[b, :Lb], Sb, seed=SEED, block_n=block_n, debug=True)
+        np.testing.assert_array_equal(ms[b].cpu().numpy().view(np.uint32), exp["m_star"].view(np.uint32),
+                                      err_msg=f"m_star b={b}")
+        np.testing.assert_array_equal(vr[b].cpu().numpy(), exp["vrows"], err_msg=f"vrows b={b}")
+        ok, mabs, mrel = tol_check(h16_to_f32(bits16(out[b])), h16_to_f32(exp["out16"]))
+        assert ok, (f"b={b} vs oracle", mabs, mrel)

@@ -126,3 +126,52 @@ def test_prop_errors(monkeypatch):
     monkeypatch.delenv("SANTA_PASS1")
     with pytest.raises(TypeError):
         m.decode_systematic_scalar(qd, Kd, Vd, 8, valid_len=3)
+
+
+def _general_inputs(H, KVH, D, L, seed, dtype=torch.bfloat16):
+    g = torch.Generator().manual_seed(seed)
+    q = torch.randn(H, D, generator=g)
+    K = torch.randn(L, KVH, D, generator=g)
+    V = torch.randn(L, KVH, D, generator=g)
+    return q.to(dtype), K.to(dtype), V.to(dtype)
+
+
+@pytest.mark.parametrize(
+    "H,KVH,D,L,S,block_n",
+    [
+        (8, 8, 128, 3000, 200, 0),     # GH 1 (auto block_n 64)
+        (16, 8, 64, 5000, 300, 0),     # GH 2, D 64 (block_n 256)
+        (32, 2, 128, 2000, 150, 48),   # GH 16, block_n 48
+        (12, 4, 80, 1000, 90, 16),     # GH 3, D 80, block_n 16
+        (32, 8, 128, 4000, 250, 128),  # GH 4 at block_n 128
+        (16, 1, 256, 900, 64, 512),    # GH 16, D 256, block_n 512
+        (4, 4, 16, 700, 40, 32),       # GH 1, D 16
+        (32, 8, 48, 2500, 100, 0),     # GH 4, D 48
+    ],
+)
+def test_prop_general_shapes(H, KVH, D, L, S, block_n, monkeypatch):
+    """Shapes outside the tuned kernels (the reference's general path takes
+    any GH, D % 16 == 0 and block_n % 16 == 0, prop/santa_cuda.cpp:212-259):
+    tile max and mass, the stash, the budgets and every count bit-exact to the
+    oracle, m* and vrows exact, the output within the bf16 tolerance."""
+    _announce(f"prop general shape H={H} KVH={KVH} D={D} L={L} S={S} bn={block_n}")
+    q, K, V = _general_inputs(H, KVH, D, L, SEED + 3 * D + H)
+    exp = _check(q, K, V, S, SEED, block_n=block_n, monkeypatch=monkeypatch)
+    assert exp["pass1_mode"] == 1
+
+
+def test_prop_general_f16(monkeypatch):
+    _announce("prop general shape f16 H=16 KVH=8 D=96 L=1500 S=70 bn=32")
+    q, K, V = _general_inputs(16, 8, 96, 1500, SEED + 5, dtype=torch.float16)
+    _check(q, K, V, 70, SEED, block_n=32, is_bf16=False, monkeypatch=monkeypatch)
+
+
+@pytest.mark.parametrize("H,KVH,D,L,block_n", [(32, 8, 128, 140000, 32), (8, 4, 64, 70000, 16)])
+def test_prop_more_than_4096_tiles(H, KVH, D, L, block_n, monkeypatch):
+    """4375 tiles per head: beyond the register network's 4096, the budgets
+    run their network in memory (for the tuned GH 4 / D 128 passes at block_n
+    32 and for a generic shape alike); every stage bit-exact to the oracle."""
+    _announce(f"prop T_c > 4096 H={H} KVH={KVH} D={D} L={L} bn={block_n}")
+    q, K, V = _general_inputs(H, KVH, D, L, SEED + L)
+    exp = _check(q, K, V, L // 50, SEED, block_n=block_n, monkeypatch=monkeypatch)
+    assert exp["T_c"] == 4375
