@@ -766,8 +766,76 @@ __device__ __forceinline__ float wave_ell(const float (&u)[2][2]) {
   }
 }
 
-// P1: santa_prop pass 1 with the vec path's numerics (the flash tile
-// statistics): per tile and head m and ell into dbg_m / dbg_ell ([B, H, T_c])
+// ell of four heads with the general path's association: the reference's
+// WMMA pass 1 sums each head's u over a 16-row slab in row order, then the
+// slabs in order (prop/santa_cuda_kernel.cu:225-262).  In the wave layout a
+// slab is 8 consecutive lanes of one register pair, so the u values go
+// through LDS (two regions of this wave's sample-list area, which pass 1
+// leaves unused): head k's 256 values at fa_k[row], fa_k = (k < 2 ? fa01 :
+// fa23) + 256 (k & 1).  Then lane 16k + w sums slab w of head k in row
+// order, and lane k sums head k's 16 slab sums in slab order.  Rows past the
+// tile's end hold u = 0, which adds exactly.
+__device__ __forceinline__ void slab_ell4(const float (&u)[4][2][2], float* fa01, float* fa23, int lane,
+                                          float (&ell)[4]) {
+  const int jrow = lane >> 4, qq = lane & 15;
+#pragma unroll
+  for (int k = 0; k < 4; ++k)
+#pragma unroll
+    for (int hh = 0; hh < 2; ++hh)
+      *reinterpret_cast<float2*>((k < 2 ? fa01 : fa23) + 256 * (k & 1) + 128 * hh + 32 * jrow + 2 * qq) =
+          make_float2(u[k][hh][0], u[k][hh][1]);
+  __builtin_amdgcn_wave_barrier();
+  const int ks = lane >> 4;
+  const float4* src = reinterpret_cast<const float4*>((ks < 2 ? fa01 : fa23) + 256 * (ks & 1) + 16 * (lane & 15));
+  const float4 a = src[0], b = src[1], c = src[2], d = src[3];
+  float p = a.x;
+  p = p + a.y;
+  p = p + a.z;
+  p = p + a.w;
+  p = p + b.x;
+  p = p + b.y;
+  p = p + b.z;
+  p = p + b.w;
+  p = p + c.x;
+  p = p + c.y;
+  p = p + c.z;
+  p = p + c.w;
+  p = p + d.x;
+  p = p + d.y;
+  p = p + d.z;
+  p = p + d.w;
+  // every lane's reads have returned (p needs all of them), so the slab sums
+  // may overwrite the start of head 0's values
+  __builtin_amdgcn_wave_barrier();
+  fa01[lane] = p;
+  __builtin_amdgcn_wave_barrier();
+  const float4* s2 = reinterpret_cast<const float4*>(fa01 + 16 * (lane & 3));
+  const float4 e0 = s2[0], e1 = s2[1], e2 = s2[2], e3 = s2[3];
+  float e = e0.x;
+  e = e + e0.y;
+  e = e + e0.z;
+  e = e + e0.w;
+  e = e + e1.x;
+  e = e + e1.y;
+  e = e + e1.z;
+  e = e + e1.w;
+  e = e + e2.x;
+  e = e + e2.y;
+  e = e + e2.z;
+  e = e + e2.w;
+  e = e + e3.x;
+  e = e + e3.y;
+  e = e + e3.z;
+  e = e + e3.w;
+#pragma unroll
+  for (int k = 0; k < 4; ++k) ell[k] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(e), k));
+  __builtin_amdgcn_wave_barrier();
+}
+
+// P1: santa_prop pass 1 -- for GH 4 with the vec path's numerics (the flash
+// tile statistics), for GH 8 with the general path's (q rounded after
+// scaling, ell per 16-row slab): per tile and head m and ell into dbg_m /
+// dbg_ell ([B, H, T_c])
 // and the 16-bit u into u_stash ([B, L_storage, H]); no sampling, no partials.
 // ROWS: a workgroup of KVH waves (KVH <= 8), wave kv taking KV head kv over
 // every tile of the workgroup's chunk, so the KV heads of a token chunk are
@@ -826,7 +894,12 @@ __global__ __launch_bounds__(ROWS ? 512 : kThreads, ROWS ? 1 : 2) void wave_kern
   for (int hb = 0; hb < NHB; ++hb) {
     const uint16_t* qh = Q + (static_cast<size_t>(b) * H + h0 + 4 * hb + (lane & 3)) * kD + (lane >> 2);
 #pragma unroll
-    for (int m = 0; m < 8; ++m) qa[hb][m] = h16_to_f32<BF16>(qh[16 * m]) * q_scale;
+    for (int m = 0; m < 8; ++m) {
+      qa[hb][m] = h16_to_f32<BF16>(qh[16 * m]) * q_scale;
+      // pass 1 of GH 8 is santa_prop's general path: q rounded to the 16-bit
+      // type after scaling (prop/santa_cuda_kernel.cu:121-140)
+      if constexpr (P1 && GH == 8) qa[hb][m] = h16_to_f32<BF16>(f32_to_h16<BF16>(qa[hb][m]));
+    }
   }
 
   float runM[GH], runZ[GH], num0[GH], num1[GH];
@@ -1083,8 +1156,12 @@ __global__ __launch_bounds__(ROWS ? 512 : kThreads, ROWS ? 1 : 2) void wave_kern
             ub[k][hh][e] = round16_nonneg<BF16>(u[k][hh][e]);
           }
       float ell[4];
+      if constexpr (P1 && GH == 8) {
+        slab_ell4(u, reinterpret_cast<float*>(lrow), lcw, lane, ell);
+      } else {
 #pragma unroll
-      for (int k = 0; k < 4; ++k) ell[k] = wave_ell<GH>(u[k]);
+        for (int k = 0; k < 4; ++k) ell[k] = wave_ell<GH>(u[k]);
+      }
       if constexpr (P1) {
 #pragma unroll
         for (int k = 0; k < 4; ++k) {
@@ -1769,16 +1846,21 @@ hipError_t launch_prop_pass1(const void* q, const void* K, int dtype, int B, int
     chunk_plan(B, KVH, a.T_c, &a.cs, &a.cpg);
   }
   const int GH = H / KVH;
-  if (path == 0) {
-    // the vec path (GH 4, block_n 256) on the wave kernel; for KVH = 8 in its
-    // rows form, with a plan of its own (pass 1 writes no chunk partials, so
-    // it need not share pass 2's chunking)
+  if (prop_wave_pass1(path, GH, block_n)) {
+    // block_n 256 on the wave kernel -- GH 4 with the vec path's numerics,
+    // GH 8 with the general path's; for KVH = 8 in its rows form, with a
+    // plan of its own (pass 1 writes no chunk partials, so it need not share
+    // pass 2's chunking)
     const float q_scale = 1.0f / sqrtf(static_cast<float>(kD));
     // little K to read and the [L, H] stash: four waves per tile, as for flash
     const long long kv_tiles = (a.seq_lens ? total_tiles : static_cast<long long>(a.B) * a.T_c) * a.KVH;
-    if (stash_ld == 0 && !a.pt.table && (!a.seq_lens || total_tiles >= 0) && small_prop_pass(kv_tiles))
-      return (dtype == SANTA_BF16) ? launch_bn<true, 4, kPass1Vec>(256, a, stream)
-                                   : launch_bn<false, 4, kPass1Vec>(256, a, stream);
+    if (stash_ld == 0 && !a.pt.table && (!a.seq_lens || total_tiles >= 0) && small_prop_pass(kv_tiles)) {
+      if (GH == 4)
+        return (dtype == SANTA_BF16) ? launch_bn<true, 4, kPass1Vec>(256, a, stream)
+                                     : launch_bn<false, 4, kPass1Vec>(256, a, stream);
+      return (dtype == SANTA_BF16) ? launch_bn<true, 8, kPass1Gen>(256, a, stream)
+                                   : launch_bn<false, 8, kPass1Gen>(256, a, stream);
+    }
     const bool rows = rows_layout(a.KVH) && (!a.seq_lens || total_tiles >= 0);
     if (rows) {
       if (a.seq_lens) {
@@ -1792,24 +1874,32 @@ hipError_t launch_prop_pass1(const void* q, const void* K, int dtype, int B, int
     if (rows) grid /= static_cast<unsigned>(a.KVH);
     if (grid == 0) return hipSuccess;
     const dim3 block(rows ? static_cast<unsigned>(64 * a.KVH) : static_cast<unsigned>(kThreads));
-#define SANTA_P1_LAUNCH(BF, PG, RW)                                                                               \
-  hipLaunchKernelGGL((wave_kernel<BF, 4, false, true, PG, RW>), dim3(grid), block, 0, stream,                     \
+#define SANTA_P1_LAUNCH(BF, G, PG, RW)                                                                            \
+  hipLaunchKernelGGL((wave_kernel<BF, G, false, true, PG, RW>), dim3(grid), block, 0, stream,                     \
                      static_cast<const uint16_t*>(a.q), static_cast<const uint16_t*>(a.K), nullptr, a.H, a.KVH,     \
                      a.L_valid, a.L_storage, a.T_c, a.cs, a.cpg, q_scale, 0, 0ULL, nullptr, nullptr, a.seq_lens,   \
                      a.B, 0LL, m_tiles, ell_tiles, nullptr, u_stash, stash_ld, a.pt)
+#define SANTA_P1_GH(BF, PG, RW)    \
+  do {                             \
+    if (GH == 4)                   \
+      SANTA_P1_LAUNCH(BF, 4, PG, RW); \
+    else                           \
+      SANTA_P1_LAUNCH(BF, 8, PG, RW); \
+  } while (0)
     if (dtype == SANTA_BF16) {
       if (rows) {
-        if (a.pt.table) SANTA_P1_LAUNCH(true, true, true); else SANTA_P1_LAUNCH(true, false, true);
+        if (a.pt.table) SANTA_P1_GH(true, true, true); else SANTA_P1_GH(true, false, true);
       } else {
-        if (a.pt.table) SANTA_P1_LAUNCH(true, true, false); else SANTA_P1_LAUNCH(true, false, false);
+        if (a.pt.table) SANTA_P1_GH(true, true, false); else SANTA_P1_GH(true, false, false);
       }
     } else {
       if (rows) {
-        if (a.pt.table) SANTA_P1_LAUNCH(false, true, true); else SANTA_P1_LAUNCH(false, false, true);
+        if (a.pt.table) SANTA_P1_GH(false, true, true); else SANTA_P1_GH(false, false, true);
       } else {
-        if (a.pt.table) SANTA_P1_LAUNCH(false, true, false); else SANTA_P1_LAUNCH(false, false, false);
+        if (a.pt.table) SANTA_P1_GH(false, true, false); else SANTA_P1_GH(false, false, false);
       }
     }
+#undef SANTA_P1_GH
 #undef SANTA_P1_LAUNCH
     return hipGetLastError();
   }
@@ -1842,6 +1932,11 @@ bool small_pass(long long kv_tiles) { return kv_tiles <= rows_per_round(); }
 // about 32k tokens of one sequence (per call: 4k 30.8 -> 19.7 us, 16k 38.5 ->
 // 31.3 us; 32k 44.0 -> 45.8 us, 64k 54.3 -> 64.5 us).
 bool small_prop_pass(long long kv_tiles) { return kv_tiles <= rows_per_round() / 4; }
+// santa_prop's pass 1 runs on the wave kernel at block_n 256 for the vec
+// path (GH 4) and for the general path at GH 8.
+bool prop_wave_pass1(int path, int GH, int block_n) {
+  return block_n == 256 && ((path == 0 && GH == 4) || (path == 1 && GH == 8));
+}
 static bool small_pass(int B, int KVH, int T_c) { return small_pass(static_cast<long long>(B) * KVH * T_c); }
 
 // Ragged batches: chunks small enough for about eight resident rounds over

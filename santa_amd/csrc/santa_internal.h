@@ -59,6 +59,10 @@ bool rows_layout(int KVH);
 // vec pass 1 that also means the [L, H] stash layout.
 bool small_pass(long long kv_tiles);
 bool small_prop_pass(long long kv_tiles);
+// santa_prop's pass 1 on the wave kernel (block_n 256: the vec path at GH 4,
+// the general path at GH 8); it writes the head-major stash when given a
+// stash_ld, which pass 2 then reads.
+bool prop_wave_pass1(int path, int GH, int block_n);
 int rows_per_round();
 // The block_n = 256 online tile pass (the wave kernel) with its per-tile
 // statistics m, ell [B, H, T_c] and counts [B, H, T_c, 256] written out

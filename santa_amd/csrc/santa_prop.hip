@@ -938,11 +938,11 @@ extern "C" int santa_prop_decode(const void* q, const void* K, const void* V, in
   float* a0 = reinterpret_cast<float*>(base + w.a0);
   uint16_t* stash = reinterpret_cast<uint16_t*>(base + w.stash);
   const bool gen = propgen::generic_shape(H / KVH, D, block_n);
-  // the vec path keeps the stash head-major between its two passes, except
-  // for a small pass, whose pass 1 runs four waves per tile with the [L, H]
-  // stash
+  // a pass 1 on the wave kernel (the vec path, the general path at GH 8)
+  // keeps the stash head-major between the two passes, except for a small
+  // pass, which runs four waves per tile with the [L, H] stash
   const bool small = flash::small_prop_pass(static_cast<long long>(T_c) * KVH);
-  const int sld = (pass1_path == 0 && !small) ? prop::stash_ld(L) : 0;
+  const int sld = (!gen && flash::prop_wave_pass1(pass1_path, H / KVH, block_n) && !small) ? prop::stash_ld(L) : 0;
   hipError_t e = gen ? propgen::launch_pass1(q, K, dtype, 1, H, KVH, D, L, L, block_n, m_tiles, ell_tiles, stash,
                                              nullptr, -1, PageTable{nullptr, 0, 3, 1}, stream)
                      : flash::launch_prop_pass1(q, K, dtype, 1, H, KVH, L, L, block_n, pass1_path, m_tiles, ell_tiles,
@@ -995,7 +995,8 @@ static int prop_decode_batched(const void* q, const void* K, const void* V, int 
   uint16_t* stash = reinterpret_cast<uint16_t*>(base + w.stash);
   const bool gen = propgen::generic_shape(H / KVH, D, block_n);
   const bool small = !pt.table && flash::small_prop_pass(total_tiles * KVH);  // as in the scalar call
-  const int sld = (pass1_path == 0 && !small) ? prop::stash_ld(L_storage) : 0;
+  const int sld =
+      (!gen && flash::prop_wave_pass1(pass1_path, H / KVH, block_n) && !small) ? prop::stash_ld(L_storage) : 0;
   hipError_t e = gen ? propgen::launch_pass1(q, K, dtype, B, H, KVH, D, max_len, L_storage, block_n, m_tiles,
                                              ell_tiles, stash, seq_lens, total_tiles, pt, stream)
                      : flash::launch_prop_pass1(q, K, dtype, B, H, KVH, max_len, L_storage, block_n, pass1_path,
