@@ -428,14 +428,16 @@ __global__ __launch_bounds__(kThreads) void pass2_kernel(const uint16_t* __restr
     lc[k] = 0;
   };
 
-  // stash entries of tile t for this lane's rows: u[k][p][0/1]
+  // stash entries of tile t for this lane's rows: u[k][p][0/1]; heads whose
+  // bit in `heads` is clear (a zero budget on that tile) are not loaded
   using UBuf = uint16_t[HPW][NPAIR];
-  auto load_u = [&](int t, UBuf& un0, UBuf& un1) {
+  auto load_u = [&](int t, UBuf& un0, UBuf& un1, unsigned heads) {
     const int n0 = t * BN;
     const int len = min(BN, L - n0);
 #pragma unroll
     for (int k = 0; k < HPW; ++k) {
       const int h = h0 + wave + 4 * k;
+      if (!((heads >> k) & 1u)) continue;
 #pragma unroll
       for (int p = 0; p < NPAIR; ++p) {
         const int row = 32 * (4 * p + jrow) + 2 * qq;
@@ -465,11 +467,21 @@ __global__ __launch_bounds__(kThreads) void pass2_kernel(const uint16_t* __restr
   };
   // Stash entries two tiles ahead: tiles alternate between two buffers, and
   // a buffer is refilled with tile t + 2 as soon as tile t has read it.
+  // heads of this wave with a nonzero budget on tile t (all of them when
+  // t's budgets are not among the loaded terms)
+  auto active_heads = [&](int t) -> unsigned {
+    const int li = t - (t_begin + ((t - t_begin) & ~63));
+    unsigned m = 0;
+#pragma unroll
+    for (int k = 0; k < HPW; ++k)
+      if (__int_as_float(__builtin_amdgcn_readlane(__float_as_int(inv_l[k]), li)) > 0.0f) m |= 1u << k;
+    return m;
+  };
   UBuf ua0, ua1, ub0, ub1;
   if (t_begin < t_end) {
-    load_u(t_begin, ua0, ua1);
-    if (t_begin + 1 < t_end) load_u(t_begin + 1, ub0, ub1);
     load_terms(t_begin);
+    load_u(t_begin, ua0, ua1, active_heads(t_begin));
+    if (t_begin + 1 < t_end) load_u(t_begin + 1, ub0, ub1, (t_begin + 1) - t_begin < 64 ? active_heads(t_begin + 1) : ~0u);
   }
 
   auto tile_step = [&](int t, UBuf& un0, UBuf& un1) {
@@ -489,12 +501,24 @@ __global__ __launch_bounds__(kThreads) void pass2_kernel(const uint16_t* __restr
         x1[k][p] = (inv[k] > 0.0f) ? h16_to_f32<BF16>(un1[k][p]) * inv[k] : 0.0f;
       }
     }
-    if (t + 2 < t_end) load_u(t + 2, un0, un1);
+    // tile t + 2's budgets are loaded when it lies in the same 64-tile window
+    if (t + 2 < t_end) load_u(t + 2, un0, un1, (li + 2 < 64) ? active_heads(t + 2) : ~0u);
 
 #pragma unroll
     for (int k = 0; k < HPW; ++k) {
       const int g = wave + 4 * k;
       const int h = h0 + g;
+      if (!(inv[k] > 0.0f)) {
+        // a zero budget on this tile: x = 0 on every row, so every count is 0
+        // (floor(a0) - floor(a0)) and nothing is listed
+        if (lane == 0)
+#pragma unroll
+          for (int m = 0; m < NM; ++m) s_mask[par][g * NM + m] = 0;
+        if (dbg_counts)
+          for (int r = lane; r < BN; r += 64)
+            dbg_counts[((static_cast<size_t>(b) * H + h) * T_c + t) * BN + r] = 0;
+        continue;
+      }
       int c0[NPAIR], c1[NPAIR];
       systematic_counts<NCH>(x0[k], x1[k], len, a0v[k], lane, c0, c1);
       const uint64_t below = (1ull << lane) - 1ull;

@@ -358,6 +358,12 @@ __global__ __launch_bounds__(kThreads) void pass2_kernel(const uint16_t* __restr
       const size_t ht = (static_cast<size_t>(b) * H + h) * T_c + t;
       const float inv = invdelta[ht];
       const float a0 = a0_tile[ht];
+      if (!(inv > 0.0f)) {
+        // a zero budget on this tile: every count is 0, nothing is listed
+        if (dbg_counts)
+          for (int r = lane; r < BN; r += 64) dbg_counts[ht * BN + r] = 0;
+        continue;
+      }
       float carry = 0.0f;
       int lc = 0;
       for (int base = 0; base < len; base += 32) {
