@@ -968,10 +968,12 @@ __global__ __launch_bounds__(ROWS ? 512 : kThreads, ROWS ? 1 : 2) void wave_kern
     const int len = (t < t_end) ? min(BN, L_valid - t * BN) : 0;
     const int r0 = 128 * (sb >> 1) + (sb & 1);
     const char* kt = Kg + static_cast<size_t>(t * BN + r0) * rb;
+    // rows of the sub-block's stride-2 run still valid, wave-uniform (one
+    // readfirstlane, then scalar arithmetic per load)
+    const int rem = __builtin_amdgcn_readfirstlane(len - r0);
 #pragma unroll
     for (int c = 0; c < 16; ++c) {
-      // wave-uniform; readfirstlane keeps the descriptor in SGPRs
-      const int nvalid = __builtin_amdgcn_readfirstlane(min(max(len - r0 - 8 * c, 0), 8));
+      const int nvalid = min(max(rem - 8 * c, 0), 8);
       const char* gb = PAGED ? group_base(t, r0 + 8 * c, pv) : kt + static_cast<size_t>(8 * c) * rb;
       const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
           const_cast<char*>(gb), static_cast<short>(0), nvalid * static_cast<int>(rb), kBufferWord3);
@@ -992,9 +994,10 @@ __global__ __launch_bounds__(ROWS ? 512 : kThreads, ROWS ? 1 : 2) void wave_kern
     const uint32_t rb = row_bytes;
     const int len = min(BN, L_valid - t * BN);
     const char* kt = Kg + static_cast<size_t>(t * BN) * rb;
+    const int rem = __builtin_amdgcn_readfirstlane(len);
 #pragma unroll
     for (int c = 0; c < 16; ++c) {
-      const int nvalid = __builtin_amdgcn_readfirstlane(min(max(len - 8 * c, 0), 8));
+      const int nvalid = min(max(rem - 8 * c, 0), 8);
       const char* gb = PAGED ? group_base(t, 8 * c, pv) : kt + static_cast<size_t>(8 * c) * rb;
       const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
           const_cast<char*>(gb), static_cast<short>(0), nvalid * static_cast<int>(rb), kBufferWord3);

@@ -21,7 +21,9 @@ __device__ __forceinline__ uint16_t to_bf(float f) { return f32_to_h16<true>(f);
 constexpr int kNormThreads = 256;
 
 // One workgroup per row: h = bf16(h + a) when add, then
-// x = bf16(float(h) * rsqrt(mean(float(h)^2) + eps) * float(w)).
+// x = bf16(float(w) * float(bf16(float(h) * rsqrt(mean(float(h)^2) + eps)))),
+// the roundings of LlamaRMSNorm: the normalised row is rounded to bf16
+// before the weight multiply.
 __global__ __launch_bounds__(kNormThreads) void add_rms_norm_kernel(uint16_t* __restrict__ h,
                                                                     const uint16_t* __restrict__ a,
                                                                     const uint16_t* __restrict__ w,
@@ -50,7 +52,7 @@ __global__ __launch_bounds__(kNormThreads) void add_rms_norm_kernel(uint16_t* __
 #pragma unroll
   for (int i = 0; i < kNormThreads / 64; ++i) tot += s_part[i];
   const float r = 1.0f / sqrtf(tot / static_cast<float>(hidden) + eps);
-  for (int i = threadIdx.x; i < hidden; i += kNormThreads) xr[i] = to_bf((bf(hr[i]) * r) * bf(w[i]));
+  for (int i = threadIdx.x; i < hidden; i += kNormThreads) xr[i] = to_bf(bf(w[i]) * bf(to_bf(bf(hr[i]) * r)));
 }
 
 // Thread per (b, head, d): heads [0, H) are q (to q_out [B, H, D]), [H,

@@ -52,9 +52,12 @@ LLAMA_3_1_8B = LlamaShape(hidden=4096, intermediate=14336, heads=32, kv_heads=8,
 
 
 def _rms_norm(x: torch.Tensor, w: torch.Tensor, eps: float) -> torch.Tensor:
+    """LlamaRMSNorm's roundings (the reference's model, runtime_common.py:536):
+    x·rsqrt(mean(x²) + eps) in float32, rounded to x's dtype, then times the
+    weight in the weight's dtype."""
     xf = x.float()
     xf = xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + eps)
-    return (xf * w.float()).to(x.dtype)
+    return w * xf.to(x.dtype)
 
 
 class _FusedOps:

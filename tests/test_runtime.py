@@ -64,3 +64,25 @@ def test_greedy_decode_and_deviation():
     assert torch.equal(a["tokens"], b["tokens"])
     dev = decode_deviation(a["logits"], b["logits"])
     assert max(dev["max_abs"]) == 0.0 and min(dev["top1_agree"]) == 1.0
+
+
+def test_rms_norm_matches_llama_rms_norm():
+    """_rms_norm has LlamaRMSNorm's roundings (the reference model's norm,
+    runtime_common.py:536): the normalised row is rounded to the input dtype
+    before the weight multiply, in bf16 and in float32."""
+    from transformers.models.llama.modeling_llama import LlamaRMSNorm
+
+    from santa_amd.runtime import _rms_norm
+
+    g = torch.Generator().manual_seed(5)
+    for dtype in (torch.bfloat16, torch.float32):
+        x = (3.0 * torch.randn(4, 4096, generator=g)).to(dtype)
+        w = (1.0 + 0.3 * torch.randn(4096, generator=g)).to(dtype)
+        ref = LlamaRMSNorm(4096, eps=1e-5).to(dtype)
+        with torch.no_grad():
+            ref.weight.copy_(w)
+            want = ref(x)
+        got = _rms_norm(x, w, 1e-5)
+        assert got.dtype == want.dtype
+        assert torch.equal(got.view(torch.int16 if dtype == torch.bfloat16 else torch.int32),
+                           want.view(torch.int16 if dtype == torch.bfloat16 else torch.int32))

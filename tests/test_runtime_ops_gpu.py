@@ -4,8 +4,10 @@ against the torch expressions of santa_amd/runtime.py they replace.
 * RoPE with the cache write: bit-exact (each product and the sum are one
   IEEE float operation rounded to bf16, as in torch's bf16 arithmetic);
   rows of the caches other than the written position are untouched.
-* add + RMSNorm: the residual sum bit-exact; the norm to one bf16 unit in
-  the last place (the float32 sum of squares is reduced in another order).
+* add + RMSNorm: the residual sum bit-exact; the norm to two bf16 units in
+  the last place (the float32 sum of squares is reduced in another order, so
+  the normalised row can round to a neighbouring bf16 value, which the weight
+  multiply scales by up to 1.3 before the second rounding).
 * SwiGLU: to one bf16 unit in the last place (exp is this library's).
 
 Every case prints its name and shape before touching the GPU.
@@ -43,8 +45,8 @@ def test_add_rms_norm(rows, hidden):
     x0 = _FusedOps.add_rms_norm(h.clone(), None, w, 1e-5)
     torch.cuda.synchronize()
     assert torch.equal(h2.view(torch.int16), ref_h.view(torch.int16))
-    _ulp_close(x, ref_x)
-    _ulp_close(x0, _rms_norm(h, w, 1e-5))
+    _ulp_close(x, ref_x, 2)
+    _ulp_close(x0, _rms_norm(h, w, 1e-5), 2)
 
 
 @pytest.mark.parametrize("B,H,KVH,pos", [(4, 32, 8, 37), (2, 64, 8, 0), (1, 16, 2, 99)])
