@@ -256,9 +256,10 @@ __global__ __launch_bounds__(64 * NW) void budgets_kernel(const float* __restric
     return;
   }
 
-  // integer bases and jittered fractional parts (:662-678)
+  // integer bases and jittered fractional parts (:662-678); u01(seed, h, t)
+  // is both the jitter's draw and the tile's a0
   int bt[R], id[R];
-  float f[R];
+  float f[R], ut[R];
   int base = 0;
 #pragma unroll
   for (int r = 0; r < R; ++r) {
@@ -266,13 +267,15 @@ __global__ __launch_bounds__(64 * NW) void budgets_kernel(const float* __restric
     bt[r] = 0;
     f[r] = -__builtin_inff();
     id[r] = -1;
+    ut[r] = 0.0f;
     if (t < T_c) {
+      ut[r] = u01(seed, h, t);
       const float q = static_cast<float>(S) * (w[r] / Z);
       const float fq = floorf(q);
       bt[r] = (fq != fq) ? 0 : (fq >= 2147483648.0f ? 2147483647 : static_cast<int>(fq));
       base += bt[r];
       const float ft = q - static_cast<float>(bt[r]);
-      const float jitter = 1.0e-7f * u01(seed, h, t);
+      const float jitter = 1.0e-7f * ut[r];
       f[r] = ft + jitter;
       id[r] = t;
     }
@@ -306,7 +309,7 @@ __global__ __launch_bounds__(64 * NW) void budgets_kernel(const float* __restric
       const int s_t = bt[r] + s_i[t];
       S_tiles[off + t] = s_t;
       invdelta[off + t] = (s_t > 0 && lv[r] > 1e-20f) ? (static_cast<float>(s_t) / lv[r]) : 0.0f;
-      a0_tile[off + t] = u01(seed, h, t);
+      a0_tile[off + t] = ut[r];
     }
   }
 }
@@ -339,8 +342,13 @@ __device__ __forceinline__ int union_rows(const uint64_t* s_mask, int lane) {
 // for the vec path: a lane reads its row pair with one 4-B load); otherwise
 // the reference's [B, L_storage, H].
 // PAGED: V is a page pool read through pt (the stash is indexed by token).
+// The kernel is bound by the latency of its per-tile chains (stash load,
+// scan, carries, list appends) and of the V gathers, so it is compiled for
+// as many resident waves as fit without spilling: six per SIMD (80 VGPRs)
+// for one head per wave at block_n 256, four (128) otherwise; the V gathers
+// go out 16 rows at a time (cfg3 step 542 -> 518 us).
 template <bool BF16, int GH, int BN, bool HM, bool PAGED = false>
-__global__ __launch_bounds__(kThreads) void pass2_kernel(const uint16_t* __restrict__ V,
+__global__ __launch_bounds__(kThreads, (GH == 4 && BN == 256) ? 6 : 4) void pass2_kernel(const uint16_t* __restrict__ V,
                                                          const uint16_t* __restrict__ u_stash, int H, int KVH,
                                                          int L, int L_storage, int T_c, int cs, int cpg,
                                                          const float* __restrict__ invdelta,
@@ -393,23 +401,24 @@ __global__ __launch_bounds__(kThreads) void pass2_kernel(const uint16_t* __restr
   int emit_total = 0;
 
   // Count-weighted V rows of the listed samples, in list (ascending) order,
-  // one fma per element (prop/santa_cuda_kernel.cu:843-857); up to 32 row
+  // one fma per element (prop/santa_cuda_kernel.cu:843-857); up to FB row
   // loads are in flight before the first is used.
   int lc[HPW];
 #pragma unroll
   for (int k = 0; k < HPW; ++k) lc[k] = 0;
+  constexpr int FB = 16;
   auto flush = [&](int k, int g) {
-    for (int base = 0; base < lc[k]; base += 32) {
-      float cf[32];
-      uint32_t vw[32];
+    for (int base = 0; base < lc[k]; base += FB) {
+      float cf[FB];
+      uint32_t vw[FB];
       // paged: lane q looks up the page of the batch's q-th row
       int pgv = 0;
       if constexpr (PAGED) {
-        const int iq = min(base + (lane & 31), lc[k] - 1);
+        const int iq = min(base + (lane & (FB - 1)), lc[k] - 1);
         pgv = page_of_row(pt, b, s_lrow[g * BN + iq], true);
       }
 #pragma unroll
-      for (int q = 0; q < 32; ++q) {
+      for (int q = 0; q < FB; ++q) {
         const int i = min(base + q, lc[k] - 1);
         const int rr = __builtin_amdgcn_readfirstlane(s_lrow[g * BN + i]);
         cf[q] = s_lcw[g * BN + i];
@@ -418,7 +427,7 @@ __global__ __launch_bounds__(kThreads) void pass2_kernel(const uint16_t* __restr
         vw[q] = *reinterpret_cast<const uint32_t*>(Vg + off + v_lane_off);
       }
 #pragma unroll
-      for (int q = 0; q < 32; ++q) {
+      for (int q = 0; q < FB; ++q) {
         if (base + q < lc[k]) {
           acc0[k] = fmaf(cf[q], lo16_to_f32<BF16>(vw[q]), acc0[k]);
           acc1[k] = fmaf(cf[q], hi16_to_f32<BF16>(vw[q]), acc1[k]);
