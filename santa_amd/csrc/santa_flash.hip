@@ -1590,6 +1590,77 @@ __global__ __launch_bounds__(1024) void merge_kernel(const float* __restrict__ p
   if (vrows && g == 0 && d == 0) vrows[bk] = e;
 }
 
+// The same merge for at most NB chunks per (b, h), one wave per (b, h): lane
+// c reads chunk c's M, Z (and emitted-row count), lane l the numerator pair
+// (2l, 2l + 1) of every chunk, all loads issued before the first use; w_c =
+// exp(M_c - m*) is computed once, by lane c; Z and the numerator are summed
+// over c in ascending order.  One memory round trip, no LDS, no barrier.
+template <bool BF16, int GH, int NB>
+__global__ __launch_bounds__(64) void merge_wave_kernel(const float* __restrict__ part,
+                                                        const int* __restrict__ part_emit, int H, int KVH, int cpg,
+                                                        int S_pt, uint16_t* __restrict__ out,
+                                                        float* __restrict__ m_star, int* __restrict__ vrows,
+                                                        const int* __restrict__ seq_lens, int BN, int cs,
+                                                        int max_len, int n_wg, long long S_total) {
+  const int bh = static_cast<int>(blockIdx.x);
+  const int b = bh / H;
+  const int h = bh % H;
+  const int kv = h / GH;
+  const int g = h % GH;
+  const int lane = static_cast<int>(threadIdx.x);
+  // chunk c of (b, kv) was workgroup base_b + c * KVH + kv
+  int base = b * cpg * KVH;
+  if (seq_lens) {
+    base = 0;
+    for (int bb = 0; bb < b; ++bb) base += KVH * (((ragged_len(seq_lens, bb, max_len) + BN - 1) / BN + cs - 1) / cs);
+    const int tiles = (ragged_len(seq_lens, b, max_len) + BN - 1) / BN;
+    cpg = (tiles + cs - 1) / cs;
+    cpg = max(0, min(cpg, (n_wg - base - kv + KVH - 1) / KVH));  // only launched workgroups wrote partials
+    S_pt = (S_total > 0) ? static_cast<int>(max(1LL, S_total / static_cast<long long>(tiles))) : 0;
+  }
+  const int n = min(cpg, NB);
+  const float* pb = part + ((static_cast<size_t>(base) + kv) * GH + g) * kPartStride;
+  const size_t cstride = static_cast<size_t>(KVH) * GH * kPartStride;
+  float Mc = -__builtin_inff(), Zc = 0.0f;
+  int ec = 0;
+  if (lane < n) {
+    Mc = pb[lane * cstride];
+    Zc = pb[lane * cstride + 1];
+    if (vrows && g == 0) ec = part_emit[static_cast<size_t>(base) + lane * KVH + kv];
+  }
+  float2 nv[NB];
+  if (n > 0) {
+#pragma unroll
+    for (int c = 0; c < NB; ++c) {
+      const int cc = min(c, n - 1);  // past n: chunk n - 1 again, weighted by 0
+      nv[c] = *reinterpret_cast<const float2*>(pb + cc * cstride + 2 + 2 * lane);
+    }
+  } else {
+#pragma unroll
+    for (int c = 0; c < NB; ++c) nv[c] = make_float2(0.0f, 0.0f);
+  }
+  const float ms = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(wave_max_lane63(Mc + 0.0f)), 63));
+  const float w = (lane < n && ms != -__builtin_inff()) ? santa_expf(Mc - ms) : 0.0f;
+  float Z = 0.0f, num0 = 0.0f, num1 = 0.0f;
+#pragma unroll
+  for (int c = 0; c < NB; ++c) {
+    const float wc = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(w), c));
+    const float zc = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(Zc), c));
+    Z = fmaf(wc, zc, Z);
+    num0 = fmaf(wc, nv[c].x, num0);
+    num1 = fmaf(wc, nv[c].y, num1);
+  }
+  const float inv_norm = (S_pt > 0 && Z > 0.0f) ? (1.0f / (Z * static_cast<float>(S_pt))) : 0.0f;
+  *reinterpret_cast<uint32_t*>(out + static_cast<size_t>(bh) * kD + 2 * lane) =
+      static_cast<uint32_t>(f32_to_h16<BF16>(num0 * inv_norm)) |
+      (static_cast<uint32_t>(f32_to_h16<BF16>(num1 * inv_norm)) << 16);
+  if (lane == 0 && m_star) m_star[bh] = ms;
+  if (vrows && g == 0) {
+    const int e = wave_sum_int(ec);
+    if (lane == 0) vrows[static_cast<size_t>(b) * KVH + kv] = e;
+  }
+}
+
 struct Args {
   const void* q;
   const void* K;
@@ -1719,8 +1790,29 @@ static hipError_t launch_merge(const float* part, const int* pe, int dtype, int 
   const int GH = H / KVH;
   const unsigned grid = static_cast<unsigned>(B) * static_cast<unsigned>(H);
   uint16_t* o = static_cast<uint16_t*>(out);
-  // thread groups of 128: enough that each merges at most 16 chunks (up to 8)
   const int max_chunks = seq_lens ? ((max_len + bn - 1) / bn + cs - 1) / cs : cpg;
+  if (max_chunks <= 64) {
+    // one wave per (b, h)
+#define SANTA_MERGE_WAVE(BF, G, NBC)                                                                          \
+  hipLaunchKernelGGL((merge_wave_kernel<BF, G, NBC>), dim3(grid), dim3(64), 0, stream, part, pe, H, KVH, cpg, \
+                     S_pt, o, m_star, vrows, seq_lens, bn, cs, max_len, n_wg, S_total)
+#define SANTA_MERGE_NB(BF, G)           \
+  if (max_chunks <= 16)                 \
+    SANTA_MERGE_WAVE(BF, G, 16);        \
+  else if (max_chunks <= 32)            \
+    SANTA_MERGE_WAVE(BF, G, 32);        \
+  else                                  \
+    SANTA_MERGE_WAVE(BF, G, 64)
+    if (dtype == SANTA_BF16) {
+      if (GH == 4) { SANTA_MERGE_NB(true, 4); } else { SANTA_MERGE_NB(true, 8); }
+    } else {
+      if (GH == 4) { SANTA_MERGE_NB(false, 4); } else { SANTA_MERGE_NB(false, 8); }
+    }
+#undef SANTA_MERGE_NB
+#undef SANTA_MERGE_WAVE
+    return hipGetLastError();
+  }
+  // thread groups of 128: enough that each merges at most 16 chunks (up to 8)
   const int ngrp = std::min(8, std::max(1, (max_chunks + 15) / 16));
   const dim3 block(static_cast<unsigned>(kD * ngrp));
   if (dtype == SANTA_BF16) {
