@@ -348,7 +348,7 @@ __device__ __forceinline__ int union_rows(const uint64_t* s_mask, int lane) {
 // for one head per wave at block_n 256, four (128) otherwise; the V gathers
 // go out 16 rows at a time (cfg3 step 542 -> 518 us).
 template <bool BF16, int GH, int BN, bool HM, bool PAGED = false>
-__global__ __launch_bounds__(kThreads, (GH == 4 && BN == 256) ? 6 : 4) void pass2_kernel(const uint16_t* __restrict__ V,
+__global__ __launch_bounds__(kThreads, (GH == 4 && BN == 256 && !PAGED) ? 6 : 4) void pass2_kernel(const uint16_t* __restrict__ V,
                                                          const uint16_t* __restrict__ u_stash, int H, int KVH,
                                                          int L, int L_storage, int T_c, int cs, int cpg,
                                                          const float* __restrict__ invdelta,
@@ -474,31 +474,44 @@ __global__ __launch_bounds__(kThreads, (GH == 4 && BN == 256) ? 6 : 4) void pass
       a0_l[k] = a0_tile[ht];
     }
   };
-  // Stash entries two tiles ahead: tiles alternate between two buffers, and
-  // a buffer is refilled with tile t + 2 as soon as tile t has read it.
-  // heads of this wave with a nonzero budget on tile t (all of them when
-  // t's budgets are not among the loaded terms)
-  auto active_heads = [&](int t) -> unsigned {
-    const int li = t - (t_begin + ((t - t_begin) & ~63));
+  // heads of this wave with a nonzero budget on tile t of the current window
+  // (which starts at t0)
+  auto active_heads = [&](int t, int t0) -> unsigned {
     unsigned m = 0;
 #pragma unroll
     for (int k = 0; k < HPW; ++k)
-      if (__int_as_float(__builtin_amdgcn_readlane(__float_as_int(inv_l[k]), li)) > 0.0f) m |= 1u << k;
+      if (__int_as_float(__builtin_amdgcn_readlane(__float_as_int(inv_l[k]), t - t0)) > 0.0f) m |= 1u << k;
     return m;
   };
-  UBuf ua0, ua1, ub0, ub1;
-  if (t_begin < t_end) {
-    load_terms(t_begin);
-    load_u(t_begin, ua0, ua1, active_heads(t_begin));
-    if (t_begin + 1 < t_end) load_u(t_begin + 1, ub0, ub1, (t_begin + 1) - t_begin < 64 ? active_heads(t_begin + 1) : ~0u);
-  }
+  // Tiles where every head of the group has a zero budget list nothing and
+  // add nothing (every count is floor(a0) - floor(a0) = 0), so each window of
+  // 64 tiles is walked over the tiles where some head of the group has a
+  // budget, in ascending order; every wave walks the same tiles, so the
+  // emit barriers match.  The debug path (counts written out) walks them all.
+  auto window_mask = [&](int t0) -> uint64_t {
+    const int tt = t0 + lane;
+    bool act = tt < t_end;
+    if (act && !dbg_counts) {
+      bool any = false;
+#pragma unroll
+      for (int g = 0; g < GH; ++g) any = any || invdelta[(static_cast<size_t>(b) * H + h0 + g) * T_c + tt] > 0.0f;
+      act = any;
+    }
+    return __ballot(act);
+  };
+  auto pop_tile = [](uint64_t& m, int t0) -> int {
+    if (m == 0) return -1;
+    const int i = __builtin_ctzll(m);
+    m &= m - 1;
+    return t0 + i;
+  };
 
-  auto tile_step = [&](int t, UBuf& un0, UBuf& un1) {
+  int processed = 0;  // tiles walked so far (parity of the emit masks)
+  auto tile_step = [&](int t, int t0, UBuf& un0, UBuf& un1) {
     const int n0 = t * BN;
     const int len = min(BN, L - n0);
-    const int par = (t - t_begin) & 1;
-    const int li = (t - t_begin) & 63;
-    if (li == 0 && t != t_begin) load_terms(t);
+    const int par = processed & 1;
+    const int li = t - t0;
     float x0[HPW][NPAIR], x1[HPW][NPAIR], inv[HPW], a0v[HPW];
 #pragma unroll
     for (int k = 0; k < HPW; ++k) {
@@ -510,9 +523,6 @@ __global__ __launch_bounds__(kThreads, (GH == 4 && BN == 256) ? 6 : 4) void pass
         x1[k][p] = (inv[k] > 0.0f) ? h16_to_f32<BF16>(un1[k][p]) * inv[k] : 0.0f;
       }
     }
-    // tile t + 2's budgets are loaded when it lies in the same 64-tile window
-    if (t + 2 < t_end) load_u(t + 2, un0, un1, (li + 2 < 64) ? active_heads(t + 2) : ~0u);
-
 #pragma unroll
     for (int k = 0; k < HPW; ++k) {
       const int g = wave + 4 * k;
@@ -574,10 +584,28 @@ __global__ __launch_bounds__(kThreads, (GH == 4 && BN == 256) ? 6 : 4) void pass
       __syncthreads();
       if (wave == 0) emit_total += union_rows<GH, NM>(s_mask[par], lane);
     }
+    ++processed;
   };
-  for (int t = t_begin; t < t_end; t += 2) {
-    tile_step(t, ua0, ua1);
-    if (t + 1 < t_end) tile_step(t + 1, ub0, ub1);
+  // stash entries two walked tiles ahead: the walked tiles alternate between
+  // two register buffers, each refilled as soon as its tile has been read
+  UBuf ua0, ua1, ub0, ub1;
+  for (int t0 = t_begin; t0 < t_end; t0 += 64) {
+    load_terms(t0);
+    uint64_t m = window_mask(t0);
+    int tA = pop_tile(m, t0), tB = pop_tile(m, t0);
+    if (tA >= 0) load_u(tA, ua0, ua1, active_heads(tA, t0));
+    if (tB >= 0) load_u(tB, ub0, ub1, active_heads(tB, t0));
+    while (tA >= 0) {
+      const int tC = pop_tile(m, t0);
+      tile_step(tA, t0, ua0, ua1);
+      if (tC >= 0) load_u(tC, ua0, ua1, active_heads(tC, t0));
+      if (tB < 0) break;
+      const int tD = pop_tile(m, t0);
+      tile_step(tB, t0, ub0, ub1);
+      if (tD >= 0) load_u(tD, ub0, ub1, active_heads(tD, t0));
+      tA = tC;
+      tB = tD;
+    }
   }
 
 #pragma unroll
