@@ -65,6 +65,10 @@ def parse_args():
                          "S=512 per sequence; single: one sequence of --ctx tokens through santa_flash (S=256) "
                          "and santa_prop (S=L/64)")
     ap.add_argument("--cpu-sample-seqs", type=int, default=8, help="sequences timed for the CPU baseline")
+    ap.add_argument("--score-scale", type=float, default=1.0,
+                    help="cfg4: multiply the query projections by this (every attention score that many times "
+                         "larger); 1 is the random model's nearly uniform attention")
+    ap.add_argument("--layers", type=int, default=0, help="cfg4: decoder layers (0: the 32 of Llama-3.1-8B)")
     ap.add_argument("--page-size", type=int, default=0,
                     help="cfg2 / cfg3 through the paged-KV entry point: the same tokens scattered over a pool of "
                          "pages of this many tokens in a seeded random order (0: contiguous cache)")
@@ -531,9 +535,11 @@ def run_cfg4(args, dev):
     from santa_amd.runtime import (LLAMA_3_1_8B, ExactDecodeBackend, NHDCache, RandomLlama, decode_deviation,
                                    greedy_decode)
 
+    import dataclasses
+
     B, P, steps, S, seed = 4, 32768, 64, 256, args.seed
-    shape = LLAMA_3_1_8B
-    model = RandomLlama(shape, seed=seed, device=dev)
+    shape = LLAMA_3_1_8B if args.layers <= 0 else dataclasses.replace(LLAMA_3_1_8B, layers=args.layers)
+    model = RandomLlama(shape, seed=seed, device=dev, score_scale=args.score_scale)
     prompt = torch.randint(0, shape.vocab, (B, P), generator=torch.Generator().manual_seed(seed)).to(dev)
     cache = NHDCache(shape, B, P + steps, torch.bfloat16, dev)
     t0 = time.perf_counter()
@@ -559,9 +565,11 @@ def run_cfg4(args, dev):
         "value": tok_s, "unit": "tokens/s", "n_gpus": 1, "steps": steps, "warmup": 3,
         "ms_per_step": step_s * 1e3, "us_per_step": step_s * 1e6, "higher_is_better": True, "scaling": "weak",
         "vs_baseline": None, "dtype": "bf16", "data": "synthetic",
-        "config": {"workload": f"model-level greedy decode, random-init Llama-3.1-8B shape (32 layers, 4096 hidden, "
-                               f"32q/8kv, d=128, 14336 MLP, 128256 vocab; N(0, 0.02) bf16), B={B}, {P}-token "
-                               f"seeded random prompts, {steps} tokens, santa_flash S={S} in every layer",
+        "config": {"workload": f"model-level greedy decode, random-init Llama-3.1-8B shape ({shape.layers} layers, "
+                               f"4096 hidden, 32q/8kv, d=128, 14336 MLP, 128256 vocab; N(0, 0.02) bf16"
+                               + (f", query projections x{args.score_scale:g}" if args.score_scale != 1.0 else "")
+                               + f"), B={B}, {P}-token seeded random prompts, {steps} tokens, santa_flash S={S} in "
+                               "every layer",
                    "global_batch": B, "seq_len": P, "S": S, "parallelism": "single GPU"},
         "roofline": {"bound": "hbm", "achieved": step_bytes / step_s / 1e9, "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                      "frac": step_bytes / step_s / 1e9 / HBM_PEAK_GBPS, "traffic": None,

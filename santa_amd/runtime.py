@@ -225,10 +225,15 @@ class NHDCache:
 
 class RandomLlama:
     """A Llama-architecture decoder with seeded N(0, std) weights (RMSNorm
-    weights 1).  QKV and gate/up projections are stored fused."""
+    weights 1).  QKV and gate/up projections are stored fused.
+
+    score_scale multiplies the query projection, so every attention score is
+    that many times larger: 1 keeps the random model's nearly uniform
+    attention over a long context, larger values give the peaky attention of
+    a trained model, the regime a sampled estimator is built for."""
 
     def __init__(self, shape: LlamaShape, *, seed: int = 1690, std: float = 0.02, dtype=torch.bfloat16,
-                 device="cuda"):
+                 device="cuda", score_scale: float = 1.0):
         self.shape = shape
         self.dtype = dtype
         self.device = torch.device(device)
@@ -254,6 +259,8 @@ class RandomLlama:
                 "wgu": w(2 * s.intermediate, s.hidden),
                 "wd": w(s.hidden, s.intermediate),
             })
+            if score_scale != 1.0:
+                self.layers[-1]["wqkv"][:s.heads * D].mul_(score_scale)
 
     # ------------------------------------------------------------ pieces
     def _qkv(self, L: Dict[str, torch.Tensor], x: torch.Tensor):

@@ -57,3 +57,38 @@ def test_santa_backends_in_the_decode_loop():
     res_p = greedy_decode(model, logits, 700, cache.clone(), prop, 6, forced=exact["tokens"])
     torch.cuda.synchronize()
     assert prop.actual_mode == "batch" and torch.isfinite(res_p["logits"]).all()
+
+
+def test_peaky_attention_agrees_with_exact_at_cfg4_shape():
+    """The model-level loop at cfg4's attention shape (hidden 4096, 32q/8kv,
+    d=128, B=4, 32768-token prompts, santa_flash S=256: T_c=129, S_per_tile=1)
+    with two layers.  With the random model's nearly uniform attention over
+    32k keys the S=256 estimate is noise; scaling the query projection (a
+    trained model's peaky attention) makes the sampled decode agree with the
+    exact one, and the agreement grows with the sharpness."""
+    from santa_amd.runtime import LLAMA_3_1_8B, LlamaShape
+
+    s = LLAMA_3_1_8B
+    shape = LlamaShape(hidden=s.hidden, intermediate=s.intermediate, heads=s.heads, kv_heads=s.kv_heads, layers=2,
+                       vocab=s.vocab)
+    B, P, steps = 4, 32768, 6
+    dev = torch.device("cuda:0")
+    prompt = torch.randint(0, shape.vocab, (B, P), generator=torch.Generator().manual_seed(1690)).to(dev)
+    stats = {}
+    for scale in (1.0, 32.0):
+        print(f"\n[case] cfg4 attention shape, 2 layers, B={B} P={P}, score_scale={scale}", flush=True)
+        model = RandomLlama(shape, seed=1690, device=dev, score_scale=scale)
+        cache = NHDCache(shape, B, P + steps, torch.bfloat16, dev)
+        logits0 = model.prefill(prompt, cache)
+        exact = greedy_decode(model, logits0, P, cache.clone(), ExactDecodeBackend(), steps)
+        flash = ab.SantaFlashBackend(S=256, seed=1690, block_n=None)
+        res = greedy_decode(model, logits0, P, cache, flash, steps, forced=exact["tokens"])
+        torch.cuda.synchronize()
+        assert flash.actual_mode == "batch"
+        d = decode_deviation(res["logits"], exact["logits"])
+        stats[scale] = (sum(d["mean_rel"]) / steps, sum(d["top1_agree"]) / steps)
+        del model, cache
+        torch.cuda.empty_cache()
+    print(stats, flush=True)
+    assert stats[32.0][0] <= 0.1 and stats[32.0][1] >= 0.8, stats
+    assert stats[32.0][0] < 0.2 * stats[1.0][0], stats
