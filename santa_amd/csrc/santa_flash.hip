@@ -875,11 +875,9 @@ __global__ __launch_bounds__(ROWS ? 512 : kThreads, ROWS ? 1 : 2) void wave_kern
   const int t_first = ROWS ? t_begin : t_begin + wave;
 
   __shared__ u32x4 s_k[NWV * 64 * 16];  // per wave: 64 rows x 256 B staging; the chunk merge reuses it
-  __shared__ int s_lrow[NWV * GH * LCAP];
-  __shared__ float s_lcw[NWV * GH * LCAP];
+  __shared__ int2 s_list[NWV * GH * LCAP];  // (row, coefficient bits) per listed row
   u32x4* const wk = s_k + wave * 64 * 16;
-  int* const lrow = s_lrow + wave * GH * LCAP;
-  float* const lcw = s_lcw + wave * GH * LCAP;
+  int2* const list = s_list + wave * GH * LCAP;
 
   // Paged: the base is the pool's (plus this KV head), rows go through pt.
   const size_t row_stride = static_cast<size_t>(KVH) * kD;
@@ -914,33 +912,52 @@ __global__ __launch_bounds__(ROWS ? 512 : kThreads, ROWS ? 1 : 2) void wave_kern
   }
   int emit_total = 0;
 
+  // Gathers of listed rows: lane i holds the V row address of list entry i
+  // (computed for all entries at once), and entry j's row is loaded through
+  // that address read back as a scalar base, the lane's 4 B at v_lane_off.
+  auto v_addr = [&](int rowv, bool ok) -> uint64_t {
+    if constexpr (PAGED) {
+      return reinterpret_cast<uint64_t>(Vg + paged_row(pt, page_of_row(pt, b, rowv, ok), rowv, row_bytes));
+    } else {
+      return reinterpret_cast<uint64_t>(Vg + static_cast<size_t>(rowv) * row_bytes);
+    }
+  };
+  auto v_load = [&](uint64_t av, int j) -> uint32_t {
+    const uint32_t lo = __builtin_amdgcn_readlane(static_cast<uint32_t>(av), j);
+    const uint32_t hi = __builtin_amdgcn_readlane(static_cast<uint32_t>(av >> 32), j);
+    typedef const __attribute__((address_space(1))) char* gbytes;
+    const gbytes row = reinterpret_cast<gbytes>((static_cast<uint64_t>(hi) << 32) | lo);
+    return *reinterpret_cast<const __attribute__((address_space(1))) uint32_t*>(row + v_lane_off);
+  };
+  // entry q0 + q of a list of n into the numerator (a selected update, so the
+  // loads past n -- repeats of entry n - 1 -- are consumed but change nothing)
+  auto accumulate = [&](int g, float coefv, const uint32_t (&vw)[16], int q0, int n) {
+#pragma unroll
+    for (int q = 0; q < 16; ++q) {
+      const float c = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(coefv), min(q0 + q, n - 1)));
+      const float a0 = fmaf(c, lo16_to_f32<BF16>(vw[q]), num0[g]);
+      const float a1 = fmaf(c, hi16_to_f32<BF16>(vw[q]), num1[g]);
+      const bool ok = q0 + q < n;
+      num0[g] = ok ? a0 : num0[g];
+      num1[g] = ok ? a1 : num1[g];
+    }
+  };
+
   // the listed rows of head g, in list order, into the numerator
   auto flush = [&](int g) {
     const int n = lcnt[g];
-    if (n == 0) return;
-    const int rowv = (lane < n) ? lrow[g * LCAP + lane] : 0;
-    const float coefv = (lane < n) ? lcw[g * LCAP + lane] : 0.0f;
-    const int pgv = PAGED ? page_of_row(pt, b, rowv, lane < n) : 0;
-    for (int q0 = 0; q0 < n; q0 += 16) {
-      float coef[16];
+    if (n <= 0) return;
+    const int2 ent = (lane < n) ? list[g * LCAP + lane] : make_int2(0, 0);
+    const uint64_t av = v_addr(ent.x, lane < n);
+    const float coefv = __int_as_float(ent.y);
+    int q0 = 0;
+    do {
       uint32_t vw[16];
 #pragma unroll
-      for (int q = 0; q < 16; ++q) {
-        const int j = min(q0 + q, n - 1);
-        const int row = __builtin_amdgcn_readlane(rowv, j);
-        coef[q] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(coefv), j));
-        const size_t off = PAGED ? paged_row(pt, __builtin_amdgcn_readlane(pgv, j), row, row_bytes)
-                                 : static_cast<size_t>(row) * row_bytes;
-        vw[q] = *reinterpret_cast<const uint32_t*>(Vg + off + v_lane_off);
-      }
-#pragma unroll
-      for (int q = 0; q < 16; ++q) {
-        if (q0 + q < n) {
-          num0[g] = fmaf(coef[q], lo16_to_f32<BF16>(vw[q]), num0[g]);
-          num1[g] = fmaf(coef[q], hi16_to_f32<BF16>(vw[q]), num1[g]);
-        }
-      }
-    }
+      for (int q = 0; q < 16; ++q) vw[q] = v_load(av, min(q0 + q, n - 1));
+      accumulate(g, coefv, vw, q0, n);
+      q0 += 16;
+    } while (q0 < n);
     lcnt[g] = 0;
   };
 
@@ -1014,7 +1031,6 @@ __global__ __launch_bounds__(ROWS ? 512 : kThreads, ROWS ? 1 : 2) void wave_kern
 
   const int jrow = lane >> 4;
   const int qq = lane & 15;
-  const uint64_t below = (1ull << lane) - 1ull;
   // ROWS: waves w and w ^ 4 share a SIMD and walk the same tiles.  Left to
   // the oldest-first issue order, waves 0-3 would end their loops about
   // 14 us (at 32k tokens, 4 tiles per wave) before waves 4-7 and leave half
@@ -1160,7 +1176,7 @@ __global__ __launch_bounds__(ROWS ? 512 : kThreads, ROWS ? 1 : 2) void wave_kern
           }
       float ell[4];
       if constexpr (P1 && GH == 8) {
-        slab_ell4(u, reinterpret_cast<float*>(lrow), lcw, lane, ell);
+        slab_ell4(u, reinterpret_cast<float*>(list), reinterpret_cast<float*>(list) + GH * LCAP, lane, ell);
       } else {
 #pragma unroll
         for (int k = 0; k < 4; ++k) ell[k] = wave_ell<GH>(u[k]);
@@ -1241,7 +1257,10 @@ __global__ __launch_bounds__(ROWS ? 512 : kThreads, ROWS ? 1 : 2) void wave_kern
 #pragma unroll
       for (int k = 0; k < 4; ++k) {
         const int g = 4 * hb + k;
-        if (grow[k] && lane < lcnt[g]) lcw[g * LCAP + lane] *= rsc[k];
+        if (grow[k] && lane < lcnt[g]) {
+          int* const cw = &list[g * LCAP + lane].y;
+          *cw = __float_as_int(__int_as_float(*cw) * rsc[k]);
+        }
 #pragma unroll
         for (int hh = 0; hh < 2; ++hh)
 #pragma unroll
@@ -1252,10 +1271,12 @@ __global__ __launch_bounds__(ROWS ? 512 : kThreads, ROWS ? 1 : 2) void wave_kern
             const int nn = __popcll(nz);
             if (nn) {
               if (lcnt[g] + nn > LCAP) flush(g);
-              const int pos = lcnt[g] + __popcll(nz & below);
               if (c != 0) {
-                lrow[g * LCAP + pos] = n0 + 128 * hh + 32 * jrow + 2 * qq + e;
-                lcw[g * LCAP + pos] = static_cast<float>(c) * f[k];
+                const int pos = lcnt[g] + static_cast<int>(__builtin_amdgcn_mbcnt_hi(
+                                              static_cast<uint32_t>(nz >> 32),
+                                              __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(nz), 0u)));
+                list[g * LCAP + pos] =
+                    make_int2(n0 + 128 * hh + 32 * jrow + 2 * qq + e, __float_as_int(static_cast<float>(c) * f[k]));
               }
               lcnt[g] += nn;
             }
@@ -1305,15 +1326,61 @@ __global__ __launch_bounds__(ROWS ? 512 : kThreads, ROWS ? 1 : 2) void wave_kern
   // head are issued together (one memory round trip per 16 rows, not one per
   // head), then accumulated head by head in list order, as flush() does.
   {
-    int rowv[GH], pgv[GH];
-    float coefv[GH];
     int nmax = 0;
 #pragma unroll
+    for (int g = 0; g < GH; ++g) nmax = max(nmax, lcnt[g]);
+    // Non-paged V with 32-bit offsets: the entries are read two at a time as
+    // one LDS broadcast and each row loads through one descriptor; slots past
+    // a list's end take an offset past the descriptor's range (no traffic,
+    // zero) and are not accumulated.
+    const bool v32 = !PAGED && static_cast<uint64_t>(L_valid) * row_bytes <= 0xffffffffull;
+    if (v32 && nmax > 0) {
+      const __amdgpu_buffer_rsrc_t rs_v = __builtin_amdgcn_make_buffer_rsrc(
+          const_cast<char*>(Vg), static_cast<short>(0), static_cast<int>(static_cast<uint32_t>(L_valid) * row_bytes),
+          kBufferWord3);
+      for (int q0 = 0; q0 < nmax; q0 += 16) {
+        uint32_t vw[GH][16];
+        float cw[GH][16];
+#pragma unroll
+        for (int g = 0; g < GH; ++g) {
+          if (lcnt[g] > q0) {
+#pragma unroll
+            for (int p = 0; p < 8; ++p) {
+              const int4 e2 = *reinterpret_cast<const int4*>(&list[g * LCAP + q0 + 2 * p]);
+              cw[g][2 * p] = __int_as_float(e2.y);
+              cw[g][2 * p + 1] = __int_as_float(e2.w);
+              const uint32_t o0 = (q0 + 2 * p < lcnt[g]) ? __umul24(static_cast<uint32_t>(e2.x), row_bytes) + v_lane_off
+                                                          : 0xffffffffu;
+              const uint32_t o1 = (q0 + 2 * p + 1 < lcnt[g])
+                                      ? __umul24(static_cast<uint32_t>(e2.z), row_bytes) + v_lane_off
+                                      : 0xffffffffu;
+              vw[g][2 * p] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_raw_buffer_load_b32(rs_v, o0, 0, 0));
+              vw[g][2 * p + 1] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_raw_buffer_load_b32(rs_v, o1, 0, 0));
+            }
+          }
+        }
+#pragma unroll
+        for (int g = 0; g < GH; ++g) {
+          if (lcnt[g] > q0) {
+#pragma unroll
+            for (int q = 0; q < 16; ++q) {
+              if (q0 + q < lcnt[g]) {
+                num0[g] = fmaf(cw[g][q], lo16_to_f32<BF16>(vw[g][q]), num0[g]);
+                num1[g] = fmaf(cw[g][q], hi16_to_f32<BF16>(vw[g][q]), num1[g]);
+              }
+            }
+          }
+        }
+      }
+      nmax = 0;
+    }
+    uint64_t av[GH];
+    float coefv[GH];
+#pragma unroll
     for (int g = 0; g < GH; ++g) {
-      rowv[g] = (lane < lcnt[g]) ? lrow[g * LCAP + lane] : 0;
-      coefv[g] = (lane < lcnt[g]) ? lcw[g * LCAP + lane] : 0.0f;
-      pgv[g] = PAGED ? page_of_row(pt, b, rowv[g], lane < lcnt[g]) : 0;
-      nmax = max(nmax, lcnt[g]);
+      const int2 ent = (lane < lcnt[g]) ? list[g * LCAP + lane] : make_int2(0, 0);
+      av[g] = v_addr(ent.x, lane < lcnt[g]);
+      coefv[g] = __int_as_float(ent.y);
     }
     for (int q0 = 0; q0 < nmax; q0 += 16) {
       uint32_t vw[GH][16];
@@ -1321,27 +1388,12 @@ __global__ __launch_bounds__(ROWS ? 512 : kThreads, ROWS ? 1 : 2) void wave_kern
       for (int g = 0; g < GH; ++g) {
         if (lcnt[g] > q0) {
 #pragma unroll
-          for (int q = 0; q < 16; ++q) {
-            const int j = min(q0 + q, lcnt[g] - 1);
-            const int row = __builtin_amdgcn_readlane(rowv[g], j);
-            const size_t off = PAGED ? paged_row(pt, __builtin_amdgcn_readlane(pgv[g], j), row, row_bytes)
-                                     : static_cast<size_t>(row) * row_bytes;
-            vw[g][q] = *reinterpret_cast<const uint32_t*>(Vg + off + v_lane_off);
-          }
+          for (int q = 0; q < 16; ++q) vw[g][q] = v_load(av[g], min(q0 + q, lcnt[g] - 1));
         }
       }
 #pragma unroll
       for (int g = 0; g < GH; ++g) {
-        if (lcnt[g] > q0) {
-#pragma unroll
-          for (int q = 0; q < 16; ++q) {
-            if (q0 + q < lcnt[g]) {
-              const float c = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(coefv[g]), q0 + q));
-              num0[g] = fmaf(c, lo16_to_f32<BF16>(vw[g][q]), num0[g]);
-              num1[g] = fmaf(c, hi16_to_f32<BF16>(vw[g][q]), num1[g]);
-            }
-          }
-        }
+        if (lcnt[g] > q0) accumulate(g, coefv[g], vw[g], q0, lcnt[g]);
       }
     }
 #pragma unroll
