@@ -1338,35 +1338,43 @@ __global__ __launch_bounds__(ROWS ? 512 : kThreads, ROWS ? 1 : 2) void wave_kern
       const __amdgpu_buffer_rsrc_t rs_v = __builtin_amdgcn_make_buffer_rsrc(
           const_cast<char*>(Vg), static_cast<short>(0), static_cast<int>(static_cast<uint32_t>(L_valid) * row_bytes),
           kBufferWord3);
+      // four heads at a time (GH 8: two such blocks, so that the 16 rows and
+      // coefficients in flight per head fit the registers)
       for (int q0 = 0; q0 < nmax; q0 += 16) {
-        uint32_t vw[GH][16];
-        float cw[GH][16];
 #pragma unroll
-        for (int g = 0; g < GH; ++g) {
-          if (lcnt[g] > q0) {
+        for (int hb = 0; hb < NHB; ++hb) {
+          uint32_t vw[4][16];
+          float cw[4][16];
 #pragma unroll
-            for (int p = 0; p < 8; ++p) {
-              const int4 e2 = *reinterpret_cast<const int4*>(&list[g * LCAP + q0 + 2 * p]);
-              cw[g][2 * p] = __int_as_float(e2.y);
-              cw[g][2 * p + 1] = __int_as_float(e2.w);
-              const uint32_t o0 = (q0 + 2 * p < lcnt[g]) ? __umul24(static_cast<uint32_t>(e2.x), row_bytes) + v_lane_off
-                                                          : 0xffffffffu;
-              const uint32_t o1 = (q0 + 2 * p + 1 < lcnt[g])
-                                      ? __umul24(static_cast<uint32_t>(e2.z), row_bytes) + v_lane_off
-                                      : 0xffffffffu;
-              vw[g][2 * p] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_raw_buffer_load_b32(rs_v, o0, 0, 0));
-              vw[g][2 * p + 1] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_raw_buffer_load_b32(rs_v, o1, 0, 0));
+          for (int k = 0; k < 4; ++k) {
+            const int g = 4 * hb + k;
+            if (lcnt[g] > q0) {
+#pragma unroll
+              for (int p = 0; p < 8; ++p) {
+                const int4 e2 = *reinterpret_cast<const int4*>(&list[g * LCAP + q0 + 2 * p]);
+                cw[k][2 * p] = __int_as_float(e2.y);
+                cw[k][2 * p + 1] = __int_as_float(e2.w);
+                const uint32_t o0 = (q0 + 2 * p < lcnt[g])
+                                        ? __umul24(static_cast<uint32_t>(e2.x), row_bytes) + v_lane_off
+                                        : 0xffffffffu;
+                const uint32_t o1 = (q0 + 2 * p + 1 < lcnt[g])
+                                        ? __umul24(static_cast<uint32_t>(e2.z), row_bytes) + v_lane_off
+                                        : 0xffffffffu;
+                vw[k][2 * p] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_raw_buffer_load_b32(rs_v, o0, 0, 0));
+                vw[k][2 * p + 1] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_raw_buffer_load_b32(rs_v, o1, 0, 0));
+              }
             }
           }
-        }
 #pragma unroll
-        for (int g = 0; g < GH; ++g) {
-          if (lcnt[g] > q0) {
+          for (int k = 0; k < 4; ++k) {
+            const int g = 4 * hb + k;
+            if (lcnt[g] > q0) {
 #pragma unroll
-            for (int q = 0; q < 16; ++q) {
-              if (q0 + q < lcnt[g]) {
-                num0[g] = fmaf(cw[g][q], lo16_to_f32<BF16>(vw[g][q]), num0[g]);
-                num1[g] = fmaf(cw[g][q], hi16_to_f32<BF16>(vw[g][q]), num1[g]);
+              for (int q = 0; q < 16; ++q) {
+                if (q0 + q < lcnt[g]) {
+                  num0[g] = fmaf(cw[k][q], lo16_to_f32<BF16>(vw[k][q]), num0[g]);
+                  num1[g] = fmaf(cw[k][q], hi16_to_f32<BF16>(vw[k][q]), num1[g]);
+                }
               }
             }
           }
