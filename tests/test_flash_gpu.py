@@ -234,6 +234,38 @@ def test_headline_workload_parity():
     assert ok, ("vs oracle", mabs, mrel)
 
 
+@pytest.mark.parametrize("B,H", [(8, 32), (4, 64)])
+def test_wave_kernel_full_lists_parity(B, H):
+    """The production wave kernel with a budget that fills the per-head sample
+    lists within every tile (L=32768, S=8192, so 64 samples per tile and
+    head): the lists are gathered mid-chunk many times and hold up to 64
+    entries at the chunk's end.  Tile max, tile mass and every count
+    bit-exact to the oracle, m* and vrows exact, the output within the bf16
+    tolerance (GH 4 and GH 8)."""
+    KVH, L, S = 8, 32768, 8192
+    _announce(f"full sample lists B={B} H={H} KVH={KVH} L={L} S={S} seed={SEED}")
+    m = _mod()
+    q, K, V = gen_qkv(B, H, KVH, L, seed=SEED + H, lowrank=0.5)
+    dev = torch.device("cuda:0")
+    qd, Kd, Vd = q.to(dev), K.to(dev), V.to(dev)
+    mt, lt, cnt = m._debug_wave(qd, Kd, Vd, S, seed=SEED, valid_len=-1)
+    out, ms, vr = m.decode_systematic_batched(qd, Kd, Vd, S, seed=SEED, want_vrows=True)
+    torch.cuda.synchronize()
+    exp = oracle.flash_decode(q, K, V, S, seed=SEED, block_n=256, is_bf16=True, debug=True)
+    np.testing.assert_array_equal(mt.cpu().numpy().view(np.uint32), exp["m_tiles"].view(np.uint32), err_msg="m_tiles")
+    np.testing.assert_array_equal(lt.cpu().numpy().view(np.uint32), exp["ell_tiles"].view(np.uint32),
+                                  err_msg="ell_tiles")
+    c_gpu = cnt.cpu().numpy()
+    assert np.array_equal(c_gpu, exp["counts"]), f"counts differ at {np.argwhere(c_gpu != exp['counts'])[:8]}"
+    # the lists do fill: more than 32 distinct rows per tile and head on
+    # average, so a chunk of two or more tiles overflows a 64-entry list
+    assert (c_gpu > 0).sum(-1).mean() > 32
+    np.testing.assert_array_equal(ms.cpu().numpy().view(np.uint32), exp["m_star"].view(np.uint32), err_msg="m_star")
+    np.testing.assert_array_equal(vr.cpu().numpy(), exp["vrows"], err_msg="vrows")
+    ok, mabs, mrel = tol_check(h16_to_f32(bits16(out)), h16_to_f32(exp["out16"]))
+    assert ok, ("vs oracle", mabs, mrel)
+
+
 def test_cfg5_shape_parity():
     """cfg5's per-sequence shape and key recipe (64q/8kv so GH 8, L=131072,
     S=512, Student-t(3) keys with planted needles, bench.device_inputs) on 4

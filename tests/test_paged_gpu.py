@@ -170,6 +170,31 @@ def test_flash_paged_wave_kernel_against_oracle(H, S, page_size):
 
 
 @pytest.mark.parametrize("H,page_size", [(32, 16), (64, 256)])
+def test_flash_paged_full_lists_against_oracle(H, page_size):
+    """The paged wave kernel with a budget that fills the per-head sample lists
+    within every tile (64 samples per tile and head over lengths in
+    [16384, 32768]): the lists are gathered through the page table mid-chunk
+    and at the chunk's end.  Bit-identical to the contiguous ragged call;
+    every sequence's m* and vrows exact against the oracle, its output within
+    the bf16 tolerance."""
+    import santa_flash_batch_cuda as m
+
+    lens = seeded_lens(4, 16384, 32768, SEED + 7 * H + page_size)
+    assert sum((l + 255) // 256 for l in lens) * 8 > 2048
+    S = 64 * max((l + 255) // 256 for l in lens)
+    seed = SEED + 17 * H + page_size
+    print(f"\n[case] flash paged full lists vs oracle H={H} lens={lens} S={S} page_size={page_size} seed={seed}",
+          flush=True)
+    q, K, V, Kp, Vp, table = _inputs(len(lens), H, 8, lens, page_size, torch.bfloat16, seed)
+    got = m.decode_systematic_paged(q, Kp, Vp, table, lens, S, seed=SEED, want_vrows=True)
+    ref = m.decode_systematic_batched(q, K, V, S, seed=SEED, want_vrows=True, valid_len=lens)
+    torch.cuda.synchronize()
+    _check(got, ref, True, True, "paged vs contiguous")
+    _oracle_checks(got, q, K, V, lens, "flash paged",
+                   lambda qc, Kc, Vc, b, Lb: flash_oracle_sequence(qc, Kc, Vc, b, Lb, S, 256))
+
+
+@pytest.mark.parametrize("H,page_size", [(32, 16), (64, 256)])
 def test_prop_paged_against_oracle(H, page_size, monkeypatch):
     """Paged batched santa_prop on lengths in [9000, 40000] with S_b = L_b // 64
     (GH 4: the vec pass 1 on the wave kernel; GH 8: the general pass 1):
