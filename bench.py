@@ -236,6 +236,10 @@ class Timing:
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         torch.cuda.synchronize()
         t0 = time.perf_counter()
+        # one untimed call keeps the GPU busy while the timed ones are submitted:
+        # e0 then fires when it ends and the window holds the n calls back to
+        # back, without the host's latency to its first launch
+        fn()
         e0.record(stream)
         for _ in range(n):
             fn()
