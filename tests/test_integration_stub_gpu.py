@@ -1,11 +1,14 @@
-"""The ctypes binding that INTEGRATION.md shows a maintainer (section 3) runs
-as written and gives the extension module's results.
+"""The ctypes binding of santa_flash_decode that the repository's integration
+notes give a maintainer runs as written and gives the extension module's
+results.
 
-The test reads the stub's code block from INTEGRATION.md itself, so the
-document and the tested code cannot drift apart, executes it from the
-repository root (its library path is relative), and compares its
-decode_systematic_batched with santa_flash_batch_cuda's on the same inputs:
-out, m* and vrows bit-identical (the same launches through the C ABI).
+The test reads the stub's code block from the notes themselves (the one
+python block that loads the library with ctypes and calls
+santa_flash_decode), so the document and the tested code cannot drift apart,
+executes it from the repository root (its library path is relative), and
+compares its decode_systematic_batched with santa_flash_batch_cuda's on the
+same inputs: out, m* and vrows bit-identical (the same launches through the
+C ABI).
 """
 import os
 import re
@@ -26,7 +29,7 @@ def _stub_source():
         text = f.read()
     blocks = re.findall(r"```python\n(.*?)```", text, flags=re.S)
     stubs = [b for b in blocks if "ctypes.CDLL" in b and "santa_flash_decode" in b]
-    assert len(stubs) == 1, "INTEGRATION.md must hold exactly one ctypes stub of santa_flash_decode"
+    assert len(stubs) == 1, "the integration notes must hold exactly one ctypes stub of santa_flash_decode"
     return stubs[0]
 
 
@@ -34,7 +37,7 @@ def _stub_source():
 def test_ctypes_stub_matches_extension(B, L, S, valid_len, monkeypatch):
     import santa_flash_batch_cuda as flash
 
-    print(f"\n[case] INTEGRATION.md ctypes stub B={B} L={L} S={S} valid_len={valid_len}", flush=True)
+    print(f"\n[case] integration-notes ctypes stub B={B} L={L} S={S} valid_len={valid_len}", flush=True)
     monkeypatch.chdir(REPO)
     ns = {}
     exec(compile(_stub_source(), "INTEGRATION.md", "exec"), ns)
