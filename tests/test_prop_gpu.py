@@ -175,3 +175,46 @@ def test_prop_more_than_4096_tiles(H, KVH, D, L, block_n, monkeypatch):
     q, K, V = _general_inputs(H, KVH, D, L, SEED + L)
     exp = _check(q, K, V, L // 50, SEED, block_n=block_n, monkeypatch=monkeypatch)
     assert exp["T_c"] == 4375
+
+
+def test_prop_unbiased_given_budgets_at_full_size():
+    """santa_prop on one sequence of 32768 tokens (32q/8kv, S = L / 64 = 512,
+    the rank-4 key bias recipe) through the production call.  Its output is
+    sum_r c_r v_r / S with integer tile budgets S_t from the largest-remainder
+    allocation, so it estimates sum_t (S_t / S) o_t rather than exact
+    attention; given the budgets, the systematic sampler's expected count of
+    row r is x_r = f32(u16_r) * invdelta_t.  The output averaged over 2048
+    seeds agrees with sum_r x_r v_r / S (budgets and u16 from the debug call)
+    within 6 standard errors of the mean in every element (plus 0.4 % of the
+    value for the bf16 rounding of each output), and the same criterion
+    rejects that expectation scaled by 1.1."""
+    import santa_prop_batch_cuda as m
+
+    H, KVH, L, D, BN = 32, 8, 32768, 128, 256
+    S = L // 64
+    n = 2048
+    print(f"\n[case] prop unbiased given budgets over {n} seeds H={H} KVH={KVH} L={L} S={S}", flush=True)
+    q, K, V = gen_qkv(1, H, KVH, L, seed=SEED + 23, lowrank=0.5)
+    dev = torch.device("cuda:0")
+    qd, Kd, Vd = q[0].to(dev), K[0].to(dev), V[0].to(dev)
+    dbg = m._debug_pass(qd, Kd, Vd, S, seed=0)
+    invdelta, stash = dbg[4], dbg[6]  # [H, T_c], [L, H]
+    x = stash.float().t() * invdelta.repeat_interleave(BN, dim=1)[:, :L]  # [H, L]
+    GH = H // KVH
+    Vf = Vd.float()  # [L, KVH, D]
+    expected = torch.stack([x[h] @ Vf[:, h // GH, :] for h in range(H)]) / S  # [H, D]
+    acc = torch.zeros(H, D, dtype=torch.float64, device=dev)
+    acc2 = torch.zeros(H, D, dtype=torch.float64, device=dev)
+    for sd in range(n):
+        out, _, _ = m.decode_systematic_scalar(qd, Kd, Vd, S, seed=sd)
+        o = out.double()
+        acc += o
+        acc2 += o * o
+    mean = acc / n
+    se = ((acc2 / n - mean * mean).clamp_min(0.0) / n).sqrt()
+    ex = expected.double()
+    floor = 4e-3 * ex.abs() + 1e-6
+    zs = {f: ((mean - (1.0 + f) * ex).abs() / (se + floor)).max().item() for f in (0.0, 0.02, 0.05, 0.1, 0.2)}
+    print("[case] z for a scale error of " + ", ".join(f"{f:.0%}: {v:.2f}" for f, v in zs.items()), flush=True)
+    assert zs[0.0] < 6.0, zs
+    assert zs[0.1] > 6.0, zs
