@@ -236,10 +236,12 @@ class Timing:
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         torch.cuda.synchronize()
         t0 = time.perf_counter()
-        # one untimed call keeps the GPU busy while the timed ones are submitted:
-        # e0 then fires when it ends and the window holds the n calls back to
-        # back, without the host's latency to its first launch
-        fn()
+        # three untimed calls keep the GPU busy (and at its working clocks)
+        # while the timed ones are submitted: e0 then fires when they end and
+        # the window holds the n calls back to back, without the host's latency
+        # to its first launch
+        for _ in range(3):
+            fn()
         e0.record(stream)
         for _ in range(n):
             fn()

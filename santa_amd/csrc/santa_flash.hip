@@ -1951,8 +1951,8 @@ static hipError_t launch_merge(const float* part, const int* pe, int dtype, int 
   uint16_t* o = static_cast<uint16_t*>(out);
   const int max_chunks = seq_lens ? ((max_len + bn - 1) / bn + cs - 1) / cs : cpg;
   if (max_chunks <= 64) {
-    // one wave per (b, h) up to 16 chunks, else two or four waves of 16
-    // chunks each (B = 1 at 32k, 64 chunks: step 24.7 -> 23.4 us)
+    // one wave per (b, h) up to 32 chunks, else four waves of 16 chunks
+    // each (B = 1 at 32k, 64 chunks: step 24.7 -> 23.6 us)
 #define SANTA_MERGE_WAVE(BF, G, NBC)                                                                          \
   hipLaunchKernelGGL((merge_wave_kernel<BF, G, NBC>), dim3(grid), dim3(64), 0, stream, part, pe, H, KVH, cpg, \
                      S_pt, o, m_star, vrows, seq_lens, bn, cs, max_len, n_wg, S_total)
@@ -1963,7 +1963,7 @@ static hipError_t launch_merge(const float* part, const int* pe, int dtype, int 
   if (max_chunks <= 16)                 \
     SANTA_MERGE_WAVE(BF, G, 16);        \
   else if (max_chunks <= 32)            \
-    SANTA_MERGE_SPLIT(BF, G, 2);        \
+    SANTA_MERGE_WAVE(BF, G, 32);        \
   else                                  \
     SANTA_MERGE_SPLIT(BF, G, 4)
     if (dtype == SANTA_BF16) {
