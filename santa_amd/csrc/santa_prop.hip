@@ -58,7 +58,7 @@ constexpr int kMaxTiles = 4096;  // budgets: 16 waves x 4 registers x 64 lanes
 
 // The value of lane (lane ^ J): DPP inside 16-lane rows (quad permutes for
 // 1 and 2; row shifts up or down for 4 and 8, picked by the lane's bit J),
-// an LDS permute across rows.
+// the row and half-wave swaps for 16 and 32 (no LDS round trip).
 template <int J>
 __device__ __forceinline__ int lane_xor(int v, int lane) {
   if constexpr (J == 1) {
@@ -69,9 +69,39 @@ __device__ __forceinline__ int lane_xor(int v, int lane) {
     const int from_above = __builtin_amdgcn_update_dpp(0, v, 0x100 + J, 0xF, 0xF, true);  // lane + J
     const int from_below = __builtin_amdgcn_update_dpp(0, v, 0x110 + J, 0xF, 0xF, true);  // lane - J
     return (lane & J) ? from_below : from_above;
+  } else if constexpr (J == 16) {
+    // the swap of the odd rows of its first operand with the even rows of its
+    // second (both v) leaves rows (0, 0, 2, 2) in the first result and
+    // (1, 1, 3, 3) in the second: even rows take the second, odd the first
+    const auto s = __builtin_amdgcn_permlane16_swap(static_cast<unsigned>(v), static_cast<unsigned>(v), false, false);
+    return static_cast<int>((lane & 16) ? s[0] : s[1]);
   } else {
-    return __shfl_xor(v, J, 64);
+    static_assert(J == 32, "lane_xor: J is a power of two below 64");
+    // the swap of the upper half of its first operand with the lower half of
+    // its second (both v) leaves (lo, lo) in the first result and (hi, hi) in
+    // the second: the lower half takes the second, the upper the first
+    const auto s = __builtin_amdgcn_permlane32_swap(static_cast<unsigned>(v), static_cast<unsigned>(v), false, false);
+    return static_cast<int>((lane & 32) ? s[0] : s[1]);
   }
+}
+
+// Butterfly reductions over the wave through lane_xor (every lane gets the
+// result): maximum of floats, sum of ints (both exact in any order).
+__device__ __forceinline__ float wave_max_xor(float v, int lane) {
+  v = fmaxf(v, __int_as_float(lane_xor<32>(__float_as_int(v), lane)));
+  v = fmaxf(v, __int_as_float(lane_xor<16>(__float_as_int(v), lane)));
+  v = fmaxf(v, __int_as_float(lane_xor<8>(__float_as_int(v), lane)));
+  v = fmaxf(v, __int_as_float(lane_xor<4>(__float_as_int(v), lane)));
+  v = fmaxf(v, __int_as_float(lane_xor<2>(__float_as_int(v), lane)));
+  return fmaxf(v, __int_as_float(lane_xor<1>(__float_as_int(v), lane)));
+}
+__device__ __forceinline__ int wave_sum_xor(int v, int lane) {
+  v += lane_xor<32>(v, lane);
+  v += lane_xor<16>(v, lane);
+  v += lane_xor<8>(v, lane);
+  v += lane_xor<4>(v, lane);
+  v += lane_xor<2>(v, lane);
+  return v + lane_xor<1>(v, lane);
 }
 
 // One compare-exchange step given each element's partner value (of, oi):
@@ -207,8 +237,7 @@ __global__ __launch_bounds__(64 * NW) void budgets_kernel(const float* __restric
 #pragma unroll
   for (int r = 0; r < R; ++r)
     if (NT * r + tid < T_c) ms = fmaxf(ms, mv[r]);
-#pragma unroll
-  for (int s = 32; s > 0; s >>= 1) ms = fmaxf(ms, __shfl_xor(ms, s, 64));
+  ms = wave_max_xor(ms, lane);
   if (lane == 0) s_red[wv] = ms;
   __syncthreads();
   ms = s_red[0];
@@ -236,8 +265,14 @@ __global__ __launch_bounds__(64 * NW) void budgets_kernel(const float* __restric
   __syncthreads();
   if (wv == 0) {
     float z = s_z[lane] + s_z[lane + 64];
-#pragma unroll
-    for (int s = 32; s > 0; s >>= 1) z = z + __shfl_down(z, s, 64);
+    // the tree z[i] += z[i + s] for s = 32 .. 1: for the lanes below s that
+    // it reads, lane ^ s is lane + s, so lane 0 ends with the same sum
+    z = z + __int_as_float(lane_xor<32>(__float_as_int(z), lane));
+    z = z + __int_as_float(lane_xor<16>(__float_as_int(z), lane));
+    z = z + __int_as_float(lane_xor<8>(__float_as_int(z), lane));
+    z = z + __int_as_float(lane_xor<4>(__float_as_int(z), lane));
+    z = z + __int_as_float(lane_xor<2>(__float_as_int(z), lane));
+    z = z + __int_as_float(lane_xor<1>(__float_as_int(z), lane));
     if (lane == 0) s_z[0] = z;
   }
   __syncthreads();
@@ -280,8 +315,7 @@ __global__ __launch_bounds__(64 * NW) void budgets_kernel(const float* __restric
       id[r] = t;
     }
   }
-#pragma unroll
-  for (int s = 32; s > 0; s >>= 1) base += __shfl_xor(base, s, 64);
+  base = wave_sum_xor(base, lane);
   if (lane == 0) s_ired[wv] = base;
   __syncthreads();
   base = 0;
