@@ -700,12 +700,18 @@ __global__ __launch_bounds__(kThreads, 2) void tile_kernel(
 // are merged in wave order at the end of the chunk.
 constexpr int kWaveListCap = 64;  // listed rows per head (one per lane)
 
+// The value of lane i + 16 in the even 16-lane rows (rows 0, 2; the odd rows
+// get their own value back): the second result of the row swap of v with
+// itself.  The callers read it in the even rows only.
 template <int N>
-__device__ __forceinline__ float xrow16(float v) {  // rows 0<->1, 2<->3
+__device__ __forceinline__ float xrow16(float v) {
   const auto s = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
   return __uint_as_float(s[1]);
 }
-__device__ __forceinline__ float xhalf32(float v) {  // lanes i <-> i + 32
+// The value of lane i + 32 in lanes 0..31 (lanes 32..63 get their own value
+// back): the second result of the half-wave swap of v with itself.  The
+// callers read it in lanes 0..31 only.
+__device__ __forceinline__ float xhalf32(float v) {
   const auto s = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
   return __uint_as_float(s[1]);
 }
