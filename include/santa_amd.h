@@ -243,12 +243,20 @@ int santa_prop_decode_paged(const void* q, const void* K_pages, const void* V_pa
  * [B, storage, KVH, D]; RoPE in the rotate-half convention with cos, sin
  * [D] and bf16 rounding of each product and of the sum.
  * santa_rt_silu_mul: out [rows, inter] = bf16(bf16(silu(gate)) * up), gate
- * and up the two halves of gu [rows, 2 inter]. */
+ * and up the two halves of gu [rows, 2 inter].
+ * santa_rt_linear: the decode step's weight products (the HF layers'
+ * nn.Linear, bf16, no bias): y [M, N] = bf16(x [M, K] . w [N, K]^T),
+ * float32 accumulation, for 1 <= M <= 8, K a multiple of 8, M rounded up to
+ * 1, 2, 4 or 8 times K rounded up to 2048 at most 65536, x and w 16-byte
+ * aligned.  swiglu != 0: w is [2N, K] (gate rows, then up rows) and
+ * y [M, N] = bf16(bf16(silu(bf16(g))) * bf16(u)), silu_mul of the product.
+ * The weights are read once at the HBM bound. */
 int santa_rt_add_rms_norm(void* h, const void* a, const void* w, void* x, int rows, int hidden, float eps,
                           hipStream_t stream);
 int santa_rt_rope_write(const void* qkv, const void* cos_, const void* sin_, void* q_out, void* k_cache, void* v_cache,
                         int B, int H, int KVH, int D, long long storage, int pos, hipStream_t stream);
 int santa_rt_silu_mul(const void* gu, void* out, int rows, int inter, hipStream_t stream);
+int santa_rt_linear(const void* x, const void* w, void* y, int M, int N, int K, int swiglu, hipStream_t stream);
 
 #ifdef __cplusplus
 }

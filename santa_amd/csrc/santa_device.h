@@ -457,4 +457,33 @@ __device__ __forceinline__ float tree32(float* v) {
   return v[0];
 }
 
+// The value of lane (lane ^ J): DPP inside 16-lane rows (quad permutes for
+// 1 and 2; row shifts up or down for 4 and 8, picked by the lane's bit J),
+// the row and half-wave swaps for 16 and 32 (no LDS round trip).
+template <int J>
+__device__ __forceinline__ int lane_xor(int v, int lane) {
+  if constexpr (J == 1) {
+    return __builtin_amdgcn_update_dpp(0, v, kDppQuadXor1, 0xF, 0xF, false);
+  } else if constexpr (J == 2) {
+    return __builtin_amdgcn_update_dpp(0, v, kDppQuadXor2, 0xF, 0xF, false);
+  } else if constexpr (J == 4 || J == 8) {
+    const int from_above = __builtin_amdgcn_update_dpp(0, v, 0x100 + J, 0xF, 0xF, true);  // lane + J
+    const int from_below = __builtin_amdgcn_update_dpp(0, v, 0x110 + J, 0xF, 0xF, true);  // lane - J
+    return (lane & J) ? from_below : from_above;
+  } else if constexpr (J == 16) {
+    // the swap of the odd rows of its first operand with the even rows of its
+    // second (both v) leaves rows (0, 0, 2, 2) in the first result and
+    // (1, 1, 3, 3) in the second: even rows take the second, odd the first
+    const auto s = __builtin_amdgcn_permlane16_swap(static_cast<unsigned>(v), static_cast<unsigned>(v), false, false);
+    return static_cast<int>((lane & 16) ? s[0] : s[1]);
+  } else {
+    static_assert(J == 32, "lane_xor: J is a power of two below 64");
+    // the swap of the upper half of its first operand with the lower half of
+    // its second (both v) leaves (lo, lo) in the first result and (hi, hi) in
+    // the second: the lower half takes the second, the upper the first
+    const auto s = __builtin_amdgcn_permlane32_swap(static_cast<unsigned>(v), static_cast<unsigned>(v), false, false);
+    return static_cast<int>((lane & 32) ? s[0] : s[1]);
+  }
+}
+
 }  // namespace santa

@@ -103,6 +103,200 @@ __global__ __launch_bounds__(256) void silu_mul_kernel(const uint16_t* __restric
   out[i] = to_bf(s * u);
 }
 
+// ------------------------------------------------------------------ linear
+// y[M, N] = bf16(x[M, K] . W[N, K]^T) for the decode step's few rows
+// (M <= 8): the weights are read from HBM once, so the product runs at the
+// HBM bound, not on matrix cores.  A workgroup of 16 waves per CU stages x
+// (zero-padded to MP rows and Kp columns) in LDS once; then each wave streams
+// pairs of weight rows, 16 bytes per lane per 512-column segment, four
+// segments (a "chunk" of 2048 columns) per row at a time, with two such
+// units in flight while one is multiplied (v_dot2 with float32
+// accumulation).  At the end of a row pair the wave's M x 2 partial sums are
+// reduced across the 64 lanes by halving exchanges, so each output ends in
+// one lane.  Rows beyond N and columns beyond K read as zero through the
+// buffer descriptors' range checks.
+// SWIGLU: W holds 2N rows (gate rows, then up rows); the pair of wave rows is
+// (n, n + N) and the output is bf16(bf16(silu(g)) * u) with g and u rounded to
+// bf16 first, the roundings of silu_mul_kernel after a bf16 product.
+constexpr int kLinWaves = 16;
+constexpr int kLinThreads = kLinWaves * 64;
+constexpr int kLinSeg = 512;                // columns per wave-wide 16-byte load
+constexpr int kLinChunkSegs = 4;            // segments per row loaded at once
+constexpr int kLinChunk = kLinSeg * kLinChunkSegs;
+constexpr int kLinLdsVecs = 8192;           // 16-byte LDS slots: MP * Kp <= 65536
+constexpr int kBufWord3 = 0x00020000;       // raw buffer descriptor, gfx9 family
+constexpr int kBufNontemporal = 2;
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+
+// Eight bf16 products summed into acc, two per v_dot2 (the whole vector is
+// reinterpreted, then split into pairs: a bit cast of one 32-bit component
+// of a vector lvalue has been seen to read the first component instead).
+__device__ __forceinline__ float dot8(const u32x4 a, const u32x4 b, float acc) {
+  const bf16x8 av = __builtin_bit_cast(bf16x8, a), bv = __builtin_bit_cast(bf16x8, b);
+  acc = __builtin_amdgcn_fdot2_f32_bf16(av.s01, bv.s01, acc, false);
+  acc = __builtin_amdgcn_fdot2_f32_bf16(av.s23, bv.s23, acc, false);
+  acc = __builtin_amdgcn_fdot2_f32_bf16(av.s45, bv.s45, acc, false);
+  return __builtin_amdgcn_fdot2_f32_bf16(av.s67, bv.s67, acc, false);
+}
+
+template <int J>
+__device__ __forceinline__ float fxor(float v, int lane) {
+  return __int_as_float(lane_xor<J>(__float_as_int(v), lane));
+}
+
+// Sums of V per-lane values over the wave, each ending in its own lanes.
+// Halving exchanges at distance D = 32, 16, ...: both lanes of a pair add
+// the pair's copies of both halves and keep the half their bit D selects
+// (upper for the lane with the bit set), so after log2(V) steps the lane's
+// element 0 is index lane >> (6 - log2 V); the remaining distances then sum
+// it over the other lanes.  Every index goes through the same tree of
+// lanes, so a value's sum does not depend on its index.
+template <int V, int D, typename T>
+__device__ __forceinline__ void lane_reduce(T& acc, int lane) {
+  if constexpr (V > 1) {
+    constexpr int H = V / 2;
+    const bool hi = (lane & D) != 0;
+#pragma unroll
+    for (int i = 0; i < H; ++i) {
+      const float lo = acc[i] + fxor<D>(acc[i], lane);
+      const float up = acc[i + H] + fxor<D>(acc[i + H], lane);
+      acc[i] = hi ? up : lo;
+    }
+    lane_reduce<H, D / 2>(acc, lane);
+  } else if constexpr (D >= 1) {
+    acc[0] += fxor<D>(acc[0], lane);
+    lane_reduce<1, D / 2>(acc, lane);
+  }
+}
+
+template <int MP, bool SWIGLU>
+__global__ __launch_bounds__(kLinThreads, 1) void linear_kernel(const uint16_t* __restrict__ x,
+                                                                const uint16_t* __restrict__ W,
+                                                                uint16_t* __restrict__ y, int M, int N, int K, int Kp,
+                                                                int nbatch) {
+  __shared__ u32x4 xs[kLinLdsVecs];
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int kv = Kp / 8;  // LDS slots per x row
+  const int nch = Kp / kLinChunk;
+  const int stride = gridDim.x * kLinWaves;
+  const int rows_total = SWIGLU ? 2 * N : N;
+  const uint32_t row_bytes = static_cast<uint32_t>(K) * 2u;
+
+  // the wave's batches (row pairs): wave * grid + block, then every stride
+  int b = wave * gridDim.x + blockIdx.x;
+  auto rows_of = [&](int bb, int& r0, int& r1) {
+    if constexpr (SWIGLU) {
+      r0 = bb;
+      r1 = bb + N;
+    } else {
+      r0 = 2 * bb;
+      r1 = 2 * bb + 1;
+    }
+  };
+  // Loads of chunk c of pair bb; a pair past the last (bb >= nbatch) or a
+  // row past the weight reads zeros without touching memory, so every unit
+  // issues the same number of loads.
+  auto issue = [&](int bb, int c, u32x4 (&w0)[kLinChunkSegs], u32x4 (&w1)[kLinChunkSegs]) {
+    int r0, r1;
+    rows_of(bb, r0, r1);
+    const bool ok0 = bb < nbatch && r0 < rows_total, ok1 = bb < nbatch && r1 < rows_total;
+    const __amdgpu_buffer_rsrc_t rs0 = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint16_t*>(W) + (ok0 ? static_cast<size_t>(r0) * K : 0), (short)0, ok0 ? (int)row_bytes : 0,
+        kBufWord3);
+    const __amdgpu_buffer_rsrc_t rs1 = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint16_t*>(W) + (ok1 ? static_cast<size_t>(r1) * K : 0), (short)0, ok1 ? (int)row_bytes : 0,
+        kBufWord3);
+    const int off = (c * kLinChunk + lane * 8) * 2;
+#pragma unroll
+    for (int s = 0; s < kLinChunkSegs; ++s) {
+      w0[s] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rs0, off + s * kLinSeg * 2, 0,
+                                                                              kBufNontemporal));
+      w1[s] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rs1, off + s * kLinSeg * 2, 0,
+                                                                              kBufNontemporal));
+    }
+  };
+
+  // (b, c): the unit multiplied next; (ib, ic): the next unit to load
+  int c = 0, ib = b, ic = 0;
+  auto advance = [&](int& bb, int& cc) {
+    if (cc + 1 < nch) {
+      ++cc;
+    } else {
+      cc = 0;
+      bb += stride;
+    }
+  };
+  // the wave's first two units of weights go out before x is staged, so the
+  // wait for x overlaps their latency
+  u32x4 wa[kLinChunkSegs], wb[kLinChunkSegs], wc[kLinChunkSegs], wd[kLinChunkSegs];
+  issue(ib, ic, wa, wb);
+  advance(ib, ic);
+  issue(ib, ic, wc, wd);
+  advance(ib, ic);
+  for (int i = threadIdx.x; i < MP * kv; i += kLinThreads) {
+    const int m = i / kv, j = i - m * kv;
+    u32x4 v = {0u, 0u, 0u, 0u};
+    if (m < M && j < K / 8) v = *reinterpret_cast<const u32x4*>(x + static_cast<size_t>(m) * K + 8 * j);
+    xs[i] = v;
+  }
+  __syncthreads();
+
+  constexpr int V = 2 * MP;  // partial sums per lane: (m, row of the pair)
+  constexpr int LOGV = V == 2 ? 1 : V == 4 ? 2 : V == 8 ? 3 : 4;
+  // a vector value, not an array: the exchanges below select between two
+  // of its elements, which on an array the compiler may turn into a select
+  // of addresses and place the array in LDS
+  typedef float accv_t __attribute__((ext_vector_type(V)));
+  accv_t acc = {};
+  // Multiplies the unit (b, c) held in cur (and at the end of a pair
+  // reduces and stores its sums), then loads the unit two ahead into cur;
+  // false when no unit is left.  The loop alternates two register
+  // sets, so two units are in flight and a load never waits for the
+  // registers it fills.
+  auto step = [&](u32x4 (&cura)[kLinChunkSegs], u32x4 (&curb)[kLinChunkSegs]) -> bool {
+    if (b >= nbatch) return false;
+    const u32x4* xc = xs + c * (kLinChunk / 8) + lane;
+#pragma unroll
+    for (int s = 0; s < kLinChunkSegs; ++s) {
+#pragma unroll
+      for (int m = 0; m < MP; ++m) {
+        const u32x4 xv = xc[m * kv + s * (kLinSeg / 8)];
+        acc[2 * m] = dot8(xv, cura[s], acc[2 * m]);
+        acc[2 * m + 1] = dot8(xv, curb[s], acc[2 * m + 1]);
+      }
+    }
+    if (c + 1 == nch) {
+      lane_reduce<V, 32>(acc, lane);
+      const int idx = lane >> (6 - LOGV);
+      const int m = idx >> 1;
+      const bool lead = (lane & ((64 >> LOGV) - 1)) == 0;
+      int r0, r1;
+      rows_of(b, r0, r1);
+      if constexpr (SWIGLU) {
+        const float u = fxor<(64 >> LOGV)>(acc[0], lane);  // the (m, up) sum
+        if (lead && (idx & 1) == 0 && m < M) {
+          const float g = bf(to_bf(acc[0]));
+          const float sg = bf(to_bf(g / (1.0f + expf(-g))));
+          y[static_cast<size_t>(m) * N + r0] = to_bf(sg * bf(to_bf(u)));
+        }
+      } else {
+        const int r = (idx & 1) ? r1 : r0;
+        if (lead && m < M && r < N) y[static_cast<size_t>(m) * N + r] = to_bf(acc[0]);
+      }
+      acc = accv_t{};
+    }
+    issue(ib, ic, cura, curb);
+    advance(ib, ic);
+    advance(b, c);
+    return true;
+  };
+  while (step(wa, wb) && step(wc, wd)) {
+  }
+}
+
 }  // namespace rt
 }  // namespace santa
 
@@ -134,6 +328,50 @@ extern "C" int santa_rt_rope_write(const void* qkv, const void* cos_, const void
                      B, H, KVH, D, storage, pos);
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess) return set_error(SANTA_ERR_HIP, "rope_write launch failed: %s", hipGetErrorString(e));
+  return clear_error();
+}
+
+extern "C" int santa_rt_linear(const void* x, const void* w, void* y, int M, int N, int K, int swiglu,
+                               hipStream_t stream) {
+  if (!x || !w || !y || M < 1 || M > 8 || N <= 0 || K <= 0 || K % 8 != 0 ||
+      (reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(w)) % 16 != 0)
+    return set_error(SANTA_ERR_INVALID, "bad linear arguments (M in 1..8, K a multiple of 8, x and w 16-byte aligned)");
+  const int MP = M <= 1 ? 1 : M <= 2 ? 2 : M <= 4 ? 4 : 8;
+  const long long Kp = (static_cast<long long>(K) + rt::kLinChunk - 1) / rt::kLinChunk * rt::kLinChunk;
+  if (MP * Kp / 8 > rt::kLinLdsVecs)
+    return set_error(SANTA_ERR_INVALID, "linear: M x K too large for the staged rows (M rounded up to 1, 2, 4 or 8, "
+                                        "times K rounded up to 2048, at most 65536)");
+  if (static_cast<long long>(swiglu ? 2 : 1) * N * K * 2 > 0x7fffffffffffLL)
+    return set_error(SANTA_ERR_INVALID, "linear: weight too large");
+  const int nbatch = swiglu ? N : (N + 1) / 2;
+  static int cached_dev = -1, cus = 256;
+  int dev = 0;
+  if (hipGetDevice(&dev) == hipSuccess && dev != cached_dev) {
+    int c = 0;
+    cus = (hipDeviceGetAttribute(&c, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && c > 0) ? c : 256;
+    cached_dev = dev;
+  }
+  const unsigned grid = static_cast<unsigned>(nbatch < cus ? nbatch : cus);
+  const uint16_t* xp = static_cast<const uint16_t*>(x);
+  const uint16_t* wp = static_cast<const uint16_t*>(w);
+  uint16_t* yp = static_cast<uint16_t*>(y);
+  const int kp = static_cast<int>(Kp);
+#define SANTA_LIN(MPV)                                                                                              \
+  if (swiglu)                                                                                                       \
+    hipLaunchKernelGGL((rt::linear_kernel<MPV, true>), dim3(grid), dim3(rt::kLinThreads), 0, stream, xp, wp, yp, M, \
+                       N, K, kp, nbatch);                                                                           \
+  else                                                                                                              \
+    hipLaunchKernelGGL((rt::linear_kernel<MPV, false>), dim3(grid), dim3(rt::kLinThreads), 0, stream, xp, wp, yp,  \
+                       M, N, K, kp, nbatch);
+  switch (MP) {
+    case 1: SANTA_LIN(1) break;
+    case 2: SANTA_LIN(2) break;
+    case 4: SANTA_LIN(4) break;
+    default: SANTA_LIN(8) break;
+  }
+#undef SANTA_LIN
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return set_error(SANTA_ERR_HIP, "linear launch failed: %s", hipGetErrorString(e));
   return clear_error();
 }
 

@@ -83,6 +83,7 @@ class _FusedOps:
                 ctypes.c_longlong, ctypes.c_int, ctypes.c_void_p]
             L.santa_rt_silu_mul.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int, ctypes.c_int,
                                             ctypes.c_void_p]
+            L.santa_rt_linear.argtypes = [ctypes.c_void_p] * 3 + [ctypes.c_int] * 4 + [ctypes.c_void_p]
             cls._lib = L
         return cls._lib
 
@@ -117,6 +118,31 @@ class _FusedOps:
                                                  kc.data_ptr(), vc.data_ptr(), B, heads, kv_heads, head_dim,
                                                  kc.shape[1], pos, cls._stream(qkv)))
         return q
+
+    @staticmethod
+    def linear_fits(rows: int, K: int) -> bool:
+        """Whether santa_rt_linear takes x [rows, K]: rows <= 8, K a multiple
+        of 8, rows rounded up to 1, 2, 4 or 8 times K rounded up to 2048 at
+        most 65536 (the x rows it stages in LDS)."""
+        mp = 1 if rows <= 1 else 2 if rows <= 2 else 4 if rows <= 4 else 8
+        return 1 <= rows <= 8 and K % 8 == 0 and mp * (-(-K // 2048) * 2048) <= 65536
+
+    @classmethod
+    def linear(cls, x: torch.Tensor, w: torch.Tensor, *, swiglu: bool = False) -> torch.Tensor:
+        """bf16(x @ w.T) for few rows of x (santa_rt_linear; F.linear where
+        the shape does not fit it).  swiglu: w holds the gate rows then the up
+        rows, and the result is silu_mul of the product, in silu_mul's
+        roundings."""
+        rows, K = x.numel() // x.shape[-1], x.shape[-1]
+        if not (cls.linear_fits(rows, K) and x.dtype == torch.bfloat16 and w.dtype == torch.bfloat16
+                and x.is_contiguous() and w.is_contiguous() and x.data_ptr() % 16 == 0 and w.data_ptr() % 16 == 0):
+            y = F.linear(x, w)
+            return cls.silu_mul(y) if swiglu else y
+        N = w.shape[0] // 2 if swiglu else w.shape[0]
+        y = torch.empty(*x.shape[:-1], N, dtype=x.dtype, device=x.device)
+        cls._check(cls.lib().santa_rt_linear(x.data_ptr(), w.data_ptr(), y.data_ptr(), rows, N, K, int(swiglu),
+                                             cls._stream(x)))
+        return y
 
     @classmethod
     def silu_mul(cls, gu: torch.Tensor) -> torch.Tensor:
@@ -329,24 +355,26 @@ class RandomLlama:
         return F.linear(_rms_norm(h, self.norm, s.rms_eps), self.lm_head).float()
 
     def _decode_step_fused(self, h, cos, sin, pos, cache, backend):
-        """decode_step on the GPU: per layer four fused kernels (add + norm
-        twice, RoPE with the cache write, SwiGLU) around the four weight
-        products and the backend's attention; the same arithmetic as the
-        torch expressions, in the torch expressions' bf16 roundings."""
+        """decode_step on the GPU: per layer the four weight products as
+        santa_rt_linear (the gate/up product with SwiGLU in its epilogue), two
+        fused add + norm kernels and RoPE with the cache write, around the
+        backend's attention; the torch expressions' arithmetic and bf16
+        roundings, with each product accumulated in float32 in its own order."""
         s, D = self.shape, self.shape.head_dim
         B = h.shape[0]
         h = h.contiguous()
         x = _FusedOps.add_rms_norm(h, None, self.layers[0]["ln1"], s.rms_eps)
+        lin = _FusedOps.linear
         for li, L in enumerate(self.layers):
-            qkv = F.linear(x, L["wqkv"])
+            qkv = lin(x, L["wqkv"])
             q = _FusedOps.rope_write(qkv, cos, sin, cache, li, pos, s.heads, s.kv_heads, D)
             a = backend.decode(q, cache.k[li], cache.v[li], pos + 1)
-            o = F.linear(a.reshape(B, s.heads * D), L["wo"])
+            o = lin(a.reshape(B, s.heads * D), L["wo"])
             x = _FusedOps.add_rms_norm(h, o, L["ln2"], s.rms_eps)  # h += o
-            m = F.linear(_FusedOps.silu_mul(F.linear(x, L["wgu"])), L["wd"])
+            m = lin(lin(x, L["wgu"], swiglu=True), L["wd"])
             nxt = self.layers[li + 1]["ln1"] if li + 1 < len(self.layers) else self.norm
             x = _FusedOps.add_rms_norm(h, m, nxt, s.rms_eps)  # h += m, then the next layer's (or final) norm
-        return F.linear(x, self.lm_head).float()
+        return lin(x, self.lm_head).float()
 
 
 @torch.inference_mode()

@@ -154,6 +154,23 @@ def test_compute_entry_points_validate_before_any_launch(lib):
     assert rc == ERR_INVALID
 
 
+def test_linear_validates_before_any_launch(lib):
+    """santa_rt_linear rejects what its staged rows cannot hold, and the
+    runtime's shape predicate (which routes other shapes to F.linear) agrees
+    on every rejected case; pointers are never dereferenced."""
+    from santa_amd.runtime import _FusedOps
+
+    p, null = ctypes.c_void_p(16), ctypes.c_void_p(0)
+    assert lib.santa_rt_linear(null, p, p, 4, 64, 4096, 0, null) == ERR_INVALID
+    assert lib.santa_rt_linear(ctypes.c_void_p(8), p, p, 4, 64, 4096, 0, null) == ERR_INVALID
+    for M, K in [(0, 4096), (9, 4096), (4, 4100), (4, 16392), (8, 8200), (3, 20480), (1, 65544)]:
+        assert lib.santa_rt_linear(p, p, p, M, 64, K, 0, null) == ERR_INVALID, (M, K)
+        assert not _FusedOps.linear_fits(M, K), (M, K)
+    assert b"linear" in lib.santa_last_error()
+    for M, K in [(1, 65536), (2, 32768), (4, 16384), (4, 14336), (8, 8192), (3, 16384), (5, 8)]:
+        assert _FusedOps.linear_fits(M, K), (M, K)
+
+
 def test_paged_entry_points_validate_the_page_table(lib):
     null = ctypes.c_void_p(0)
     table = (ctypes.c_int * 4)()  # host memory: only its address is checked before a launch

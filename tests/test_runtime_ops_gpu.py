@@ -9,6 +9,16 @@ against the torch expressions of santa_amd/runtime.py they replace.
   the normalised row can round to a neighbouring bf16 value, which the weight
   multiply scales by up to 1.3 before the second rounding).
 * SwiGLU: to one bf16 unit in the last place (exp is this library's).
+* The few-row weight product (santa_rt_linear) against the float64 product
+  of the same bf16 operands: at least 99.9 % of the outputs are that value
+  rounded to bf16 (float32 accumulation changes the rounding only next to a
+  rounding boundary) and every output is within 2^-7 relative plus 2^-20 of
+  sum |x| |w|.  With the SwiGLU epilogue: bit for bit silu_mul of the
+  plain product (same sums, silu_mul's roundings), and at least 99.9 % equal
+  to silu_mul of the float64 product's bf16 roundings.  Shapes cover every
+  row padding (1, 2, 4, 8 staged rows), odd N, K not a multiple of the
+  2048-column chunk, the largest staged K, and more row pairs than resident
+  waves.
 
 Every case prints its name and shape before touching the GPU.
 """
@@ -84,3 +94,48 @@ def test_silu_mul(rows, inter):
     ref = F.silu(gate) * up
     torch.cuda.synchronize()
     _ulp_close(out, ref)
+
+
+def _bf16_bits_diff(got: torch.Tensor, ref: torch.Tensor) -> np.ndarray:
+    a = got.contiguous().view(torch.int16).cpu().numpy().astype(np.int32)
+    b = ref.contiguous().view(torch.int16).cpu().numpy().astype(np.int32)
+    return np.abs(a - b)
+
+
+@pytest.mark.parametrize("M,N,K", [(4, 6144, 4096), (4, 4096, 14336), (1, 1000, 512), (3, 777, 1000),
+                                   (8, 1030, 8192), (2, 129, 2056), (5, 64, 8), (4, 128256, 4096)])
+def test_linear(M, N, K):
+    print(f"\n[case] linear M={M} N={N} K={K}", flush=True)
+    assert _FusedOps.linear_fits(M, K)
+    g = torch.Generator(device=DEV).manual_seed(M * 7919 + N + K)
+    x = torch.randn(M, K, device=DEV, generator=g).to(torch.bfloat16)
+    w = (0.02 * torch.randn(N, K, device=DEV, generator=g)).to(torch.bfloat16)
+    y = _FusedOps.linear(x, w)
+    ref = x.double() @ w.double().t()
+    bound = ref.abs() * 2.0 ** -7 + (x.double().abs() @ w.double().abs().t()) * 2.0 ** -20
+    torch.cuda.synchronize()
+    assert y.shape == (M, N) and y.dtype == torch.bfloat16
+    assert ((y.double() - ref).abs() <= bound).all()
+    exact = (_bf16_bits_diff(y, ref.to(torch.bfloat16)) == 0).mean()
+    assert exact >= 0.999, exact
+
+
+@pytest.mark.parametrize("M,inter,K", [(4, 14336, 4096), (3, 1000, 1000), (1, 33, 2048), (8, 256, 8192)])
+def test_linear_swiglu(M, inter, K):
+    print(f"\n[case] linear swiglu M={M} inter={inter} K={K}", flush=True)
+    g = torch.Generator(device=DEV).manual_seed(M * 104729 + inter + K)
+    x = torch.randn(M, K, device=DEV, generator=g).to(torch.bfloat16)
+    w = (0.05 * torch.randn(2 * inter, K, device=DEV, generator=g)).to(torch.bfloat16)
+    out = _FusedOps.linear(x, w, swiglu=True)
+    # each row's sum takes the same path through the lanes wherever it sits
+    # in the wave's pair of rows, so the epilogue sees the plain product's
+    # values and applies silu_mul's roundings to them
+    two = _FusedOps.silu_mul(_FusedOps.linear(x, w))
+    gu = (x.double() @ w.double().t()).to(torch.bfloat16)
+    gate, up = gu.chunk(2, dim=-1)
+    ref = F.silu(gate) * up
+    torch.cuda.synchronize()
+    assert out.shape == (M, inter)
+    assert torch.equal(out.view(torch.int16), two.view(torch.int16))
+    exact = (out.view(torch.int16) == ref.view(torch.int16)).float().mean().item()
+    assert exact >= 0.999, exact
