@@ -41,7 +41,7 @@ def _ulp_close(got: torch.Tensor, ref: torch.Tensor, ulps: int = 1):
     assert np.abs(a - b).max() <= ulps, np.abs(a - b).max()
 
 
-@pytest.mark.parametrize("rows,hidden", [(1, 4096), (4, 4096), (3, 1000)])
+@pytest.mark.parametrize("rows,hidden", [(1, 4096), (4, 4096), (3, 1000), (2, 14336), (2, 8192), (2, 1004)])
 def test_add_rms_norm(rows, hidden):
     print(f"\n[case] add_rms_norm rows={rows} hidden={hidden}", flush=True)
     g = torch.Generator(device=DEV).manual_seed(rows * 7 + hidden)
