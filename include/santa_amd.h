@@ -250,13 +250,23 @@ int santa_prop_decode_paged(const void* q, const void* K_pages, const void* V_pa
  * 1, 2, 4 or 8 times K rounded up to 2048 at most 65536, x and w 16-byte
  * aligned.  swiglu != 0: w is [2N, K] (gate rows, then up rows) and
  * y [M, N] = bf16(bf16(silu(bf16(g))) * bf16(u)), silu_mul of the product.
- * The weights are read once at the HBM bound. */
+ * The weights are read once at the HBM bound.
+ * santa_rt_linear_rope: the fused q/k/v projection of rows x [M, K] by
+ * w [(H + 2 KVH) D, K] (head by head) with santa_rt_rope_write's epilogue
+ * applied to the bf16 products: q heads rotated into q_out [M, H, D], k heads
+ * rotated into k_cache[b, pos], v heads into v_cache[b, pos] (caches
+ * [M, storage, KVH, D]); bit for bit santa_rt_rope_write of santa_rt_linear's
+ * output, without writing that output.  D even; the santa_rt_linear limits
+ * on M and K. */
 int santa_rt_add_rms_norm(void* h, const void* a, const void* w, void* x, int rows, int hidden, float eps,
                           hipStream_t stream);
 int santa_rt_rope_write(const void* qkv, const void* cos_, const void* sin_, void* q_out, void* k_cache, void* v_cache,
                         int B, int H, int KVH, int D, long long storage, int pos, hipStream_t stream);
 int santa_rt_silu_mul(const void* gu, void* out, int rows, int inter, hipStream_t stream);
 int santa_rt_linear(const void* x, const void* w, void* y, int M, int N, int K, int swiglu, hipStream_t stream);
+int santa_rt_linear_rope(const void* x, const void* w, int M, int K, const void* cos_, const void* sin_, void* q_out,
+                         void* k_cache, void* v_cache, int H, int KVH, int D, long long storage, int pos,
+                         hipStream_t stream);
 
 #ifdef __cplusplus
 }

@@ -194,9 +194,25 @@ __global__ __launch_bounds__(256) void silu_mul_kernel(const uint16_t* __restric
 // reduced across the 64 lanes by halving exchanges, so each output ends in
 // one lane.  Rows beyond N and columns beyond K read as zero through the
 // buffer descriptors' range checks.
-// SWIGLU: W holds 2N rows (gate rows, then up rows); the pair of wave rows is
-// (n, n + N) and the output is bf16(bf16(silu(g)) * u) with g and u rounded to
-// bf16 first, the roundings of silu_mul_kernel after a bf16 product.
+// kLinSwiglu: W holds 2N rows (gate rows, then up rows); the pair of wave
+// rows is (n, n + N) and the output is bf16(bf16(silu(g)) * u) with g and u
+// rounded to bf16 first, the roundings of silu_mul_kernel after a bf16
+// product.
+// kLinRope: W is the fused q/k/v projection, N = (H + 2 KVH) D rows, head by
+// head; the pair is (d, d + D/2) of one head, the two elements rotate-half
+// RoPE combines, and the output goes where rope_write_kernel puts it (q
+// rotated to q_out, k rotated and v as is to the caches at pos), in its
+// roundings applied to the bf16 products; y is not written.
+constexpr int kLinPlain = 0, kLinSwiglu = 1, kLinRope = 2;
+struct RopeOut {
+  const uint16_t* cos;
+  const uint16_t* sin;
+  uint16_t* q;
+  uint16_t* k;
+  uint16_t* v;
+  int H, KVH, D, pos;
+  long long storage;
+};
 constexpr int kLinWaves = 16;
 constexpr int kLinThreads = kLinWaves * 64;
 constexpr int kLinSeg = 512;                // columns per wave-wide 16-byte load
@@ -250,26 +266,31 @@ __device__ __forceinline__ void lane_reduce(T& acc, int lane) {
   }
 }
 
-template <int MP, bool SWIGLU>
+template <int MP, int MODE>
 __global__ __launch_bounds__(kLinThreads, 1) void linear_kernel(const uint16_t* __restrict__ x,
                                                                 const uint16_t* __restrict__ W,
                                                                 uint16_t* __restrict__ y, int M, int N, int K, int Kp,
-                                                                int nbatch) {
+                                                                int nbatch, RopeOut ro) {
   __shared__ u32x4 xs[kLinLdsVecs];
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int kv = Kp / 8;  // LDS slots per x row
   const int nch = Kp / kLinChunk;
   const int stride = gridDim.x * kLinWaves;
-  const int rows_total = SWIGLU ? 2 * N : N;
+  const int rows_total = MODE == kLinSwiglu ? 2 * N : N;
+  const int half = ro.D / 2;
   const uint32_t row_bytes = static_cast<uint32_t>(K) * 2u;
 
   // the wave's batches (row pairs): wave * grid + block, then every stride
   int b = wave * gridDim.x + blockIdx.x;
   auto rows_of = [&](int bb, int& r0, int& r1) {
-    if constexpr (SWIGLU) {
+    if constexpr (MODE == kLinSwiglu) {
       r0 = bb;
       r1 = bb + N;
+    } else if constexpr (MODE == kLinRope) {
+      const int head = bb / half;
+      r0 = head * ro.D + (bb - head * half);
+      r1 = r0 + half;
     } else {
       r0 = 2 * bb;
       r1 = 2 * bb + 1;
@@ -354,12 +375,34 @@ __global__ __launch_bounds__(kLinThreads, 1) void linear_kernel(const uint16_t* 
       const bool lead = (lane & ((64 >> LOGV) - 1)) == 0;
       int r0, r1;
       rows_of(b, r0, r1);
-      if constexpr (SWIGLU) {
+      if constexpr (MODE == kLinSwiglu) {
         const float u = fxor<(64 >> LOGV)>(acc[0], lane);  // the (m, up) sum
         if (lead && (idx & 1) == 0 && m < M) {
           const float g = bf(to_bf(acc[0]));
           const float sg = bf(to_bf(g / (1.0f + expf(-g))));
           y[static_cast<size_t>(m) * N + r0] = to_bf(sg * bf(to_bf(u)));
+        }
+      } else if constexpr (MODE == kLinRope) {
+        const float u = fxor<(64 >> LOGV)>(acc[0], lane);  // the (m, d + D/2) sum
+        if (lead && (idx & 1) == 0 && m < M) {
+          const int head = r0 / ro.D, d = r0 - head * ro.D;
+          const uint16_t x0 = to_bf(acc[0]), x1 = to_bf(u);
+          if (head >= ro.H + ro.KVH) {  // v: as is
+            uint16_t* dst = ro.v + ((static_cast<size_t>(m) * ro.storage + ro.pos) * ro.KVH + (head - ro.H - ro.KVH)) *
+                                       ro.D;
+            dst[d] = x0;
+            dst[d + half] = x1;
+          } else {
+            // out = bf16(bf16(x * cos) + bf16(rot(x) * sin)), rot(x) = (-x[D/2:], x[:D/2])
+            const float f0 = bf(x0), f1 = bf(x1);
+            const uint16_t o0 = to_bf(bf(to_bf(f0 * bf(ro.cos[d]))) + bf(to_bf(-f1 * bf(ro.sin[d]))));
+            const uint16_t o1 = to_bf(bf(to_bf(f1 * bf(ro.cos[d + half]))) + bf(to_bf(f0 * bf(ro.sin[d + half]))));
+            uint16_t* dst = head < ro.H ? ro.q + (static_cast<size_t>(m) * ro.H + head) * ro.D
+                                        : ro.k + ((static_cast<size_t>(m) * ro.storage + ro.pos) * ro.KVH +
+                                                  (head - ro.H)) * ro.D;
+            dst[d] = o0;
+            dst[d + half] = o1;
+          }
         }
       } else {
         const int r = (idx & 1) ? r1 : r0;
@@ -428,9 +471,12 @@ extern "C" int santa_rt_rope_write(const void* qkv, const void* cos_, const void
   return clear_error();
 }
 
-extern "C" int santa_rt_linear(const void* x, const void* w, void* y, int M, int N, int K, int swiglu,
-                               hipStream_t stream) {
-  if (!x || !w || !y || M < 1 || M > 8 || N <= 0 || K <= 0 || K % 8 != 0 ||
+namespace {
+// The shape checks and launch shared by the santa_rt_linear entry points
+// (rows: the weight's row count, N the output width the kernel indexes).
+int launch_linear(int mode, const void* x, const void* w, void* y, int M, int N, int K, int rows,
+                  const rt::RopeOut& ro, hipStream_t stream) {
+  if (!x || !w || M < 1 || M > 8 || N <= 0 || K <= 0 || K % 8 != 0 ||
       (reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(w)) % 16 != 0)
     return set_error(SANTA_ERR_INVALID, "bad linear arguments (M in 1..8, K a multiple of 8, x and w 16-byte aligned)");
   const int MP = M <= 1 ? 1 : M <= 2 ? 2 : M <= 4 ? 4 : 8;
@@ -438,9 +484,8 @@ extern "C" int santa_rt_linear(const void* x, const void* w, void* y, int M, int
   if (MP * Kp / 8 > rt::kLinLdsVecs)
     return set_error(SANTA_ERR_INVALID, "linear: M x K too large for the staged rows (M rounded up to 1, 2, 4 or 8, "
                                         "times K rounded up to 2048, at most 65536)");
-  if (static_cast<long long>(swiglu ? 2 : 1) * N * K * 2 > 0x7fffffffffffLL)
-    return set_error(SANTA_ERR_INVALID, "linear: weight too large");
-  const int nbatch = swiglu ? N : (N + 1) / 2;
+  if (static_cast<long long>(rows) * K * 2 > 0x7fffffffffffLL) return set_error(SANTA_ERR_INVALID, "linear: weight too large");
+  const int nbatch = mode == rt::kLinPlain ? (N + 1) / 2 : mode == rt::kLinSwiglu ? N : N / 2;
   static int cached_dev = -1, cus = 256;
   int dev = 0;
   if (hipGetDevice(&dev) == hipSuccess && dev != cached_dev) {
@@ -453,13 +498,16 @@ extern "C" int santa_rt_linear(const void* x, const void* w, void* y, int M, int
   const uint16_t* wp = static_cast<const uint16_t*>(w);
   uint16_t* yp = static_cast<uint16_t*>(y);
   const int kp = static_cast<int>(Kp);
-#define SANTA_LIN(MPV)                                                                                              \
-  if (swiglu)                                                                                                       \
-    hipLaunchKernelGGL((rt::linear_kernel<MPV, true>), dim3(grid), dim3(rt::kLinThreads), 0, stream, xp, wp, yp, M, \
-                       N, K, kp, nbatch);                                                                           \
-  else                                                                                                              \
-    hipLaunchKernelGGL((rt::linear_kernel<MPV, false>), dim3(grid), dim3(rt::kLinThreads), 0, stream, xp, wp, yp,  \
-                       M, N, K, kp, nbatch);
+#define SANTA_LIN(MPV)                                                                                            \
+  if (mode == rt::kLinSwiglu)                                                                                     \
+    hipLaunchKernelGGL((rt::linear_kernel<MPV, rt::kLinSwiglu>), dim3(grid), dim3(rt::kLinThreads), 0, stream, xp, \
+                       wp, yp, M, N, K, kp, nbatch, ro);                                                          \
+  else if (mode == rt::kLinRope)                                                                                  \
+    hipLaunchKernelGGL((rt::linear_kernel<MPV, rt::kLinRope>), dim3(grid), dim3(rt::kLinThreads), 0, stream, xp,   \
+                       wp, yp, M, N, K, kp, nbatch, ro);                                                          \
+  else                                                                                                            \
+    hipLaunchKernelGGL((rt::linear_kernel<MPV, rt::kLinPlain>), dim3(grid), dim3(rt::kLinThreads), 0, stream, xp,  \
+                       wp, yp, M, N, K, kp, nbatch, ro);
   switch (MP) {
     case 1: SANTA_LIN(1) break;
     case 2: SANTA_LIN(2) break;
@@ -470,6 +518,28 @@ extern "C" int santa_rt_linear(const void* x, const void* w, void* y, int M, int
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess) return set_error(SANTA_ERR_HIP, "linear launch failed: %s", hipGetErrorString(e));
   return clear_error();
+}
+}  // namespace
+
+extern "C" int santa_rt_linear(const void* x, const void* w, void* y, int M, int N, int K, int swiglu,
+                               hipStream_t stream) {
+  if (!y) return set_error(SANTA_ERR_INVALID, "bad linear arguments (null output)");
+  const rt::RopeOut none{nullptr, nullptr, nullptr, nullptr, nullptr, 0, 0, 2, 0, 0};
+  return launch_linear(swiglu ? rt::kLinSwiglu : rt::kLinPlain, x, w, y, M, N, K, swiglu ? 2 * N : N, none, stream);
+}
+
+extern "C" int santa_rt_linear_rope(const void* x, const void* w, int M, int K, const void* cos_, const void* sin_,
+                                    void* q_out, void* k_cache, void* v_cache, int H, int KVH, int D,
+                                    long long storage, int pos, hipStream_t stream) {
+  if (!cos_ || !sin_ || !q_out || !k_cache || !v_cache || H <= 0 || KVH <= 0 || D <= 0 || D % 2 != 0 || pos < 0 ||
+      pos >= storage)
+    return set_error(SANTA_ERR_INVALID, "bad linear_rope arguments");
+  const long long n = static_cast<long long>(H + 2 * KVH) * D;
+  if (n > 0x7fffffff) return set_error(SANTA_ERR_INVALID, "linear_rope: projection too wide");
+  const rt::RopeOut ro{static_cast<const uint16_t*>(cos_), static_cast<const uint16_t*>(sin_),
+                       static_cast<uint16_t*>(q_out), static_cast<uint16_t*>(k_cache), static_cast<uint16_t*>(v_cache),
+                       H, KVH, D, pos, storage};
+  return launch_linear(rt::kLinRope, x, w, q_out, M, static_cast<int>(n), K, static_cast<int>(n), ro, stream);
 }
 
 extern "C" int santa_rt_silu_mul(const void* gu, void* out, int rows, int inter, hipStream_t stream) {

@@ -84,6 +84,8 @@ class _FusedOps:
             L.santa_rt_silu_mul.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int, ctypes.c_int,
                                             ctypes.c_void_p]
             L.santa_rt_linear.argtypes = [ctypes.c_void_p] * 3 + [ctypes.c_int] * 4 + [ctypes.c_void_p]
+            L.santa_rt_linear_rope.argtypes = [ctypes.c_void_p] * 2 + [ctypes.c_int] * 2 + [ctypes.c_void_p] * 5 + [
+                ctypes.c_int] * 3 + [ctypes.c_longlong, ctypes.c_int, ctypes.c_void_p]
             cls._lib = L
         return cls._lib
 
@@ -143,6 +145,24 @@ class _FusedOps:
         cls._check(cls.lib().santa_rt_linear(x.data_ptr(), w.data_ptr(), y.data_ptr(), rows, N, K, int(swiglu),
                                              cls._stream(x)))
         return y
+
+    @classmethod
+    def linear_rope(cls, x: torch.Tensor, w: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor, cache: "NHDCache",
+                    layer: int, pos: int, heads: int, kv_heads: int, head_dim: int) -> torch.Tensor:
+        """rope_write(linear(x, w), ...) as one kernel (santa_rt_linear_rope):
+        q rotated ([B, H, D]) returned, k rotated and v written to the caches
+        at pos; the two calls where the shape does not fit it."""
+        B, K = x.shape[0], x.shape[-1]
+        if not (cls.linear_fits(B, K) and x.dtype == torch.bfloat16 and w.dtype == torch.bfloat16
+                and x.is_contiguous() and w.is_contiguous() and x.data_ptr() % 16 == 0 and w.data_ptr() % 16 == 0
+                and cos.is_contiguous() and sin.is_contiguous() and head_dim % 2 == 0):
+            return cls.rope_write(cls.linear(x, w), cos, sin, cache, layer, pos, heads, kv_heads, head_dim)
+        q = torch.empty(B, heads, head_dim, dtype=x.dtype, device=x.device)
+        kc, vc = cache.k[layer], cache.v[layer]
+        cls._check(cls.lib().santa_rt_linear_rope(x.data_ptr(), w.data_ptr(), B, K, cos.data_ptr(), sin.data_ptr(),
+                                                  q.data_ptr(), kc.data_ptr(), vc.data_ptr(), heads, kv_heads,
+                                                  head_dim, kc.shape[1], pos, cls._stream(x)))
+        return q
 
     @classmethod
     def silu_mul(cls, gu: torch.Tensor) -> torch.Tensor:
@@ -356,18 +376,18 @@ class RandomLlama:
 
     def _decode_step_fused(self, h, cos, sin, pos, cache, backend):
         """decode_step on the GPU: per layer the four weight products as
-        santa_rt_linear (the gate/up product with SwiGLU in its epilogue), two
-        fused add + norm kernels and RoPE with the cache write, around the
-        backend's attention; the torch expressions' arithmetic and bf16
-        roundings, with each product accumulated in float32 in its own order."""
+        santa_rt_linear (the q/k/v product with RoPE and the cache write in its
+        epilogue, the gate/up product with SwiGLU) and two fused add + norm
+        kernels, around the backend's attention; the torch expressions'
+        arithmetic and bf16 roundings, with each product accumulated in
+        float32 in its own order."""
         s, D = self.shape, self.shape.head_dim
         B = h.shape[0]
         h = h.contiguous()
         x = _FusedOps.add_rms_norm(h, None, self.layers[0]["ln1"], s.rms_eps)
         lin = _FusedOps.linear
         for li, L in enumerate(self.layers):
-            qkv = lin(x, L["wqkv"])
-            q = _FusedOps.rope_write(qkv, cos, sin, cache, li, pos, s.heads, s.kv_heads, D)
+            q = _FusedOps.linear_rope(x, L["wqkv"], cos, sin, cache, li, pos, s.heads, s.kv_heads, D)
             a = backend.decode(q, cache.k[li], cache.v[li], pos + 1)
             o = lin(a.reshape(B, s.heads * D), L["wo"])
             x = _FusedOps.add_rms_norm(h, o, L["ln2"], s.rms_eps)  # h += o

@@ -169,6 +169,16 @@ def test_linear_validates_before_any_launch(lib):
     assert b"linear" in lib.santa_last_error()
     for M, K in [(1, 65536), (2, 32768), (4, 16384), (4, 14336), (8, 8192), (3, 16384), (5, 8)]:
         assert _FusedOps.linear_fits(M, K), (M, K)
+    # the RoPE form: odd D, pos outside the cache, null outputs, then the
+    # product's own limits
+    rope = lambda M, K, D, storage, pos, out=p: lib.santa_rt_linear_rope(p, p, M, K, p, p, out, p, p, 32, 8, D,
+                                                                        ctypes.c_longlong(storage), pos, null)
+    assert rope(4, 4096, 127, 100, 5) == ERR_INVALID
+    assert rope(4, 4096, 128, 100, 100) == ERR_INVALID
+    assert rope(4, 4096, 128, 100, -1) == ERR_INVALID
+    assert rope(4, 4096, 128, 100, 5, null) == ERR_INVALID
+    assert rope(9, 4096, 128, 100, 5) == ERR_INVALID
+    assert rope(4, 16392, 128, 100, 5) == ERR_INVALID
 
 
 def test_paged_entry_points_validate_the_page_table(lib):

@@ -18,7 +18,8 @@ against the torch expressions of santa_amd/runtime.py they replace.
   to silu_mul of the float64 product's bf16 roundings.  Shapes cover every
   row padding (1, 2, 4, 8 staged rows), odd N, K not a multiple of the
   2048-column chunk, the largest staged K, and more row pairs than resident
-  waves.
+  waves.  With the RoPE epilogue: bit for bit rope_write of the plain
+  product (q, the cache rows at pos), the caches' other rows untouched.
 
 Every case prints its name and shape before touching the GPU.
 """
@@ -139,3 +140,24 @@ def test_linear_swiglu(M, inter, K):
     assert torch.equal(out.view(torch.int16), two.view(torch.int16))
     exact = (out.view(torch.int16) == ref.view(torch.int16)).float().mean().item()
     assert exact >= 0.999, exact
+
+
+@pytest.mark.parametrize("B,H,KVH,D,K,pos", [(4, 32, 8, 128, 4096, 37), (2, 4, 1, 128, 512, 0), (3, 16, 2, 64, 1000, 99)])
+def test_linear_rope(B, H, KVH, D, K, pos):
+    print(f"\n[case] linear_rope B={B} H={H} KVH={KVH} D={D} K={K} pos={pos}", flush=True)
+    shape = LlamaShape(hidden=H * D, intermediate=8, heads=H, kv_heads=KVH, layers=1, vocab=8)  # head_dim D
+    g = torch.Generator(device=DEV).manual_seed(B * 31 + H + D + K + pos)
+    x = torch.randn(B, K, device=DEV, generator=g).to(torch.bfloat16)
+    w = (0.05 * torch.randn((H + 2 * KVH) * D, K, device=DEV, generator=g)).to(torch.bfloat16)
+    cos, sin = _rope_cos_sin(torch.tensor([pos], device=DEV), D, 5e5, torch.bfloat16)
+    cos, sin = cos.reshape(D).contiguous(), sin.reshape(D).contiguous()
+    fused = NHDCache(shape, B, pos + 5, torch.bfloat16, DEV)
+    for t in (fused.k[0], fused.v[0]):
+        t.copy_(torch.randn(t.shape, device=DEV, generator=g).to(torch.bfloat16))
+    two = fused.clone()
+    q = _FusedOps.linear_rope(x, w, cos, sin, fused, 0, pos, H, KVH, D)
+    q2 = _FusedOps.rope_write(_FusedOps.linear(x, w), cos, sin, two, 0, pos, H, KVH, D)
+    torch.cuda.synchronize()
+    assert torch.equal(q.view(torch.int16), q2.view(torch.int16))
+    assert torch.equal(fused.k[0].view(torch.int16), two.k[0].view(torch.int16))
+    assert torch.equal(fused.v[0].view(torch.int16), two.v[0].view(torch.int16))
