@@ -2184,7 +2184,8 @@ bool rows_layout(int KVH) { return KVH == 8; }
 int rows_per_round() { return 4 * resident_workgroups(); }
 
 // Little K to read (at most one resident round of single-wave items: B = 1
-// up to 64k tokens, B = 8 up to 8k): the block_n = 256 tile pass runs on the
+// up to 64k tokens, B = 8 up to 8k; uniform batches take one and a half,
+// see the overload below): the block_n = 256 tile pass runs on the
 // tile kernel, four waves per tile, whose per-tile latency chain is a
 // quarter of a wave's (B = 1, 4k tokens: 13.0 against 31.2 us per step; B =
 // 1, 32k: 26.5 against 36.2 us).  Above it the wave kernel is faster (B = 4,
@@ -2201,7 +2202,14 @@ bool small_prop_pass(long long kv_tiles) { return kv_tiles <= rows_per_round() /
 bool prop_wave_pass1(int path, int GH, int block_n) {
   return block_n == 256 && ((path == 0 && GH == 4) || (path == 1 && GH == 8));
 }
-static bool small_pass(int B, int KVH, int T_c) { return small_pass(static_cast<long long>(B) * KVH * T_c); }
+// Uniform batches keep the tile kernel up to one and a half rounds: at 32k
+// tokens it measures 41.3 us for B = 2 just past 2,048 items (T_c = 129)
+// against 50.8 us for the rows layout, and the two meet near 4,096 items
+// (B = 4: 66.4 against 67.2 us at T_c = 129; B = 8 is 10 % faster on the rows
+// layout).  Ragged grids keep the one-round threshold.
+static bool small_pass(int B, int KVH, int T_c) {
+  return static_cast<long long>(B) * KVH * T_c <= static_cast<long long>(rows_per_round()) * 3 / 2;
+}
 
 // Ragged batches: chunks small enough for about eight resident rounds over
 // all (kv, tile) items, so the hardware's workgroup dispatch evens out the
