@@ -257,7 +257,11 @@ int santa_prop_decode_paged(const void* q, const void* K_pages, const void* V_pa
  * rotated into k_cache[b, pos], v heads into v_cache[b, pos] (caches
  * [M, storage, KVH, D]); bit for bit santa_rt_rope_write of santa_rt_linear's
  * output, without writing that output.  D even; the santa_rt_linear limits
- * on M and K. */
+ * on M and K.
+ * santa_rt_argmax: out[r] (int64) = the index of the maximum of row r of
+ * x [rows, n] (float32), torch.argmax's choice: NaN above any number, the
+ * first index among equal values; the greedy step's token choice
+ * (tutorial_code/runtime_common.py:574-675). */
 int santa_rt_add_rms_norm(void* h, const void* a, const void* w, void* x, int rows, int hidden, float eps,
                           hipStream_t stream);
 int santa_rt_rope_write(const void* qkv, const void* cos_, const void* sin_, void* q_out, void* k_cache, void* v_cache,
@@ -267,6 +271,7 @@ int santa_rt_linear(const void* x, const void* w, void* y, int M, int N, int K, 
 int santa_rt_linear_rope(const void* x, const void* w, int M, int K, const void* cos_, const void* sin_, void* q_out,
                          void* k_cache, void* v_cache, int H, int KVH, int D, long long storage, int pos,
                          hipStream_t stream);
+int santa_rt_argmax(const float* x, int rows, int n, long long* out, hipStream_t stream);
 
 #ifdef __cplusplus
 }

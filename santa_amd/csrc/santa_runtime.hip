@@ -419,6 +419,89 @@ __global__ __launch_bounds__(kLinThreads, 1) void linear_kernel(const uint16_t* 
   }
 }
 
+// ------------------------------------------------------------------ argmax
+// Index of the maximum of each row of x [rows, n] (float32), torch.argmax's
+// choice: NaN counts as larger than any number, and among equal values (or
+// NaNs) the first index wins.  One 1024-thread workgroup per row; each thread
+// scans a strided slice (batches of eight 16-byte loads when the row allows),
+// then the waves and the workgroup keep the better (value, index) pair.
+constexpr int kArgmaxThreads = 1024;
+__device__ __forceinline__ bool argmax_better(float a, int ia, float b, int ib) {
+  const bool na = a != a, nb = b != b;
+  if (na != nb) return na;
+  if (!na && a != b) return a > b;
+  return ia < ib;
+}
+__global__ __launch_bounds__(kArgmaxThreads) void argmax_kernel(const float* __restrict__ x, int n,
+                                                                long long* __restrict__ out, int vec) {
+  __shared__ float s_v[kArgmaxThreads / 64];
+  __shared__ int s_i[kArgmaxThreads / 64];
+  const float* xr = x + static_cast<size_t>(blockIdx.x) * n;
+  const int tid = static_cast<int>(threadIdx.x);
+  float best = -__builtin_inff();
+  int bi = 0x7fffffff;
+  if (vec) {
+    typedef float f32x4v __attribute__((ext_vector_type(4)));
+    const f32x4v* xv = reinterpret_cast<const f32x4v*>(xr);
+    // eight independent 16-byte loads per thread in flight before any is
+    // compared (the pair rule orders by index, so the visiting order is free)
+    const int nv = n / 4;
+    for (int base = tid; base < nv; base += 8 * kArgmaxThreads) {
+      f32x4v v[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        const int i = base + u * kArgmaxThreads;
+        if (i < nv) v[u] = xv[i];
+      }
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        const int i = base + u * kArgmaxThreads;
+        if (i < nv) {
+#pragma unroll
+          for (int k = 0; k < 4; ++k)
+            if (argmax_better(v[u][k], 4 * i + k, best, bi)) {
+              best = v[u][k];
+              bi = 4 * i + k;
+            }
+        }
+      }
+    }
+    for (int i = (n / 4) * 4 + tid; i < n; i += kArgmaxThreads)
+      if (argmax_better(xr[i], i, best, bi)) {
+        best = xr[i];
+        bi = i;
+      }
+  } else {
+    for (int i = tid; i < n; i += kArgmaxThreads)
+      if (argmax_better(xr[i], i, best, bi)) {
+        best = xr[i];
+        bi = i;
+      }
+  }
+#pragma unroll
+  for (int m = 32; m > 0; m >>= 1) {
+    const float ov = __shfl_xor(best, m, 64);
+    const int oi = __shfl_xor(bi, m, 64);
+    if (argmax_better(ov, oi, best, bi)) {
+      best = ov;
+      bi = oi;
+    }
+  }
+  if ((tid & 63) == 0) {
+    s_v[tid >> 6] = best;
+    s_i[tid >> 6] = bi;
+  }
+  __syncthreads();
+  if (tid == 0) {
+    for (int w = 1; w < kArgmaxThreads / 64; ++w)
+      if (argmax_better(s_v[w], s_i[w], best, bi)) {
+        best = s_v[w];
+        bi = s_i[w];
+      }
+    out[blockIdx.x] = bi;
+  }
+}
+
 }  // namespace rt
 }  // namespace santa
 
@@ -540,6 +623,16 @@ extern "C" int santa_rt_linear_rope(const void* x, const void* w, int M, int K, 
                        static_cast<uint16_t*>(q_out), static_cast<uint16_t*>(k_cache), static_cast<uint16_t*>(v_cache),
                        H, KVH, D, pos, storage};
   return launch_linear(rt::kLinRope, x, w, q_out, M, static_cast<int>(n), K, static_cast<int>(n), ro, stream);
+}
+
+extern "C" int santa_rt_argmax(const float* x, int rows, int n, long long* out, hipStream_t stream) {
+  if (!x || !out || rows < 0 || n <= 0) return set_error(SANTA_ERR_INVALID, "bad argmax arguments");
+  if (rows == 0) return clear_error();
+  const int vec = (n % 4 == 0 && reinterpret_cast<uintptr_t>(x) % 16 == 0) ? 1 : 0;
+  hipLaunchKernelGGL(rt::argmax_kernel, dim3(rows), dim3(rt::kArgmaxThreads), 0, stream, x, n, out, vec);
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return set_error(SANTA_ERR_HIP, "argmax launch failed: %s", hipGetErrorString(e));
+  return clear_error();
 }
 
 extern "C" int santa_rt_silu_mul(const void* gu, void* out, int rows, int inter, hipStream_t stream) {

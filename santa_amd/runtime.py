@@ -86,6 +86,7 @@ class _FusedOps:
             L.santa_rt_linear.argtypes = [ctypes.c_void_p] * 3 + [ctypes.c_int] * 4 + [ctypes.c_void_p]
             L.santa_rt_linear_rope.argtypes = [ctypes.c_void_p] * 2 + [ctypes.c_int] * 2 + [ctypes.c_void_p] * 5 + [
                 ctypes.c_int] * 3 + [ctypes.c_longlong, ctypes.c_int, ctypes.c_void_p]
+            L.santa_rt_argmax.argtypes = [ctypes.c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p]
             cls._lib = L
         return cls._lib
 
@@ -163,6 +164,16 @@ class _FusedOps:
                                                   q.data_ptr(), kc.data_ptr(), vc.data_ptr(), heads, kv_heads,
                                                   head_dim, kc.shape[1], pos, cls._stream(x)))
         return q
+
+    @classmethod
+    def argmax(cls, logits: torch.Tensor) -> torch.Tensor:
+        """torch.argmax(logits, dim=-1) for float32 rows (santa_rt_argmax)."""
+        assert logits.dtype == torch.float32 and logits.is_contiguous()
+        n = logits.shape[-1]
+        rows = logits.numel() // n
+        out = torch.empty(logits.shape[:-1], dtype=torch.int64, device=logits.device)
+        cls._check(cls.lib().santa_rt_argmax(logits.data_ptr(), rows, n, out.data_ptr(), cls._stream(logits)))
+        return out
 
     @classmethod
     def silu_mul(cls, gu: torch.Tensor) -> torch.Tensor:
@@ -417,7 +428,12 @@ def greedy_decode(model: RandomLlama, first_logits: torch.Tensor, prompt_len: in
     t0 = time.perf_counter()
     pos = prompt_len
     for step in range(steps):
-        nxt = forced[:, step] if forced is not None else torch.argmax(logits, dim=-1)
+        if forced is not None:
+            nxt = forced[:, step]
+        elif timed and logits.dtype == torch.float32 and logits.is_contiguous():
+            nxt = _FusedOps.argmax(logits)
+        else:
+            nxt = torch.argmax(logits, dim=-1)
         toks.append(nxt)
         outs.append(logits)
         if step == steps - 1:

@@ -179,6 +179,9 @@ def test_linear_validates_before_any_launch(lib):
     assert rope(4, 4096, 128, 100, 5, null) == ERR_INVALID
     assert rope(9, 4096, 128, 100, 5) == ERR_INVALID
     assert rope(4, 16392, 128, 100, 5) == ERR_INVALID
+    assert lib.santa_rt_argmax(null, 4, 100, p, null) == ERR_INVALID
+    assert lib.santa_rt_argmax(p, 4, 0, p, null) == ERR_INVALID
+    assert lib.santa_rt_argmax(p, -1, 100, p, null) == ERR_INVALID
 
 
 def test_paged_entry_points_validate_the_page_table(lib):

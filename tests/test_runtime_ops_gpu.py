@@ -20,6 +20,10 @@ against the torch expressions of santa_amd/runtime.py they replace.
   2048-column chunk, the largest staged K, and more row pairs than resident
   waves.  With the RoPE epilogue: bit for bit rope_write of the plain
   product (q, the cache rows at pos), the caches' other rows untouched.
+* The greedy step's argmax: equal to torch.argmax on random rows, rows
+  with the maximum planted at several positions (first index wins), a NaN
+  row (NaN counts as the maximum), an all -inf row, and a width that is not
+  a multiple of 4 (the scalar path).
 
 Every case prints its name and shape before touching the GPU.
 """
@@ -161,3 +165,24 @@ def test_linear_rope(B, H, KVH, D, K, pos):
     assert torch.equal(q.view(torch.int16), q2.view(torch.int16))
     assert torch.equal(fused.k[0].view(torch.int16), two.k[0].view(torch.int16))
     assert torch.equal(fused.v[0].view(torch.int16), two.v[0].view(torch.int16))
+
+
+@pytest.mark.parametrize("rows,n", [(4, 128256), (3, 1001), (1, 7)])
+def test_argmax(rows, n):
+    print(f"\n[case] argmax rows={rows} n={n}", flush=True)
+    g = torch.Generator(device=DEV).manual_seed(rows * 13 + n)
+    x = torch.randn(rows, n, device=DEV, generator=g)
+    got = _FusedOps.argmax(x)
+    assert torch.equal(got, torch.argmax(x, dim=-1))
+    # ties: the row maximum planted at several positions
+    y = x.clone()
+    for r in range(rows):
+        cols = torch.randint(0, n, (3,), generator=torch.Generator().manual_seed(r + n)).tolist()
+        y[r, cols] = 10.0
+    assert torch.equal(_FusedOps.argmax(y), torch.argmax(y, dim=-1))
+    # NaN above any number; an all -inf row
+    z = x.clone()
+    z[0, n // 2] = float("nan")
+    z[-1] = float("-inf")
+    torch.cuda.synchronize()
+    assert torch.equal(_FusedOps.argmax(z), torch.argmax(z, dim=-1))
