@@ -28,6 +28,22 @@
  *   santa_prop_decode         <- the launch sequence of decode_systematic_scalar,
  *                                prop/santa_cuda.cpp:270-352
  *
+ * The stage entry points keep the reference launchers' split of the work and
+ * their argument meaning, with these deviations:
+ *   - no q_scale / scale argument (santa_flash_fused_tiles, santa_prop_pass1):
+ *     the scale is computed inside from D exactly as the reference's host
+ *     computes the value it passes, 1.0f / sqrtf((float)D) (flash: D = 128,
+ *     bits 0x3DB504F3, flash/santa_cuda.cpp:210; prop/santa_cuda.cpp:208);
+ *   - santa_flash_fused_tiles writes emit_cnt [B,KVH,T_c] (rows emitted per
+ *     tile) where launch_fused_tiles_* writes rowmask [B,KVH,L]
+ *     (flash/santa_cuda_kernel.cu:514-519), and santa_flash_finalize derives
+ *     vrows from it (the reference's launch_reduce_vrows sums the rowmask);
+ *   - one entry point per stage takes dtype, block_n and the pass-1 path as
+ *     arguments where the reference has one launcher per (dtype, block_n,
+ *     path) instantiation;
+ *   - santa_prop_pass2 also casts and scales the output (the reference's
+ *     launch_cast_scale_out_* is a separate launcher).
+ *
  * Layouts (row-major, contiguous):
  *   q   [B, H, D]            (B = 1 for the single-request form [H, D])
  *   K,V [B, L_storage, KVH, D]  (NHD cache; prop: [L, KVH, D])
@@ -123,7 +139,10 @@ int santa_flash_decode_merge(const void* workspace, size_t workspace_bytes, int 
  * reads).  Every call on a device shares that device's array: calls that
  * overlap on one device (different streams, or host threads) race and must
  * be ordered by the caller.  Results are bit-identical to santa_flash_decode
- * on the same arguments. */
+ * on the same arguments.  Under HIP graph capture: make one uncaptured call
+ * on each device first (it takes the scratch array's device address with
+ * hipGetSymbolAddress); captured calls then record kernel launches only (no
+ * memset or copy nodes), and their replays give the direct call's bits. */
 int santa_flash_decode_noalloc(const void* q, const void* K, const void* V, int dtype, int B, int H, int KVH, int D,
                                int L_valid, int L_storage, int block_n, int S_per_tile, uint64_t seed, void* out,
                                float* m_star, int* vrows, hipStream_t stream);

@@ -441,7 +441,8 @@ std::tuple<at::Tensor, at::Tensor> mfma_fma_check(at::Tensor a, at::Tensor b, at
 std::string tile_pass_kernel(int64_t B, int64_t H, int64_t KVH, int64_t T_c, int64_t block_n) {
   TORCH_CHECK(B > 0 && H > 0 && KVH > 0 && H % KVH == 0 && T_c > 0, "bad shape");
   const std::string gh = "GH " + std::to_string(H / KVH);
-  if (block_n == 256 && !santa::flash::small_pass(B * KVH * T_c))
+  if (block_n == 256 && !santa::flash::uniform_small_pass(static_cast<int>(B), static_cast<int>(KVH),
+                                                         static_cast<int>(T_c)))
     return "santa::flash::wave_kernel (block_n 256, " + gh +
            (santa::flash::rows_layout(static_cast<int>(KVH)) ? ", rows layout)" : ", four-wave layout)");
   return "santa::flash::tile_kernel (block_n " + std::to_string(block_n) + ", " + gh + ", online)";

@@ -58,6 +58,10 @@ bool rows_layout(int KVH);
 // waves per tile (tile_kernel) rather than one (wave_kernel); for santa_prop's
 // vec pass 1 that also means the [L, H] stash layout.
 bool small_pass(long long kv_tiles);
+// Uniform (one length) flash calls keep the tile kernel up to one and a half
+// resident rounds; the launch, the workspace plan and the bench label all
+// decide with this one function.
+bool uniform_small_pass(int B, int KVH, int T_c);
 bool small_prop_pass(long long kv_tiles);
 // santa_prop's pass 1 on the wave kernel (block_n 256: the vec path at GH 4,
 // the general path at GH 8); it writes the head-major stash when given a

@@ -569,12 +569,12 @@ int launch_linear(int mode, const void* x, const void* w, void* y, int M, int N,
                                         "times K rounded up to 2048, at most 65536)");
   if (static_cast<long long>(rows) * K * 2 > 0x7fffffffffffLL) return set_error(SANTA_ERR_INVALID, "linear: weight too large");
   const int nbatch = mode == rt::kLinPlain ? (N + 1) / 2 : mode == rt::kLinSwiglu ? N : N / 2;
-  static int cached_dev = -1, cus = 256;
-  int dev = 0;
-  if (hipGetDevice(&dev) == hipSuccess && dev != cached_dev) {
+  // the CU count of the current device, queried on each call (cheap next to
+  // a weight-streaming kernel, and free of shared state between host threads)
+  int dev = 0, cus = 256;
+  if (hipGetDevice(&dev) == hipSuccess) {
     int c = 0;
-    cus = (hipDeviceGetAttribute(&c, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && c > 0) ? c : 256;
-    cached_dev = dev;
+    if (hipDeviceGetAttribute(&c, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && c > 0) cus = c;
   }
   const unsigned grid = static_cast<unsigned>(nbatch < cus ? nbatch : cus);
   const uint16_t* xp = static_cast<const uint16_t*>(x);

@@ -372,6 +372,29 @@ def build(names: Sequence[str], *, santa_s: int, santa_seed: int, santa_block_n:
     return out
 
 
+# The backends a run compares by default: the exact comparator (this build's
+# counterpart of the reference's FA2 baseline, which is not available on
+# ROCm offline) and the two santa variants (benchmark_longctx.py:37).
+MAIN_BACKENDS = ["exact", "santa_flash", "santa_prop"]
+
+
+def format_optional_int(x: Optional[int]) -> str:
+    """None -> "unset(default)", else the integer as text (runtime_common.py:99-102)."""
+    return "unset(default)" if x is None else str(int(x))
+
+
+def write_invocation(out_dir: str, args: argparse.Namespace, device: Any, dtype: str = "bf16") -> str:
+    """invocation.json: the command-line arguments, device, dtype, santa block
+    size and the main backends, written before the model loads
+    (benchmark_longctx.py:739-751).  Returns the file's path."""
+    os.makedirs(out_dir, exist_ok=True)
+    path = os.path.join(out_dir, "invocation.json")
+    write_json(path, {"argv": vars(args), "device": str(device), "dtype": dtype,
+                      "santa_block_n": format_optional_int(getattr(args, "santa_block_n", None)),
+                      "paper_main_backends": list(MAIN_BACKENDS), "timestamp_unix": time.time()})
+    return path
+
+
 def parse_args(argv=None) -> argparse.Namespace:
     ap = argparse.ArgumentParser(description=__doc__.split("\n\n")[0])
     ap.add_argument("--out-dir", required=True)
@@ -396,6 +419,7 @@ def parse_args(argv=None) -> argparse.Namespace:
 def main(argv=None) -> int:
     args = parse_args(argv)
     dev = torch.device("cuda:0")
+    write_invocation(args.out_dir, args, dev)
     model = make_model(args.model, dev, seed=args.seed)
     backends = build(args.backends, santa_s=args.santa_s, santa_seed=args.santa_seed, santa_block_n=args.santa_block_n)
     batches = synthetic_batches(num_batches=args.num_batches, batch_size=args.batch_size, prompt_len=args.prompt_len,

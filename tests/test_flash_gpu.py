@@ -361,3 +361,72 @@ def test_cfg4_attention_shape_parity(valid_len):
     np.testing.assert_array_equal(vr.cpu().numpy(), exp["vrows"], err_msg="vrows")
     ok, mabs, mrel = tol_check(h16_to_f32(bits16(out)), h16_to_f32(exp["out16"]))
     assert ok, ("vs oracle", mabs, mrel)
+
+
+@pytest.mark.parametrize("B,L", [(3, 32768), (2, 32800)])
+def test_uniform_small_pass_range_parity(B, L):
+    """Uniform calls of 2,049 to 3,072 (kv, tile) items run their block_n =
+    256 tile pass on the tile kernel (B=3 at 32768 tokens: 3,072 items; B=2
+    at 32800: T_c = 129, 2,064 items, a last tile of 32 rows).  The
+    production call's m* and vrows exact to the oracle and its output within
+    the bf16 tolerance; the tile kernel's per-tile statistics and counts
+    (reference-structured mode) bit-exact."""
+    H, KVH, S = 32, 8, 256
+    m = _mod()
+    T_c = (L + 255) // 256
+    assert 2048 < B * KVH * T_c <= 3072
+    assert "tile_kernel" in m._tile_pass_kernel(B, H, KVH, T_c, 256)
+    _announce(f"uniform small pass B={B} H={H} KVH={KVH} L={L} S={S} items={B * KVH * T_c}")
+    q, K, V = gen_qkv(B, H, KVH, L, seed=SEED + B, lowrank=0.5)
+    dev = torch.device("cuda:0")
+    qd, Kd, Vd = q.to(dev), K.to(dev), V.to(dev)
+    mt, lt, cnt, _, _ = m._debug_tiles(qd, Kd, Vd, S, seed=SEED)
+    out, ms, vr = m.decode_systematic_batched(qd, Kd, Vd, S, seed=SEED, want_vrows=True)
+    torch.cuda.synchronize()
+    exp = oracle.flash_decode(q, K, V, S, seed=SEED, is_bf16=True, debug=True)
+    np.testing.assert_array_equal(mt.cpu().numpy().view(np.uint32), exp["m_tiles"].view(np.uint32), err_msg="m_tiles")
+    np.testing.assert_array_equal(lt.cpu().numpy().view(np.uint32), exp["ell_tiles"].view(np.uint32),
+                                  err_msg="ell_tiles")
+    c_gpu = cnt.cpu().numpy()
+    assert np.array_equal(c_gpu, exp["counts"]), f"counts differ at {np.argwhere(c_gpu != exp['counts'])[:8]}"
+    np.testing.assert_array_equal(ms.cpu().numpy().view(np.uint32), exp["m_star"].view(np.uint32), err_msg="m_star")
+    np.testing.assert_array_equal(vr.cpu().numpy(), exp["vrows"], err_msg="vrows")
+    ok, mabs, mrel = tol_check(h16_to_f32(bits16(out)), h16_to_f32(exp["out16"]))
+    assert ok, ("vs oracle", mabs, mrel)
+
+
+def test_cfg5_production_plan_parity():
+    """cfg5 itself (B=32, 64q/8kv so GH 8, L=131072, S=512, Student-t(3)
+    keys with planted needles, bench.device_inputs): the production call at
+    B=32 runs 64-tile chunks per wave with S_per_tile = 1, so the per-head
+    sample lists fill and are gathered mid-chunk.  Sequences 5 and 30 against
+    the oracle run on their own with b_offset = b (RNG key b*H + h): tile
+    max, tile mass and every count of the production-layout debug kernel
+    bit-exact, m* and vrows of the production call exact, its output within
+    the bf16 tolerance."""
+    import bench
+
+    B, H, KVH, L, S = 32, 64, 8, 131072, 512
+    _announce(f"cfg5 production plan B={B} H={H} KVH={KVH} L={L} S={S} needles seed={SEED}")
+    m = _mod()
+    dev = torch.device("cuda:0")
+    qd, Kd, Vd = bench.device_inputs(B, L, H, KVH, 128, SEED, dev, keys="needles")
+    out, ms, vr = m.decode_systematic_batched(qd, Kd, Vd, S, seed=SEED, want_vrows=True)
+    mt, lt, cnt = m._debug_wave(qd, Kd, Vd, S, seed=SEED, valid_len=-1)
+    torch.cuda.synchronize()
+    for b in (5, 30):
+        _announce(f"cfg5 production plan: sequence {b} against the oracle (b_offset={b})")
+        sl = slice(b, b + 1)
+        exp = oracle.flash_decode(qd[sl].cpu(), Kd[sl].cpu(), Vd[sl].cpu(), S, seed=SEED, block_n=256,
+                                  is_bf16=True, debug=True, b_offset=b)
+        np.testing.assert_array_equal(mt[sl].cpu().numpy().view(np.uint32), exp["m_tiles"].view(np.uint32),
+                                      err_msg=f"m_tiles b={b}")
+        np.testing.assert_array_equal(lt[sl].cpu().numpy().view(np.uint32), exp["ell_tiles"].view(np.uint32),
+                                      err_msg=f"ell_tiles b={b}")
+        c_gpu = cnt[sl].cpu().numpy()
+        assert np.array_equal(c_gpu, exp["counts"]), f"b={b}: counts differ at {np.argwhere(c_gpu != exp['counts'])[:8]}"
+        np.testing.assert_array_equal(ms[sl].cpu().numpy().view(np.uint32), exp["m_star"].view(np.uint32),
+                                      err_msg=f"m_star b={b}")
+        np.testing.assert_array_equal(vr[sl].cpu().numpy(), exp["vrows"], err_msg=f"vrows b={b}")
+        ok, mabs, mrel = tol_check(h16_to_f32(bits16(out[sl])), h16_to_f32(exp["out16"]))
+        assert ok, (f"vs oracle b={b}", mabs, mrel)

@@ -98,3 +98,19 @@ def test_statistics_closed_forms():
     assert row["tpot_ms"] == 62.5 and row["output_tokens_per_s"] == 16 and row["steps_sampled"] == 16
     assert row["prefill_tokens_per_s"] == 200 and row["hf_generate_wrapper_overhead_s"] == 0.5
     assert math.isclose(row["requests_per_s"], 4 / 7)
+
+
+def test_invocation_file(tmp_path):
+    """invocation.json (tutorial_code/benchmark_longctx.py:739-751): the CLI's
+    arguments, device, dtype, block size as text and the main backends."""
+    args = harness.parse_args(["--out-dir", str(tmp_path / "inv"), "--santa-block-n", "256"])
+    path = harness.write_invocation(args.out_dir, args, torch.device("cpu"))
+    with open(path) as f:
+        inv = json.load(f)
+    assert set(inv) == {"argv", "device", "dtype", "santa_block_n", "paper_main_backends", "timestamp_unix"}
+    assert inv["argv"]["santa_block_n"] == 256 and inv["santa_block_n"] == "256"
+    assert inv["device"] == "cpu" and inv["dtype"] == "bf16"
+    assert inv["paper_main_backends"] == ["exact", "santa_flash", "santa_prop"]
+    args = harness.parse_args(["--out-dir", str(tmp_path / "inv2")])
+    with open(harness.write_invocation(args.out_dir, args, "cuda:0")) as f:
+        assert json.load(f)["santa_block_n"] == "unset(default)"

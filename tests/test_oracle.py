@@ -151,6 +151,43 @@ def test_uniform_tile_sampler_known_answer():
             assert np.array_equal(c[h, t], want), (h, t)
 
 
+def test_uniform_tile_sampler_known_answer_batch_key():
+    """The same closed form at B = 2: sequence b draws with RNG key b*H + h
+    (flash/santa_cuda_kernel.cu:281), so sequence 1's rows come from
+    u01(seed, H + h, t).  A key slip (b*KVH + h, or h alone) moves them."""
+    H = 32
+    q, K, V = gen_qkv(2, H, 8, 4096)
+    q = torch.zeros_like(q)
+    r = oracle.flash_decode(q, K, V, 32, seed=SEED, debug=True)
+    c = r["counts"]
+    for b in range(2):
+        for h in range(H):
+            for t in range(16):
+                a0 = oracle.u01(SEED, b * H + h, t)
+                want = np.zeros(256, np.int16)
+                want[[math.ceil((k - a0) * 128) - 1 for k in (1, 2)]] = 1
+                assert np.array_equal(c[b, h, t], want), (b, h, t)
+    # the key slips would pick other rows for sequence 1 somewhere
+    slip = [oracle.u01(SEED, 8 + h, t) for h in range(H) for t in range(16)]
+    true = [oracle.u01(SEED, H + h, t) for h in range(H) for t in range(16)]
+    assert slip != true
+
+
+def test_b_offset_equals_the_batched_sequence():
+    """flash_decode(q[b:b+1], ..., b_offset=b) is sequence b of the batched
+    call: same counts, statistics, m*, vrows and output bits."""
+    q, K, V = gen_qkv(3, 16, 4, 1000, seed=SEED + 11)
+    full = oracle.flash_decode(q, K, V, 24, seed=SEED, debug=True)
+    for b in range(3):
+        one = oracle.flash_decode(q[b:b + 1], K[b:b + 1], V[b:b + 1], 24, seed=SEED, debug=True, b_offset=b)
+        for key in ("counts", "m_tiles", "ell_tiles", "m_star", "vrows", "out"):
+            got, want = np.asarray(one[key])[0], np.asarray(full[key])[b]
+            assert np.array_equal(got.view(np.uint8), want.view(np.uint8)), (b, key)
+        if b > 0:
+            zero = oracle.flash_decode(q[b:b + 1], K[b:b + 1], V[b:b + 1], 24, seed=SEED, debug=True)
+            assert not np.array_equal(zero["counts"][0], full["counts"][b])
+
+
 def test_one_hot_tile_takes_every_sample():
     """One key row aligned with the group's query (score ~ 45 nats above the
     rest) receives all S_pt samples of its tile for every head."""

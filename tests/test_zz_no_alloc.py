@@ -78,3 +78,45 @@ def test_noalloc_matches_decode(first, second):
                                       err_msg=f"call {i + 1}: m_star")
         np.testing.assert_array_equal(got[2].cpu().numpy(), ref[2].cpu().numpy(), err_msg=f"call {i + 1}: vrows")
         assert torch.isfinite(got[0].float()).all()
+
+
+def test_noalloc_under_graph_capture():
+    """A santa_flash_decode_noalloc call captured into a HIP graph (after one
+    uncaptured call on the device, which takes the scratch array's address)
+    replays with santa_flash_decode's results: three replays, with eager
+    calls on other inputs between them (which leave other contents in the
+    shared scratch), each bit-equal to the direct call."""
+    lib = _lib()
+    dev = torch.device("cuda:0")
+    B, H, L, S = 4, 32, 16384, 256
+    print(f"\n[case] santa_flash_decode_noalloc under graph capture: B={B} H={H} KVH=8 L={L} S={S}", flush=True)
+    q, K, V = gen_qkv(B, H, 8, L, seed=SEED + 77, lowrank=0.5)
+    qd, Kd, Vd = q.to(dev), K.to(dev), V.to(dev)
+    ref = _decode(lib, qd, Kd, Vd, S, -1, noalloc=False)
+    _decode(lib, qd, Kd, Vd, S, -1, noalloc=True)  # the uncaptured first call on the device
+    torch.cuda.synchronize()
+    L_, bn, T_c, spt = (I() for _ in range(4))
+    assert lib.santa_flash_plan(L, -1, 0, S, *(ctypes.byref(x) for x in (L_, bn, T_c, spt))) == 0
+    out = torch.empty_like(qd)
+    m_star = torch.empty(B, H, device=dev)
+    vrows = torch.empty(B, 8, dtype=torch.int32, device=dev)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        rc = lib.santa_flash_decode_noalloc(qd.data_ptr(), Kd.data_ptr(), Vd.data_ptr(), 0, B, H, 8, 128, L_.value, L,
+                                            bn.value, spt.value, SEED, out.data_ptr(), m_star.data_ptr(),
+                                            vrows.data_ptr(), torch.cuda.current_stream().cuda_stream)
+    assert rc == 0, lib.santa_last_error().decode()
+    q2, K2, V2 = gen_qkv(2, H, 8, 5000, seed=SEED + 78, lowrank=0.5)
+    q2, K2, V2 = q2.to(dev), K2.to(dev), V2.to(dev)
+    for rep in range(3):
+        out.zero_()
+        m_star.zero_()
+        vrows.zero_()
+        g.replay()
+        torch.cuda.synchronize()
+        np.testing.assert_array_equal(bits16(out), bits16(ref[0]), err_msg=f"replay {rep}: out")
+        np.testing.assert_array_equal(m_star.cpu().numpy().view(np.uint32), ref[1].cpu().numpy().view(np.uint32),
+                                      err_msg=f"replay {rep}: m_star")
+        np.testing.assert_array_equal(vrows.cpu().numpy(), ref[2].cpu().numpy(), err_msg=f"replay {rep}: vrows")
+        _decode(lib, q2, K2, V2, 200, -1, noalloc=True)  # eager work between replays
+        torch.cuda.synchronize()
