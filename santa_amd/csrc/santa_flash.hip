@@ -50,6 +50,7 @@
 #include <algorithm>
 #include <type_traits>
 #include <utility>
+#include <atomic>
 #include <mutex>
 
 namespace santa {
@@ -1082,8 +1083,8 @@ __global__ __launch_bounds__(ROWS ? 512 : kThreads, ROWS ? 1 : 2) void wave_kern
 #pragma unroll
     for (int sb = 0; sb < 4; ++sb) {
       if (sb == 0) {
-        // sub-block 0 came by DMA; for GH 8 the 16 loads of sub-block 1 were
-        // issued after it
+        // sub-block 0 came by DMA; for GH 8 the 16 register loads of
+        // sub-block 1 were issued after it (and may still be in flight)
         if constexpr (GH == 4) {
           asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         } else {
@@ -1097,7 +1098,7 @@ __global__ __launch_bounds__(ROWS ? 512 : kThreads, ROWS ? 1 : 2) void wave_kern
           wk[r * 16 + ((lane & 15) ^ (r & 15))] = kw[c];
         }
         // sub-blocks 2, 3, then the next tile's sub-block 1 (GH 4; GH 8 loads
-        // it after the tail, whose registers would not fit beside it)
+        // it after the next tile's DMA, below)
         if (sb < 3) {
           load_k(t, sb + 1, pv);
         } else if constexpr (GH == 4) {
@@ -1136,6 +1137,9 @@ __global__ __launch_bounds__(ROWS ? 512 : kThreads, ROWS ? 1 : 2) void wave_kern
     // every row of the staging area has been read: the next tile's sub-block 0
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
     if (t + TS < t_end) dma_k(t + TS, pv_next);
+    // GH 8: the next tile's sub-block 1 too, so that 32 KiB per wave are in
+    // flight during the tail as for GH 4 (its registers fit beside the tail's)
+    if constexpr (GH == 8) load_k(t + TS, 1, pv_next);
     balance(3 * (t - t_first) + 2);
 
     // ---- tile max per head (exact in any order) --------------------------------
@@ -1276,7 +1280,10 @@ __global__ __launch_bounds__(ROWS ? 512 : kThreads, ROWS ? 1 : 2) void wave_kern
             uni[hh][e] |= nz;
             const int nn = __popcll(nz);
             if (nn) {
-              if (lcnt[g] + nn > LCAP) flush(g);
+              // a full list is rare (about once per chunk and head at
+              // S_per_tile = 1): the gather is laid out off the hot path, so
+              // the loop's hot code stays contiguous in the instruction cache
+              if (__builtin_expect(lcnt[g] + nn > LCAP, 0)) flush(g);
               if (c != 0) {
                 const int pos = lcnt[g] + static_cast<int>(__builtin_amdgcn_mbcnt_hi(
                                               static_cast<uint32_t>(nz >> 32),
@@ -1322,7 +1329,6 @@ __global__ __launch_bounds__(ROWS ? 512 : kThreads, ROWS ? 1 : 2) void wave_kern
         }
     }
     emit_total += __popcll(uni[0][0]) + __popcll(uni[0][1]) + __popcll(uni[1][0]) + __popcll(uni[1][1]);
-    if constexpr (GH == 8) load_k(t + TS, 1, pv_next);
     pv = pv_next;
   }
   // no load to LDS outstanding past here (the staging area is reused below)
@@ -2010,19 +2016,22 @@ static hipError_t launch_tiles(int dtype, int GH, int bn, const Args& a, hipStre
 }
 
 // Workgroups resident per device: CUs x 2 (two 256-thread workgroups per CU
-// at the tile kernel's register budget).
+// at the tile kernel's register budget), cached per device in atomics (host
+// threads on different devices each see their own count; two threads filling
+// the same entry store the same value).
 static int resident_workgroups() {
+  constexpr int kMaxDev = 64;
+  static std::atomic<int> cached[kMaxDev];
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess) return 512;
-  static int cached_dev = -1;
-  static int cached = 512;
-  if (dev != cached_dev) {
-    int cus = 0;
-    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) cus = 256;
-    cached = 2 * cus;
-    cached_dev = dev;
+  if (dev >= 0 && dev < kMaxDev) {
+    const int c = cached[dev].load(std::memory_order_relaxed);
+    if (c > 0) return c;
   }
-  return cached;
+  int cus = 0;
+  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) cus = 256;
+  if (dev >= 0 && dev < kMaxDev) cached[dev].store(2 * cus, std::memory_order_relaxed);
+  return 2 * cus;
 }
 
 // Chunking of each group's T_c tiles so that B*KVH*cpg is about one resident
@@ -2207,7 +2216,7 @@ bool prop_wave_pass1(int path, int GH, int block_n) {
 // against 50.8 us for the rows layout, and the two meet near 4,096 items
 // (B = 4: 66.4 against 67.2 us at T_c = 129; B = 8 is 10 % faster on the rows
 // layout).  Ragged grids keep the one-round threshold.
-static bool small_pass(int B, int KVH, int T_c) {
+bool uniform_small_pass(int B, int KVH, int T_c) {
   return static_cast<long long>(B) * KVH * T_c <= static_cast<long long>(rows_per_round()) * 3 / 2;
 }
 
@@ -2337,7 +2346,7 @@ struct FlashWs {
 };
 FlashWs flash_ws_layout(int B, int H, int KVH, int T_c) {
   FlashWs w{};
-  const bool rows = flash::rows_layout(KVH) && !flash::small_pass(B, KVH, T_c);
+  const bool rows = flash::rows_layout(KVH) && !flash::uniform_small_pass(B, KVH, T_c);
   flash::chunk_plan(B, KVH, T_c, &w.cs, &w.cpg, rows ? flash::rows_per_round() : 0);
   const size_t chunks = static_cast<size_t>(B) * KVH * w.cpg;
   const int GH = H / KVH;
@@ -2393,7 +2402,7 @@ extern "C" int santa_flash_decode_tiles(const void* q, const void* K, const void
   flash::Args a{q, K, V, B, H, KVH, L_valid, L_storage, T_c, S_per_tile, seed, nullptr, nullptr, nullptr, nullptr,
                 nullptr, reinterpret_cast<float*>(base + w.part), reinterpret_cast<int*>(base + w.emit), w.cs, w.cpg,
                 nullptr};
-  const bool wave = block_n == 256 && !flash::small_pass(B, KVH, T_c);
+  const bool wave = block_n == 256 && !flash::uniform_small_pass(B, KVH, T_c);
   const hipError_t e = wave ? flash::launch_wave(dtype, H / KVH, a, nullptr, nullptr, nullptr, stream)
                             : flash::launch_tiles<flash::kOnline>(dtype, H / KVH, block_n, a, stream);
   if (e != hipSuccess) return set_error(SANTA_ERR_HIP, "tile launch failed: %s", hipGetErrorString(e));
