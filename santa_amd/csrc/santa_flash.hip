@@ -1299,14 +1299,18 @@ __global__ __launch_bounds__(ROWS ? 512 : kThreads, ROWS ? 1 : 2) void wave_kern
     head_block(std::integral_constant<int, 0>{});
     if constexpr (NHB == 2) head_block(std::integral_constant<int, 1>{});
     if (P1 && stash_ld > 0) {
-      // head-major stash: per head and register pair, the lane's two rows as
-      // one 4-B store (whole tiles, 0 past len)
+      // tile-major stash [B, T, H, 256] (T = stash_ld / 256): per head and
+      // register pair, the lane's two rows as one 4-B store (whole tiles, 0
+      // past len).  The KV heads of a tile write one contiguous block (GH 8:
+      // the cfg5-shaped prop step 2058 -> 1983 us against the head-major
+      // [B, H, stash_ld], whose per-head rows lie stash_ld * 2 bytes apart)
 #pragma unroll
       for (int g = 0; g < GH; ++g)
 #pragma unroll
         for (int hh = 0; hh < 2; ++hh)
-          *reinterpret_cast<uint32_t*>(u_stash + (static_cast<size_t>(b) * H + h0 + g) * stash_ld + n0 + 128 * hh +
-                                       32 * jrow + 2 * qq) = ubits[g][hh][0] | (ubits[g][hh][1] << 16);
+          *reinterpret_cast<uint32_t*>(u_stash + static_cast<size_t>(b) * H * stash_ld +
+                                       (static_cast<size_t>(t) * H + h0 + g) * BN + 128 * hh + 32 * jrow + 2 * qq) =
+              ubits[g][hh][0] | (ubits[g][hh][1] << 16);
     } else if constexpr (P1) {
       // the stash row [n, h0 .. h0+GH) of each valid row: one 8-B (GH 4) or
       // 16-B (GH 8) store
@@ -2202,7 +2206,7 @@ int rows_per_round() { return 4 * resident_workgroups(); }
 bool small_pass(long long kv_tiles) { return kv_tiles <= rows_per_round(); }
 // santa_prop's vec pass 1 takes the tile kernel below a quarter of that: the
 // [L, H] stash it writes costs pass 2 four 2-byte loads per lane and row pair
-// where the head-major one costs one, which outweighs the shorter pass 1 from
+// where the tile-major one costs one, which outweighs the shorter pass 1 from
 // about 32k tokens of one sequence (per call: 4k 30.8 -> 19.7 us, 16k 38.5 ->
 // 31.3 us; 32k 44.0 -> 45.8 us, 64k 54.3 -> 64.5 us).
 bool small_prop_pass(long long kv_tiles) { return kv_tiles <= rows_per_round() / 4; }

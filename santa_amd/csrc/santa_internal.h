@@ -38,7 +38,7 @@ namespace flash {
 // Ragged form: seq_lens (device, [B]) holds each sequence's length, L the
 // longest (it sets the tile stride of m/ell), cs tiles per chunk and n_wg
 // workgroups (any workgroup past the last sequence exits at once).
-// stash_ld > 0 (vec path only): the stash is head-major [B, H, stash_ld],
+// stash_ld > 0 (vec path only): the stash is tile-major [B, stash_ld / 256, H, 256],
 // whole 256-row tiles, 0 past each sequence's length.
 hipError_t launch_prop_pass1(const void* q, const void* K, int dtype, int B, int H, int KVH, int L, int L_storage,
                              int block_n, int path, float* m_tiles, float* ell_tiles, uint16_t* u_stash,
@@ -64,7 +64,7 @@ bool small_pass(long long kv_tiles);
 bool uniform_small_pass(int B, int KVH, int T_c);
 bool small_prop_pass(long long kv_tiles);
 // santa_prop's pass 1 on the wave kernel (block_n 256: the vec path at GH 4,
-// the general path at GH 8); it writes the head-major stash when given a
+// the general path at GH 8); it writes the tile-major stash when given a
 // stash_ld, which pass 2 then reads.
 bool prop_wave_pass1(int path, int GH, int block_n);
 int rows_per_round();

@@ -343,7 +343,7 @@ __device__ __forceinline__ int union_rows(const uint64_t* s_mask, int lane) {
 // LDS list, then the count-weighted V rows (fma per element) added to the
 // head's running sum.  The next tile's stash entries are loaded before the
 // current tile's V gather.
-// HM: the stash is head-major [B, H, stash_ld] (the fused decode's layout
+// HM: the stash is tile-major [B, T, H, 256], T = stash_ld / 256 (the fused decode's layout
 // for the vec path: a lane reads its row pair with one 4-B load); otherwise
 // the reference's [B, L_storage, H].
 // PAGED: V is a page pool read through pt (the stash is indexed by token).
@@ -457,7 +457,7 @@ __global__ __launch_bounds__(kThreads, (GH == 4 && BN == 256 && !PAGED) ? 6 : 4)
         const int row = 32 * (4 * p + jrow) + 2 * qq;
         if constexpr (HM) {
           // whole padded tiles are in the stash (0 past len)
-          const uint32_t w = *reinterpret_cast<const uint32_t*>(ub + static_cast<size_t>(h) * stash_ld + n0 + row);
+          const uint32_t w = *reinterpret_cast<const uint32_t*>(ub + (static_cast<size_t>(t) * H + h) * BN + row);
           un0[k][p] = static_cast<uint16_t>(w & 0xffffu);
           un1[k][p] = static_cast<uint16_t>(w >> 16);
         } else {
@@ -684,7 +684,7 @@ __global__ __launch_bounds__(kD) void finalize_kernel(const float* __restrict__ 
 struct Pass2Grid {
   const int* seq_lens;
   int n_wg;
-  int stash_ld;  // > 0: head-major stash [B, H, stash_ld] (block_n 256 only)
+  int stash_ld;  // > 0: tile-major stash [B, stash_ld / 256, H, 256] (block_n 256 only)
   PageTable pt;  // paged V (pt.table set) or contiguous
 };
 
@@ -728,7 +728,7 @@ static hipError_t launch_pass2_bn(int bn, const uint16_t* V, const uint16_t* u_s
   }
 }
 
-// Leading dimension of the head-major stash: whole 256-row tiles.
+// Rows per (sequence, head) of the tile-major stash: whole 256-row tiles.
 static int stash_ld(int L_storage) { return (L_storage + 255) / 256 * 256; }
 
 // Workspace of one decode call (offsets 256-B aligned).
@@ -761,7 +761,7 @@ static PropWs prop_ws_layout(int B, int H, int KVH, int D, int L_storage, int T_
   off = align_up(off + bht * sizeof(float));
   w.a0 = off;
   off = align_up(off + bht * sizeof(float));
-  w.stash = off;  // [B, L_storage, H] or head-major [B, H, stash_ld(L_storage)]
+  w.stash = off;  // [B, L_storage, H] or tile-major [B, stash_ld(L_storage) / 256, H, 256]
   off = align_up(off + static_cast<size_t>(B) * stash_ld(L_storage) * H * sizeof(uint16_t));
   w.part = off;  // [chunks, GH, D]
   off = align_up(off + chunks * (H / KVH) * static_cast<size_t>(D) * sizeof(float));
@@ -1005,7 +1005,7 @@ extern "C" int santa_prop_decode(const void* q, const void* K, const void* V, in
   uint16_t* stash = reinterpret_cast<uint16_t*>(base + w.stash);
   const bool gen = propgen::generic_shape(H / KVH, D, block_n);
   // a pass 1 on the wave kernel (the vec path, the general path at GH 8)
-  // keeps the stash head-major between the two passes, except for a small
+  // keeps the stash tile-major between the two passes, except for a small
   // pass, which runs four waves per tile with the [L, H] stash
   const bool small = flash::small_prop_pass(static_cast<long long>(T_c) * KVH);
   const int sld = (!gen && flash::prop_wave_pass1(pass1_path, H / KVH, block_n) && !small) ? prop::stash_ld(L) : 0;
