@@ -57,13 +57,19 @@ def parse_args():
     ap.add_argument("--S", type=int, default=256)
     ap.add_argument("--seed", type=int, default=1690)
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--workload", choices=("cfg2", "cfg3", "cfg4", "cfg5", "cfg5p", "single"), default="cfg2",
+    ap.add_argument("--workload", choices=("cfg2", "cfg3", "cfg4", "cfg5", "cfg5p", "single", "propgen"),
+                    default="cfg2",
                     help="cfg2: the headline (flash, B=8, 32k); cfg3: batched ragged santa_prop (B=16, "
                          "L_b in [8192, 131072], S_b = L_b // 64); cfg4: model-level decode, random-init "
                          "Llama-3.1-8B shape, B=4, 32768-token prompt, 64 greedy steps, santa_flash S=256 vs exact; "
                          "cfg5: flash stress (B=32, 64q/8kv, 128k, S=512); cfg5p: santa_prop at cfg5's shape with "
                          "S=512 per sequence; single: one sequence of --ctx tokens through santa_flash (S=256) "
-                         "and santa_prop (S=L/64)")
+                         "and santa_prop (S=L/64); propgen: santa_prop on a shape outside the tuned kernels "
+                         "(--heads/--kv-heads/--head-dim, default MHA 32q/32kv d=128), B=--batch, --ctx tokens, "
+                         "S = L // 64 per sequence")
+    ap.add_argument("--heads", type=int, default=32, help="propgen: query heads")
+    ap.add_argument("--kv-heads", type=int, default=32, help="propgen: KV heads")
+    ap.add_argument("--head-dim", type=int, default=128, help="propgen: head_dim")
     ap.add_argument("--cpu-sample-seqs", type=int, default=8, help="sequences timed for the CPU baseline")
     ap.add_argument("--score-scale", type=float, default=1.0,
                     help="cfg4: multiply the query projections by this (every attention score that many times "
@@ -490,6 +496,39 @@ def run_cfg5p(args, dev):
     return line
 
 
+def run_propgen(args, dev):
+    """santa_prop on a shape the tuned pass-1 kernels do not take (default MHA
+    32q/32kv, d=128; GQA 2/16 and head dims other than 128 likewise), B=--batch
+    sequences of --ctx tokens, S = L // 64 per sequence, K/V ~ N(0,1); one
+    batched call per step."""
+    import torch
+    import santa_prop_batch_cuda as prop
+
+    B, L, H, KVH, D, seed = args.batch, args.ctx, args.heads, args.kv_heads, args.head_dim, args.seed
+    S = max(1, L // 64)
+    g = torch.Generator(device=dev).manual_seed(seed)
+    q = torch.randn(B, H, D, device=dev, generator=g).bfloat16()
+    K = torch.randn(B, L, KVH, D, device=dev, generator=g).bfloat16()
+    V = torch.randn(B, L, KVH, D, device=dev, generator=g).bfloat16()
+    torch.cuda.synchronize()
+
+    def step(want_vrows=False):
+        return prop.decode_systematic_batched(q, K, V, S, seed=seed, want_vrows=want_vrows)
+
+    _, _, vrows = step(True)
+    v_rows = int(vrows.sum().item())
+    tm = Timing(args).run(step)
+    line = base_line(f"sampled-attn decode µs/step + achieved HBM TB/s; tokens/s (santa_prop, {H}q/{KVH}kv, d={D})",
+                     B, tm, args)
+    line["config"] = {"workload": f"santa_prop batched decode, {H}q/{KVH}kv (GH {H // KVH}), d={D}, B={B}, {L} cached "
+                                  f"tokens, S={S} per sequence, seed {seed}, K/V ~ N(0,1)",
+                      "global_batch": B, "seq_len": L, "S": S, "parallelism": "single GPU"}
+    line["roofline"] = roofline(flash_bytes([L] * B, KVH, H, B, v_rows, D=D), tm,
+                                "whole prop step (pass 1 + budgets + pass 2 + finalize)", None, v_rows)
+    line.update(timing_keys(tm))
+    return line
+
+
 def run_single(args, dev):
     """One sequence of --ctx tokens (32q/8kv, d=128, bf16, N(0,1) from the
     seeded device generator): santa_flash decode_systematic_batched at B=1
@@ -602,7 +641,7 @@ def main():
         line = run_cfg2_paged(args, dev) if args.page_size else run_cfg2(args, dev)
     else:
         line = {"cfg3": run_cfg3, "cfg4": run_cfg4, "cfg5": run_cfg5, "cfg5p": run_cfg5p,
-                "single": run_single}[args.workload](args, dev)
+                "single": run_single, "propgen": run_propgen}[args.workload](args, dev)
     print(json.dumps(line))
     return 0
 

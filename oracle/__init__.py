@@ -235,7 +235,7 @@ def prop_pass1_mode(GH: int, D: int, bn: int, env: Optional[str] = None) -> int:
 def prop_decode(q, K, V, S: int, seed: int = 42, block_n: int = 0, is_bf16: bool = True,
                 pass1_mode: Optional[int] = None, debug: bool = False) -> Dict[str, np.ndarray]:
     """Oracle of santa_prop_batch_cuda.decode_systematic_scalar for one sequence:
-    q [H,D]; K,V [L,KVH,D] (D a multiple of 16 up to 256; block_n a multiple
+    q [H,D]; K,V [L,KVH,D] (D a multiple of 16 up to 1024; block_n a multiple
     of 16 up to 512)."""
     qb, Kb, Vb = as_bits(q), as_bits(K), as_bits(V)
     H, D = qb.shape

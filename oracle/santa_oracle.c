@@ -37,7 +37,7 @@
 #endif
 
 #define SO_D 128      /* flash: the reference's only head_dim */
-#define SO_MAX_D 256  /* prop: any multiple of 16 up to this */
+#define SO_MAX_D 1024  /* prop: any multiple of 16 up to this */
 #define SO_MAX_GH 16
 #define SO_MAX_BN 512
 #define SO_LANES 32
@@ -154,6 +154,24 @@ static float lane_tree_down(const float* in) {
   for (int off = 16; off > 0; off >>= 1) {
     for (int l = 0; l < SO_LANES; ++l) t[l] = v[l] + ((l + off < SO_LANES) ? v[l + off] : v[l]);
     memcpy(v, t, sizeof(v));
+  }
+  return v[0];
+}
+
+/* The shfl_down tree over P lanes (P <= SO_MAX_D / 4): at offsets N/2, N/4,
+ * ..., 1 (N the next power of two >= P) lane l < offset adds lane l + offset
+ * when that lane holds a value; lanes from P on hold none.  For P = 32 this is
+ * lane_tree_down. */
+static float lane_tree_down_p(const float* in, int P) {
+  float v[SO_MAX_D / 4];
+  memcpy(v, in, (size_t)P * sizeof(float));
+  int N = 1;
+  while (N < P) N <<= 1;
+  int n = P; /* lanes 0 .. n-1 hold values */
+  for (int off = N / 2; off > 0; off >>= 1) {
+    for (int l = 0; l < off; ++l)
+      if (l + off < n) v[l] = v[l] + v[l + off];
+    if (n > off) n = off;
   }
   return v[0];
 }
@@ -477,11 +495,12 @@ int so_flash_decode(const uint16_t* Q, const uint16_t* K, const uint16_t* V, int
 /* Pass-1 of the general ("WMMA") path, prop/santa_cuda_kernel.cu:87-267:
  * q' = TK(f32(q) * scale) (:121-140).  The reference's scores come from a
  * 16x16x16 MMA whose internal association is unspecified; this build fixes
- * it: for D = 128 to the vec path's (4-element fma chains per virtual lane
- * and the 32-lane tree, A.2), for any other D (a multiple of 16) to one fma
- * chain over d ascending -- the GPU kernels and this restatement agree bit
- * for bit.  ell: per 16-row slab a sequential sum (:229-246), then a
- * sequential sum over slabs (:257-259). */
+ * it for every D (a multiple of 16) to the vec path's form extended to D
+ * dims: virtual lane v chains dims 4v .. 4v+3 with fma, then the shfl_down
+ * tree over the D/4 virtual lanes (lane_tree_down_p); for D = 128 that is
+ * exactly the vec path's 32-lane association (A.2).  The GPU kernels and
+ * this restatement agree bit for bit.  ell: per 16-row slab a sequential sum
+ * (:229-246), then a sequential sum over slabs (:257-259). */
 static void tile_stats_general(const uint16_t* Qh /*[GH][D] raw*/, const uint16_t* K, size_t row0_off,
                                size_t row_stride, int len, int BN, int GH, int D, int is_bf16, float q_scale,
                                tile_stats_t* ts, float* scores) {
@@ -500,22 +519,16 @@ static void tile_stats_general(const uint16_t* Qh /*[GH][D] raw*/, const uint16_
     for (int d = 0; d < D; ++d) kf[d] = ld16(krow, (size_t)d, is_bf16);
     for (int g = 0; g < GH; ++g) {
       const float* q = qr + (size_t)g * D;
-      float sf;
-      if (D == SO_D) {
-        float lanes[SO_LANES];
-        for (int l = 0; l < SO_LANES; ++l) {
-          float sl = 0.0f;
-          sl = fmaf(q[4 * l + 0], kf[4 * l + 0], sl);
-          sl = fmaf(q[4 * l + 1], kf[4 * l + 1], sl);
-          sl = fmaf(q[4 * l + 2], kf[4 * l + 2], sl);
-          sl = fmaf(q[4 * l + 3], kf[4 * l + 3], sl);
-          lanes[l] = sl;
-        }
-        sf = lane_tree_down(lanes);
-      } else {
-        sf = 0.0f;
-        for (int d = 0; d < D; ++d) sf = fmaf(q[d], kf[d], sf);
+      float lanes[SO_MAX_D / 4];
+      for (int l = 0; l < D / 4; ++l) {
+        float sl = 0.0f;
+        sl = fmaf(q[4 * l + 0], kf[4 * l + 0], sl);
+        sl = fmaf(q[4 * l + 1], kf[4 * l + 1], sl);
+        sl = fmaf(q[4 * l + 2], kf[4 * l + 2], sl);
+        sl = fmaf(q[4 * l + 3], kf[4 * l + 3], sl);
+        lanes[l] = sl;
       }
+      const float sf = lane_tree_down_p(lanes, D / 4);
       scores[r * GH + g] = sf;
       ts->m[g] = fmaxf(ts->m[g], sf);
     }

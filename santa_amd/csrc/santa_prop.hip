@@ -794,8 +794,8 @@ static int check_common(int dtype, int H, int KVH, int D) {
   if (H <= 0 || KVH <= 0) return set_error(SANTA_ERR_INVALID, "empty head dimension");
   if (H % KVH != 0)
     return set_error(SANTA_ERR_INVALID, "H must be divisible by KVH (expected KVH == K_g.size(1) for NHD)");
-  if (D < 16 || D > 256 || D % 16 != 0)
-    return set_error(SANTA_ERR_UNSUPPORTED, "This build supports D a multiple of 16 up to 256 for santa_prop. Got D=%d",
+  if (D < 16 || D > 1024 || D % 16 != 0)
+    return set_error(SANTA_ERR_UNSUPPORTED, "This build supports D a multiple of 16 up to 1024 for santa_prop. Got D=%d",
                      D);
   const int GH = H / KVH;
   if (GH > 16)

@@ -39,10 +39,10 @@ namespace santa {
 namespace propgen {
 
 constexpr int kThreads = 256;
-constexpr int kMaxD = 256;
+constexpr int kMaxD = 1024;
 constexpr int kMaxGH = 16;
 constexpr int kMaxBN = 512;
-constexpr int kRowChunk = 64;  // K rows staged in LDS at a time
+constexpr int kStageElems = 64 * 256;  // 16-bit K elements staged in LDS at a time (64 rows at D <= 256)
 
 bool generic_shape(int GH, int D, int block_n) {
   return !(D == 128 && (GH == 4 || GH == 8) && (block_n == 32 || block_n == 64 || block_n == 256));
@@ -53,28 +53,51 @@ bool shape_supported(int GH, int D, int block_n) {
          block_n <= kMaxBN && block_n % 16 == 0;
 }
 
-// Score of one (row, head) from the rounded q' (floats) and the 16-bit K row.
-template <bool BF16, bool VEC128>
-__device__ __forceinline__ float score(const float* __restrict__ q, const uint16_t* __restrict__ k, int D) {
-  if constexpr (VEC128) {
-    float c[32];
-#pragma unroll
-    for (int v = 0; v < 32; ++v) {
-      float s = fmaf(q[4 * v], h16_to_f32<BF16>(k[4 * v]), 0.0f);
-      s = fmaf(q[4 * v + 1], h16_to_f32<BF16>(k[4 * v + 1]), s);
-      s = fmaf(q[4 * v + 2], h16_to_f32<BF16>(k[4 * v + 2]), s);
-      c[v] = fmaf(q[4 * v + 3], h16_to_f32<BF16>(k[4 * v + 3]), s);
+// Score of one (row, head) from the rounded q' (floats) and the 16-bit K row,
+// in this build's general association: virtual lane v of P = D / 4 chains
+// dims 4v .. 4v+3 with fma, then the shfl_down tree over the P lanes (at
+// offsets N/2, ..., 1, N the next power of two >= P, lane l adds lane l + off
+// when that lane holds a value).  The tree is summed depth first over the
+// lanes in bit-reversed order -- its first pairs are lanes l and l + N/2 --
+// so only log2(N) partial sums are live; float addition commutes, so each
+// pair's sum is the tree's.  For D = 128 this is the vec path's association.
+template <bool BF16>
+__device__ __forceinline__ float score(const uint16_t* __restrict__ q, const uint16_t* __restrict__ k, int D) {
+  const int P = D / 4;
+  int lg = 0;
+  while ((1 << lg) < P) ++lg;
+  const int N = 1 << lg;
+  float st[12];
+  int lv[12];
+  bool pr[12];
+  int sp = 0;
+  for (int i = 0; i < N; ++i) {
+    const int v = lg > 0 ? static_cast<int>(__builtin_bitreverse32(static_cast<uint32_t>(i)) >> (32 - lg)) : 0;
+    bool cp = v < P;
+    float cur = 0.0f;
+    if (cp) {
+      cur = fmaf(h16_to_f32<BF16>(q[4 * v]), h16_to_f32<BF16>(k[4 * v]), 0.0f);
+      cur = fmaf(h16_to_f32<BF16>(q[4 * v + 1]), h16_to_f32<BF16>(k[4 * v + 1]), cur);
+      cur = fmaf(h16_to_f32<BF16>(q[4 * v + 2]), h16_to_f32<BF16>(k[4 * v + 2]), cur);
+      cur = fmaf(h16_to_f32<BF16>(q[4 * v + 3]), h16_to_f32<BF16>(k[4 * v + 3]), cur);
     }
-#pragma unroll
-    for (int off = 16; off > 0; off >>= 1)
-#pragma unroll
-      for (int l = 0; l < off; ++l) c[l] = c[l] + c[l + off];
-    return c[0];
-  } else {
-    float s = 0.0f;
-    for (int d = 0; d < D; ++d) s = fmaf(q[d], h16_to_f32<BF16>(k[d]), s);
-    return s;
+    int lvl = 0;
+    while (sp > 0 && lv[sp - 1] == lvl) {
+      --sp;
+      if (pr[sp] && cp) {
+        cur = st[sp] + cur;
+      } else if (pr[sp]) {
+        cur = st[sp];
+      }
+      cp = cp || pr[sp];
+      ++lvl;
+    }
+    st[sp] = cur;
+    lv[sp] = lvl;
+    pr[sp] = cp;
+    ++sp;
   }
+  return st[0];
 }
 
 // Element offset of token n of sequence b, KV head kv (contiguous or paged).
@@ -91,7 +114,7 @@ __device__ __forceinline__ size_t row_offset(const PageTable& pt, int b, int n, 
 }
 
 // ------------------------------------------------------------------ pass 1
-template <bool BF16, bool VEC128, bool PAGED>
+template <bool BF16, bool PAGED>
 __global__ __launch_bounds__(kThreads) void pass1_kernel(const uint16_t* __restrict__ Q,
                                                          const uint16_t* __restrict__ K, int H, int KVH, int D,
                                                          int BN, int L_valid, int L_storage, int T_c, float q_scale,
@@ -107,8 +130,8 @@ __global__ __launch_bounds__(kThreads) void pass1_kernel(const uint16_t* __restr
   const int h0 = kv * GH;
   const int tid = static_cast<int>(threadIdx.x);
 
-  __shared__ float s_q[kMaxGH * kMaxD];
-  __shared__ uint16_t s_k[kRowChunk * kMaxD];
+  __shared__ uint16_t s_q[kMaxGH * kMaxD];  // q' (already a 16-bit value)
+  __shared__ uint16_t s_k[kStageElems];
   __shared__ float s_sc[kMaxBN * kMaxGH];
   __shared__ int s_mk[kMaxGH * 16];
   __shared__ float s_m[kMaxGH];
@@ -117,11 +140,12 @@ __global__ __launch_bounds__(kThreads) void pass1_kernel(const uint16_t* __restr
   for (int i = tid; i < GH * D; i += kThreads) {
     const int g = i / D, d = i - (i / D) * D;
     const float qv = h16_to_f32<BF16>(Q[(static_cast<size_t>(b) * H + h0 + g) * D + d]) * q_scale;
-    s_q[i] = h16_to_f32<BF16>(f32_to_h16<BF16>(qv));
+    s_q[i] = f32_to_h16<BF16>(qv);
   }
   const int hw = D / 2;  // 4-byte words per row
-  for (int r0 = 0; r0 < len; r0 += kRowChunk) {
-    const int nr = min(kRowChunk, len - r0);
+  const int row_chunk = kStageElems / D;  // K rows staged at a time
+  for (int r0 = 0; r0 < len; r0 += row_chunk) {
+    const int nr = min(row_chunk, len - r0);
     __syncthreads();  // q' written; the previous chunk's rows read
     for (int i = tid; i < nr * hw; i += kThreads) {
       const int r = i / hw, w = i - (i / hw) * hw;
@@ -132,7 +156,7 @@ __global__ __launch_bounds__(kThreads) void pass1_kernel(const uint16_t* __restr
     __syncthreads();
     for (int i = tid; i < nr * GH; i += kThreads) {
       const int r = i / GH, g = i - (i / GH) * GH;
-      s_sc[(r0 + r) * GH + g] = score<BF16, VEC128>(s_q + g * D, s_k + r * D, D);
+      s_sc[(r0 + r) * GH + g] = score<BF16>(s_q + g * D, s_k + r * D, D);
     }
   }
   __syncthreads();
@@ -172,6 +196,221 @@ __global__ __launch_bounds__(kThreads) void pass1_kernel(const uint16_t* __restr
     for (int w = 0; w < nslab; ++w) ell += s_part[tid * nslab + w];
     const size_t mt = (static_cast<size_t>(b) * H + h0 + tid) * T_c + t;
     m_tiles[mt] = s_m[tid];
+    ell_tiles[mt] = ell;
+  }
+}
+
+// ------------------------------------------------------------ fast pass 1
+// block_n 256 with D 64, 128 or 256 and any GH up to 16: one workgroup of
+// four waves per (sequence, KV head, tile), wave w owning rows 64w .. 64w+63,
+// one per lane.  The wave's rows come by 16-byte buffer loads straight into
+// LDS, each lane fetching the piece that lands in the XOR-swizzled slot of its
+// lane index (rows past the tile's end read as zero, with no traffic).  The
+// scores run on the matrix pipe: for 8 dims at a time, v_mfma_f32_4x4x1f32
+// with the A operand broadcast (q of four heads, one dim) and k of the lane's
+// row as B, so each lane accumulates its row's four heads in place; a K=1
+// MFMA is one fused multiply-add.  The chunk results are combined in the
+// general association (virtual lanes of 4 dims, then the shfl_down tree over
+// the D/4 lanes: its even lanes are chunk c's first half and its odd lanes
+// the second, and over chunks the tree pairs c with c + D/16 first).  Then
+// the tile max per head (one LDS exchange), u = exp(s - m), the 16-bit stash
+// [B, L_storage, H] and ell: per 16-row slab in row order (a DPP chain inside
+// each 16-lane row), then over the 16 slabs in order.
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+constexpr int kBufWord3 = 0x00020000;  // raw buffer descriptor word 3 (gfx9 family)
+constexpr int kBufNontemporal = 2;
+
+template <int J>
+__device__ __forceinline__ f32x4 mfma_bc(float a, float b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_4x4x1f32(a, b, c, 4, J, 0);
+}
+
+// Chunk C (dims 8C .. 8C+7) of this lane's row: the fma chains of virtual
+// lanes 2C (e) and 2C+1 (o) for the head block whose broadcast q is qa
+// (register m: dims 16m .. 16m+15, lane 4j+i: head i, dim 16m+j).
+template <bool BF16, int NS, int C>
+__device__ __forceinline__ void fast_leaf(const u32x4* wk, int row, const float* qa, f32x4& e, f32x4& o) {
+  const u32x4 kc = wk[row * NS + (C ^ (row & (NS - 1)))];
+  const float k0 = lo16_to_f32<BF16>(kc.x), k1 = hi16_to_f32<BF16>(kc.x);
+  const float k2 = lo16_to_f32<BF16>(kc.y), k3 = hi16_to_f32<BF16>(kc.y);
+  const float k4 = lo16_to_f32<BF16>(kc.z), k5 = hi16_to_f32<BF16>(kc.z);
+  const float k6 = lo16_to_f32<BF16>(kc.w), k7 = hi16_to_f32<BF16>(kc.w);
+  constexpr int M = C / 2;
+  constexpr int J = 8 * (C % 2);
+  const f32x4 z = {0.0f, 0.0f, 0.0f, 0.0f};
+  const float q = qa[M];
+  f32x4 de = mfma_bc<J + 0>(q, k0, z);
+  f32x4 dd = mfma_bc<J + 4>(q, k4, z);
+  de = mfma_bc<J + 1>(q, k1, de);
+  dd = mfma_bc<J + 5>(q, k5, dd);
+  de = mfma_bc<J + 2>(q, k2, de);
+  dd = mfma_bc<J + 6>(q, k6, dd);
+  de = mfma_bc<J + 3>(q, k3, de);
+  dd = mfma_bc<J + 7>(q, k7, dd);
+  e = de;
+  o = dd;
+}
+
+// The shfl_down tree over the chunks {R, R + S, R + 2S, ...} below NS: the
+// trees over {R, R + 2S, ...} and {R + S, R + 3S, ...} summed (the leaves R
+// and R + NS/2 form the first pairs).
+template <bool BF16, int NS, int R, int S>
+__device__ __forceinline__ void fast_tree(const u32x4* wk, int row, const float* qa, f32x4& e, f32x4& o) {
+  if constexpr (S == NS) {
+    fast_leaf<BF16, NS, R>(wk, row, qa, e, o);
+  } else {
+    f32x4 e1, o1, e2, o2;
+    fast_tree<BF16, NS, R, 2 * S>(wk, row, qa, e1, o1);
+    fast_tree<BF16, NS, R + S, 2 * S>(wk, row, qa, e2, o2);
+    e = e1 + e2;
+    o = o1 + o2;
+    // a scheduling fence after each subtree of four leaves keeps eight MFMA
+    // chains in flight rather than every leaf's accumulators live at once
+    if constexpr (4 * S == NS) __builtin_amdgcn_sched_barrier(0);
+  }
+}
+
+bool fast_pass1_shape(int GH, int D, int block_n) {
+  return block_n == 256 && (D == 64 || D == 128 || D == 256) && GH >= 1 && GH <= kMaxGH;
+}
+
+template <bool BF16, int D, int NHB, bool PAGED>
+__global__ __launch_bounds__(kThreads, 2) void pass1_fast_kernel(const uint16_t* __restrict__ Q,
+                                                                const uint16_t* __restrict__ K, int H, int KVH,
+                                                                int L_valid, int L_storage, int T_c, float q_scale,
+                                                                float* __restrict__ m_tiles,
+                                                                float* __restrict__ ell_tiles,
+                                                                uint16_t* __restrict__ u_stash,
+                                                                const int* __restrict__ seq_lens, int B, PageTable pt) {
+  constexpr int BN = 256;
+  constexpr int NS = D / 8;     // 16-byte slots (8-dim chunks) per K row
+  constexpr int RPL = 64 / NS;  // rows per 64-lane load
+  constexpr int NQ = D / 16;    // broadcast q registers per head block
+  const int GH = H / KVH;
+  const GridPos gp = grid_pos(static_cast<int>(blockIdx.x), seq_lens, B, KVH, BN, L_valid, T_c, 1, T_c);
+  if (gp.b < 0) return;
+  const int b = gp.b, kv = gp.kv, t = gp.chunk;
+  const int n0 = t * BN;
+  const int len = min(BN, gp.len - n0);
+  const int h0 = kv * GH;
+  const int tid = static_cast<int>(threadIdx.x);
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+
+  __shared__ u32x4 s_k[4 * 64 * NS];
+  __shared__ int s_wmax[4][4 * NHB];
+  __shared__ float s_slab[4 * NHB][16];
+  u32x4* const wk = s_k + wave * 64 * NS;
+
+  // this wave's rows n0 + 64 wave .. + 63 into the staging: load i fills
+  // slots 64i .. 64i+63 (rows RPL i .. RPL i + RPL - 1), lane l the piece
+  // (l % NS) ^ (row & (NS - 1)) of row RPL i + l / NS
+  const uint32_t row_bytes = static_cast<uint32_t>(KVH) * D * 2u;
+  const int wrow0 = 64 * wave;
+  const int nrows = min(max(len - wrow0, 0), 64);
+  const int rl = lane / NS, sl = lane % NS;
+#pragma unroll
+  for (int i = 0; i < NS; ++i) {
+    const int nvalid = __builtin_amdgcn_readfirstlane(min(max(nrows - i * RPL, 0), RPL));
+    const int n = n0 + wrow0 + i * RPL;  // first token of the load (RPL tokens lie in one page)
+    size_t base;
+    if constexpr (PAGED) {
+      const int page = __builtin_amdgcn_readfirstlane(page_of_row(pt, b, n, nvalid > 0));
+      base = ((static_cast<size_t>(page) << pt.shift) + static_cast<size_t>(n & ((1 << pt.shift) - 1))) * KVH * D +
+             static_cast<size_t>(kv) * D;
+    } else {
+      base = (static_cast<size_t>(b) * L_storage + n) * KVH * D + static_cast<size_t>(kv) * D;
+    }
+    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint16_t*>(K + base), static_cast<short>(0), nvalid * static_cast<int>(row_bytes), kBufWord3);
+    const uint32_t voff = static_cast<uint32_t>(rl) * row_bytes +
+                          16u * static_cast<uint32_t>(sl ^ ((i * RPL + rl) & (NS - 1)));
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (__attribute__((address_space(3))) void*)(wk + 64 * i), 16, voff, 0,
+                                             0, kBufNontemporal);
+  }
+
+  // q' = TK(f32(q) * scale) of each head block, broadcast layout (heads past
+  // GH are 0 and their results unused)
+  float qa[NHB][NQ];
+#pragma unroll
+  for (int hb = 0; hb < NHB; ++hb) {
+    const int g = 4 * hb + (lane & 3);
+#pragma unroll
+    for (int m = 0; m < NQ; ++m) {
+      float v = 0.0f;
+      if (g < GH) {
+        const float qv = h16_to_f32<BF16>(Q[(static_cast<size_t>(b) * H + h0 + g) * D + 16 * m + (lane >> 2)]) * q_scale;
+        v = h16_to_f32<BF16>(f32_to_h16<BF16>(qv));
+      }
+      qa[hb][m] = v;
+    }
+  }
+  // the loads to LDS are not ordered before LDS reads by the compiler
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __builtin_amdgcn_wave_barrier();
+
+  f32x4 sc[NHB];
+#pragma unroll
+  for (int hb = 0; hb < NHB; ++hb) {
+    f32x4 e, o;
+    fast_tree<BF16, NS, 0, 1>(wk, lane, qa[hb], e, o);
+    sc[hb] = e + o;
+    __builtin_amdgcn_sched_barrier(0);
+  }
+
+  // tile max per head (order keys: exact in any order)
+  const bool valid = wrow0 + lane < len;
+#pragma unroll
+  for (int hb = 0; hb < NHB; ++hb)
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      int key = valid ? order_key(sc[hb][k]) : (-2147483647 - 1);
+      key = wave_max_key_lane63(key);
+      const int wm = __builtin_amdgcn_readlane(key, 63);
+      if (lane == 0) s_wmax[wave][4 * hb + k] = wm;
+    }
+  __syncthreads();
+
+  uint32_t bits[NHB][4];
+  const int slab = 4 * wave + (lane >> 4);
+#pragma unroll
+  for (int hb = 0; hb < NHB; ++hb)
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const int g = 4 * hb + k;
+      const float mg = from_order_key(max(max(s_wmax[0][g], s_wmax[1][g]), max(s_wmax[2][g], s_wmax[3][g])));
+      const float u = valid ? santa_expf_nonpos(sc[hb][k] - mg) : 0.0f;
+      bits[hb][k] = BF16 ? (__float_as_uint(round16_nonneg<true>(u)) >> 16)
+                         : static_cast<uint32_t>(f32_to_h16<false>(u));
+      // the slab's sum in row order at its last lane: ((u0 + u1) + u2) + ...
+      float a = u;
+#pragma unroll
+      for (int j = 1; j < 16; ++j) a = dpp_shr_zero<1>(a) + u;
+      if ((lane & 15) == 15) s_slab[g][slab] = a;
+    }
+  if (valid) {
+    uint16_t* dst = u_stash + (static_cast<size_t>(b) * L_storage + n0 + wrow0 + lane) * H + h0;
+#pragma unroll
+    for (int hb = 0; hb < NHB; ++hb)
+#pragma unroll
+      for (int k = 0; k < 4; k += 2) {
+        const int g = 4 * hb + k;
+        if (GH % 2 == 0) {
+          if (g < GH) *reinterpret_cast<uint32_t*>(dst + g) = bits[hb][k] | (bits[hb][k + 1] << 16);
+        } else {
+          if (g < GH) dst[g] = static_cast<uint16_t>(bits[hb][k]);
+          if (g + 1 < GH) dst[g + 1] = static_cast<uint16_t>(bits[hb][k + 1]);
+        }
+      }
+  }
+  __syncthreads();
+  if (tid < GH) {
+    float ell = 0.0f;
+#pragma unroll
+    for (int w = 0; w < 16; ++w) ell += s_slab[tid][w];
+    const size_t mt = (static_cast<size_t>(b) * H + h0 + tid) * T_c + t;
+    m_tiles[mt] = from_order_key(max(max(s_wmax[0][tid], s_wmax[1][tid]), max(s_wmax[2][tid], s_wmax[3][tid])));
     ell_tiles[mt] = ell;
   }
 }
@@ -480,16 +719,50 @@ hipError_t launch_pass1(const void* q, const void* K, int dtype, int B, int H, i
   const float q_scale = 1.0f / sqrtf(static_cast<float>(D));
   const uint16_t* Qh = static_cast<const uint16_t*>(q);
   const uint16_t* Kh = static_cast<const uint16_t*>(K);
-#define SANTA_GP1(BF, V128, PG)                                                                                     \
-  hipLaunchKernelGGL((pass1_kernel<BF, V128, PG>), dim3(static_cast<unsigned>(grid)), dim3(kThreads), 0, stream, Qh, \
-                     Kh, H, KVH, D, BN, L, L_storage, T_c, q_scale, m_tiles, ell_tiles, u_stash, seq_lens, B, pt)
-  const bool bf = dtype == SANTA_BF16, v128 = D == 128, pg = pt.table != nullptr;
+  const int GH = H / KVH;
+  if (fast_pass1_shape(GH, D, BN)) {
+    // head blocks of four: GH 1-4 -> 1, 5-8 -> 2, 9-16 -> 4
+    const int nhb = GH <= 4 ? 1 : (GH <= 8 ? 2 : 4);
+    const bool bf = dtype == SANTA_BF16, pg = pt.table != nullptr;
+#define SANTA_GF1(BF, DD, NB, PG)                                                                                  \
+  hipLaunchKernelGGL((pass1_fast_kernel<BF, DD, NB, PG>), dim3(static_cast<unsigned>(grid)), dim3(kThreads), 0,    \
+                     stream, Qh, Kh, H, KVH, L, L_storage, T_c, q_scale, m_tiles, ell_tiles, u_stash, seq_lens, B, pt)
+#define SANTA_GF1_NB(BF, DD, PG) \
+  do {                           \
+    if (nhb == 1)                \
+      SANTA_GF1(BF, DD, 1, PG);  \
+    else if (nhb == 2)           \
+      SANTA_GF1(BF, DD, 2, PG);  \
+    else                         \
+      SANTA_GF1(BF, DD, 4, PG);  \
+  } while (0)
+#define SANTA_GF1_D(BF, PG)        \
+  do {                             \
+    if (D == 64)                   \
+      SANTA_GF1_NB(BF, 64, PG);    \
+    else if (D == 128)             \
+      SANTA_GF1_NB(BF, 128, PG);   \
+    else                           \
+      SANTA_GF1_NB(BF, 256, PG);   \
+  } while (0)
+    if (bf) {
+      if (pg) SANTA_GF1_D(true, true); else SANTA_GF1_D(true, false);
+    } else {
+      if (pg) SANTA_GF1_D(false, true); else SANTA_GF1_D(false, false);
+    }
+#undef SANTA_GF1_D
+#undef SANTA_GF1_NB
+#undef SANTA_GF1
+    return hipGetLastError();
+  }
+#define SANTA_GP1(BF, PG)                                                                                          \
+  hipLaunchKernelGGL((pass1_kernel<BF, PG>), dim3(static_cast<unsigned>(grid)), dim3(kThreads), 0, stream, Qh, Kh, \
+                     H, KVH, D, BN, L, L_storage, T_c, q_scale, m_tiles, ell_tiles, u_stash, seq_lens, B, pt)
+  const bool bf = dtype == SANTA_BF16, pg = pt.table != nullptr;
   if (bf) {
-    if (v128) { if (pg) SANTA_GP1(true, true, true); else SANTA_GP1(true, true, false); }
-    else { if (pg) SANTA_GP1(true, false, true); else SANTA_GP1(true, false, false); }
+    if (pg) SANTA_GP1(true, true); else SANTA_GP1(true, false);
   } else {
-    if (v128) { if (pg) SANTA_GP1(false, true, true); else SANTA_GP1(false, true, false); }
-    else { if (pg) SANTA_GP1(false, false, true); else SANTA_GP1(false, false, false); }
+    if (pg) SANTA_GP1(false, true); else SANTA_GP1(false, false);
   }
 #undef SANTA_GP1
   return hipGetLastError();

@@ -131,7 +131,7 @@ def test_compute_entry_points_validate_before_any_launch(lib):
                                      null, null, null, null, null)
     assert rc == ERR_INVALID
     # prop: block_n, D and GH outside the build (any multiple of 16 up to 512,
-    # a multiple of 16 up to 256, at most 16)
+    # a multiple of 16 up to 1024, at most 16)
     for bn in (100, 1024):
         rc = lib.santa_prop_decode(null, null, null, 0, 32, 8, 128, 1000, bn, 1, 8, ctypes.c_uint64(1), null, null,
                                    null, null, ctypes.c_size_t(0), null)
@@ -139,6 +139,13 @@ def test_compute_entry_points_validate_before_any_launch(lib):
     rc = lib.santa_prop_decode(null, null, null, 0, 32, 8, 40, 1000, 64, 1, 8, ctypes.c_uint64(1), null, null, null,
                                null, ctypes.c_size_t(0), null)
     assert rc == ERR_UNSUPPORTED and b"D a multiple of 16" in lib.santa_last_error()
+    rc = lib.santa_prop_decode(null, null, null, 0, 32, 8, 1040, 1000, 64, 1, 8, ctypes.c_uint64(1), null, null, null,
+                               null, ctypes.c_size_t(0), null)
+    assert rc == ERR_UNSUPPORTED and b"up to 1024" in lib.santa_last_error()
+    # D = 512 (above the reference-sized tuned kernels) passes validation
+    rc = lib.santa_prop_decode(null, null, null, 0, 32, 8, 512, 1000, 64, 1, 8, ctypes.c_uint64(1), null, null, null,
+                               null, ctypes.c_size_t(0), null)
+    assert rc == ERR_INVALID and b"null pointer" in lib.santa_last_error()
     rc = lib.santa_prop_decode(null, null, null, 0, 64, 2, 128, 1000, 64, 1, 8, ctypes.c_uint64(1), null, null, null,
                                null, ctypes.c_size_t(0), null)
     assert rc == ERR_UNSUPPORTED and b"GH=32" in lib.santa_last_error()

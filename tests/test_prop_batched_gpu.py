@@ -204,6 +204,8 @@ def test_cfg5_prop_leg_parity():
 @pytest.mark.parametrize("H,KVH,D,lens,Ss,block_n,page_size", [
     (16, 8, 64, [3000, 1700, 2500], [100, 40, 77], 48, 16),
     (32, 2, 128, [900, 2048, 1333, 64], [30, 64, 0, 5], 32, 256),
+    (8, 8, 128, [5000, 3300, 700], [80, 60, 10], 256, 16),     # MHA on the fast generic pass 1, ragged
+    (24, 8, 256, [4100, 2600], [70, 33], 256, 64),             # GH 3, D 256, fast generic pass 1
 ])
 def test_prop_general_batched_and_paged(H, KVH, D, lens, Ss, block_n, page_size, monkeypatch):
     """The generic kernels in the batched, ragged call (one launch sequence over
