@@ -2188,7 +2188,9 @@ hipError_t launch_prop_pass1(const void* q, const void* K, int dtype, int B, int
 }
 
 // Tile chunking shared with santa_prop's pass 2.
-void plan_chunks(int B, int KVH, int T_c, int* cs, int* cpg) { chunk_plan(B, KVH, T_c, cs, cpg); }
+void plan_chunks(int B, int KVH, int T_c, int* cs, int* cpg, int per_round) {
+  chunk_plan(B, KVH, T_c, cs, cpg, per_round);
+}
 
 // The flash tile pass runs its ROWS form (one wave per KV head) for KVH = 8
 // (its LDS is sized for eight waves); its chunks are then planned for one

@@ -83,7 +83,7 @@ hipError_t launch_mfma_check(const float* a, const float* b, const float* c, flo
                              int n_waves, hipStream_t stream);
 // Chunks of cs tiles per workgroup, cpg chunks per (b, kv) group, sized to
 // about one resident round of 256-thread workgroups on the current device.
-void plan_chunks(int B, int KVH, int T_c, int* cs, int* cpg);
+void plan_chunks(int B, int KVH, int T_c, int* cs, int* cpg, int per_round = 0);
 }  // namespace flash
 
 namespace propgen {
@@ -109,6 +109,9 @@ hipError_t launch_pass2(const void* V, const uint16_t* u_stash, int dtype, int B
                         int L_storage, int BN, int T_c, int cs, int cpg, int n_wg, const float* invdelta,
                         const float* a0, int16_t* counts, float* part, int* part_emit, int want_emit,
                         const int* seq_lens, PageTable pt, hipStream_t stream);
+// Waves per generic pass-2 workgroup (one per head, up to four); the chunk
+// plan counts min(GH, 4)-wave workgroups for GH < 4.
+int pass2_waves(int GH);
 hipError_t launch_finalize(const float* part, const int* part_emit, int dtype, int B, int H, int KVH, int D, int cpg,
                            float scale_out, void* out, int* vrows, const int* seq_lens, const int* seq_S, int BN,
                            int cs, int max_rows, int n_wg, hipStream_t stream);

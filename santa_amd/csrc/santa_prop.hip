@@ -741,12 +741,16 @@ struct PropWs {
 static PropWs prop_ws_layout(int B, int H, int KVH, int D, int L_storage, int T_c, long long total_tiles = -1) {
   PropWs w{};
   size_t chunks;
+  // GH < 4 (generic pass 2 with GH-wave workgroups): chunks for as many
+  // resident workgroups as four-wave ones leave room for
+  const int nw = propgen::pass2_waves(H / KVH);
+  const int per_round = nw < 4 ? flash::rows_per_round() / nw : 0;
   if (total_tiles >= 0) {
-    flash::plan_ragged(B, KVH, total_tiles, T_c, &w.cs, &w.n_wg);
+    flash::plan_ragged(B, KVH, total_tiles, T_c, &w.cs, &w.n_wg, per_round);
     w.cpg = 0;
     chunks = static_cast<size_t>(w.n_wg);
   } else {
-    flash::plan_chunks(B, KVH, T_c, &w.cs, &w.cpg);
+    flash::plan_chunks(B, KVH, T_c, &w.cs, &w.cpg, per_round);
     chunks = static_cast<size_t>(B) * KVH * w.cpg;
   }
   const size_t bht = static_cast<size_t>(B) * H * T_c;

@@ -544,10 +544,40 @@ __global__ __launch_bounds__(kBudgetThreads) void budgets_big_kernel(
 }
 
 // ------------------------------------------------------------------ pass 2
-constexpr int kMaxDimsPerLane = kMaxD / 64;
+// One workgroup of NWV = min(GH, 4) waves per (sequence, KV head, chunk of
+// tiles); wave w takes heads w, w + NWV, ... over every tile of the chunk (so
+// no wave idles when GH < 4; the chunk plan then counts the smaller
+// workgroups).  Per (head, tile): x_r = f32(u16 stash) * invdelta_t, the
+// systematic counts (at block_n 256 two rows per lane with the DPP scan of
+// santa_device.h, else 32-row pieces with the lane scan; both the
+// reference's 32-lane Hillis-Steele scan with a sequential carry,
+// :771-807), the sampled rows ascending, and their count-weighted V rows
+// added with one fma per element in row order (:843-857), 16 rows' loads in
+// flight at a time.  Lane l holds dims DPL l .. DPL l + DPL - 1.
+constexpr int kGatherRows = 16;
 constexpr int kMaxHeadsPerWave = kMaxGH / 4;
 
-template <bool BF16, bool PAGED>
+template <int DPL>
+__device__ __forceinline__ void load_dims(const uint16_t* p, uint16_t (&v)[DPL]) {
+  if constexpr (DPL == 1) {
+    v[0] = p[0];
+  } else if constexpr (DPL == 2) {
+    const uint32_t w = *reinterpret_cast<const uint32_t*>(p);
+    v[0] = static_cast<uint16_t>(w & 0xffffu);
+    v[1] = static_cast<uint16_t>(w >> 16);
+  } else {
+#pragma unroll
+    for (int c = 0; c < DPL / 4; ++c) {
+      const uint2 w = reinterpret_cast<const uint2*>(p)[c];
+      v[4 * c] = static_cast<uint16_t>(w.x & 0xffffu);
+      v[4 * c + 1] = static_cast<uint16_t>(w.x >> 16);
+      v[4 * c + 2] = static_cast<uint16_t>(w.y & 0xffffu);
+      v[4 * c + 3] = static_cast<uint16_t>(w.y >> 16);
+    }
+  }
+}
+
+template <bool BF16, bool PAGED, int DPL>
 __global__ __launch_bounds__(kThreads) void pass2_kernel(const uint16_t* __restrict__ V,
                                                          const uint16_t* __restrict__ u_stash, int H, int KVH, int D,
                                                          int BN, int L, int L_storage, int T_c, int cs, int cpg,
@@ -566,32 +596,37 @@ __global__ __launch_bounds__(kThreads) void pass2_kernel(const uint16_t* __restr
   const int t_begin = gp.chunk * cs;
   const int t_end = (gp.b < 0) ? t_begin : min(gp.n_tiles, t_begin + cs);
   const int tid = static_cast<int>(threadIdx.x);
+  const int nthreads = static_cast<int>(blockDim.x);
+  const int nwv = nthreads >> 6;
   const int lane = tid & 63;
-  const int wave = tid >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int jrow = lane >> 4;
+  const int qq = lane & 15;
 
   __shared__ int s_lrow[4][kMaxBN];
   __shared__ float s_lc[4][kMaxBN];
   __shared__ int s_flag[kMaxBN];
   __shared__ int s_nemit;
 
-  float acc[kMaxHeadsPerWave][kMaxDimsPerLane];
+  float acc[kMaxHeadsPerWave][DPL];
 #pragma unroll
   for (int k = 0; k < kMaxHeadsPerWave; ++k)
 #pragma unroll
-    for (int j = 0; j < kMaxDimsPerLane; ++j) acc[k][j] = 0.0f;
+    for (int j = 0; j < DPL; ++j) acc[k][j] = 0.0f;
   int emit_total = 0;
   const uint16_t* ub = u_stash + static_cast<size_t>(b) * L_storage * H;
+  const int d0 = DPL * lane;  // this lane's first dim
 
   for (int t = t_begin; t < t_end; ++t) {
     const int n0 = t * BN;
     const int len = min(BN, L - n0);
     if (want_emit) {
-      for (int r = tid; r < BN; r += kThreads) s_flag[r] = 0;
+      for (int r = tid; r < BN; r += nthreads) s_flag[r] = 0;
       __syncthreads();
     }
 #pragma unroll
     for (int k = 0; k < kMaxHeadsPerWave; ++k) {
-      const int g = wave + 4 * k;
+      const int g = wave + nwv * k;
       if (g >= GH) break;
       const int h = h0 + g;
       const size_t ht = (static_cast<size_t>(b) * H + h) * T_c + t;
@@ -603,49 +638,99 @@ __global__ __launch_bounds__(kThreads) void pass2_kernel(const uint16_t* __restr
           for (int r = lane; r < BN; r += 64) dbg_counts[ht * BN + r] = 0;
         continue;
       }
-      float carry = 0.0f;
       int lc = 0;
-      for (int base = 0; base < len; base += 32) {
-        const int r = base + lane;
-        const bool in = lane < 32 && r < len;
-        const float x = (in && inv > 0.0f) ? h16_to_f32<BF16>(ub[static_cast<size_t>(n0 + r) * H + h]) * inv : 0.0f;
-        // Hillis-Steele inclusive scan over 32 lanes, then res - x
-        // (flash/santa_cuda_kernel.cu:60-69)
-        float res = x;
+      if (BN == 256) {
+        // two rows per lane: rows 32 (4p + j) + 2q (x0) and + 1 (x1) at lane 16j + q
+        float x0[2], x1[2];
 #pragma unroll
-        for (int off = 1; off < 32; off <<= 1) {
-          const float o = __shfl_up(res, off, 32);
-          res = ((lane & 31) >= off) ? res + o : res;
+        for (int p = 0; p < 2; ++p) {
+          const int row = 32 * (4 * p + jrow) + 2 * qq;
+          x0[p] = (row < len) ? h16_to_f32<BF16>(ub[static_cast<size_t>(n0 + row) * H + h]) * inv : 0.0f;
+          x1[p] = (row + 1 < len) ? h16_to_f32<BF16>(ub[static_cast<size_t>(n0 + row + 1) * H + h]) * inv : 0.0f;
         }
-        const float pre = res - x;
-        const float pre_g = carry + pre;
-        const float cum_g = pre_g + x;
-        const int c = in ? count_from_floors(a0, pre_g, cum_g) : 0;
-        const int last = min(31, len - base - 1);
-        const float chunk_total = __shfl(pre + x, last, 64);
-        carry = carry + chunk_total;
-        if (dbg_counts && lane < 32 && r < BN) dbg_counts[ht * BN + r] = static_cast<int16_t>(c);
-        const uint64_t nz = __ballot(c != 0);
-        if (c != 0) {
-          const int pos = lc + __popcll(nz & ((1ull << lane) - 1ull));
-          s_lrow[wave][pos] = n0 + r;
-          s_lc[wave][pos] = static_cast<float>(c);
-          if (want_emit) s_flag[r] = 1;
+        int c0[2], c1[2];
+        systematic_counts<8>(x0, x1, len, a0, lane, c0, c1);
+        const uint64_t below = (1ull << lane) - 1ull;
+#pragma unroll
+        for (int p = 0; p < 2; ++p) {
+          const int row = 32 * (4 * p + jrow) + 2 * qq;
+          if (dbg_counts) {
+            dbg_counts[ht * BN + row] = static_cast<int16_t>(c0[p]);
+            dbg_counts[ht * BN + row + 1] = static_cast<int16_t>(c1[p]);
+          }
+          const uint64_t nz0 = __ballot(c0[p] != 0), nz1 = __ballot(c1[p] != 0);
+          const int pos0 = lc + __popcll(nz0 & below) + __popcll(nz1 & below);
+          const int pos1 = pos0 + (c0[p] != 0 ? 1 : 0);
+          if (c0[p] != 0) {
+            s_lrow[wave][pos0] = n0 + row;
+            s_lc[wave][pos0] = static_cast<float>(c0[p]);
+            if (want_emit) s_flag[row] = 1;
+          }
+          if (c1[p] != 0) {
+            s_lrow[wave][pos1] = n0 + row + 1;
+            s_lc[wave][pos1] = static_cast<float>(c1[p]);
+            if (want_emit) s_flag[row + 1] = 1;
+          }
+          lc += __popcll(nz0) + __popcll(nz1);
         }
-        lc += __popcll(nz);
+      } else {
+        float carry = 0.0f;
+        for (int base = 0; base < len; base += 32) {
+          const int r = base + lane;
+          const bool in = lane < 32 && r < len;
+          const float x = in ? h16_to_f32<BF16>(ub[static_cast<size_t>(n0 + r) * H + h]) * inv : 0.0f;
+          // Hillis-Steele inclusive scan over 32 lanes, then res - x
+          // (flash/santa_cuda_kernel.cu:60-69)
+          float res = x;
+#pragma unroll
+          for (int off = 1; off < 32; off <<= 1) {
+            const float o = __shfl_up(res, off, 32);
+            res = ((lane & 31) >= off) ? res + o : res;
+          }
+          const float pre = res - x;
+          const float pre_g = carry + pre;
+          const float cum_g = pre_g + x;
+          const int c = in ? count_from_floors(a0, pre_g, cum_g) : 0;
+          const int last = min(31, len - base - 1);
+          const float chunk_total = __shfl(pre + x, last, 64);
+          carry = carry + chunk_total;
+          if (dbg_counts && lane < 32 && r < BN) dbg_counts[ht * BN + r] = static_cast<int16_t>(c);
+          const uint64_t nz = __ballot(c != 0);
+          if (c != 0) {
+            const int pos = lc + __popcll(nz & ((1ull << lane) - 1ull));
+            s_lrow[wave][pos] = n0 + r;
+            s_lc[wave][pos] = static_cast<float>(c);
+            if (want_emit) s_flag[r] = 1;
+          }
+          lc += __popcll(nz);
+        }
+        if (dbg_counts)
+          for (int r = ((len + 31) / 32) * 32 + lane; r < BN; r += 64) dbg_counts[ht * BN + r] = 0;
       }
-      if (dbg_counts)
-        for (int r = ((len + 31) / 32) * 32 + lane; r < BN; r += 64) dbg_counts[ht * BN + r] = 0;
       __builtin_amdgcn_wave_barrier();
-      // count-weighted V rows, rows ascending, one fma per element
-      for (int i = 0; i < lc; ++i) {
-        const int row = __builtin_amdgcn_readfirstlane(s_lrow[wave][i]);
-        const float cf = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(s_lc[wave][i])));
-        const uint16_t* vr = V + row_offset<PAGED>(pt, b, row, kv, KVH, D, L_storage);
+      // count-weighted V rows, rows ascending, one fma per element; the loads
+      // of up to 16 rows go out before the first is used
+      for (int i0 = 0; i0 < lc; i0 += kGatherRows) {
+        uint16_t vv[kGatherRows][DPL];
+        float cf[kGatherRows];
 #pragma unroll
-        for (int j = 0; j < kMaxDimsPerLane; ++j) {
-          const int d = lane + 64 * j;
-          if (d < D) acc[k][j] = fmaf(cf, h16_to_f32<BF16>(vr[d]), acc[k][j]);
+        for (int q = 0; q < kGatherRows; ++q) {
+          const int i = min(i0 + q, lc - 1);
+          const int row = __builtin_amdgcn_readfirstlane(s_lrow[wave][i]);
+          cf[q] = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(s_lc[wave][i])));
+          if (d0 < D) {
+            load_dims<DPL>(V + row_offset<PAGED>(pt, b, row, kv, KVH, D, L_storage) + d0, vv[q]);
+          } else {
+#pragma unroll
+            for (int j = 0; j < DPL; ++j) vv[q][j] = 0;
+          }
+        }
+#pragma unroll
+        for (int q = 0; q < kGatherRows; ++q) {
+          if (i0 + q < lc) {
+#pragma unroll
+            for (int j = 0; j < DPL; ++j) acc[k][j] = fmaf(cf[q], h16_to_f32<BF16>(vv[q][j]), acc[k][j]);
+          }
         }
       }
       __builtin_amdgcn_wave_barrier();
@@ -664,16 +749,18 @@ __global__ __launch_bounds__(kThreads) void pass2_kernel(const uint16_t* __restr
   }
 #pragma unroll
   for (int k = 0; k < kMaxHeadsPerWave; ++k) {
-    const int g = wave + 4 * k;
+    const int g = wave + nwv * k;
     if (g >= GH) break;
+    if (d0 < D) {
 #pragma unroll
-    for (int j = 0; j < kMaxDimsPerLane; ++j) {
-      const int d = lane + 64 * j;
-      if (d < D) part[(static_cast<size_t>(wg) * GH + g) * D + d] = acc[k][j];
+      for (int j = 0; j < DPL; ++j) part[(static_cast<size_t>(wg) * GH + g) * D + d0 + j] = acc[k][j];
     }
   }
   if (tid == 0) part_emit[wg] = emit_total;
 }
+
+// Waves per pass-2 workgroup: one per head up to four.
+int pass2_waves(int GH) { return GH < 4 ? GH : 4; }
 
 // ---------------------------------------------------------------- finalize
 template <bool BF16>
@@ -784,15 +871,31 @@ hipError_t launch_pass2(const void* V, const uint16_t* u_stash, int dtype, int B
   const long long grid = seq_lens ? n_wg : static_cast<long long>(B) * KVH * cpg;
   if (grid <= 0) return hipSuccess;
   const uint16_t* Vh = static_cast<const uint16_t*>(V);
-#define SANTA_GP2(BF, PG)                                                                                          \
-  hipLaunchKernelGGL((pass2_kernel<BF, PG>), dim3(static_cast<unsigned>(grid)), dim3(kThreads), 0, stream, Vh,      \
-                     u_stash, H, KVH, D, BN, L, L_storage, T_c, cs, cpg, invdelta, a0, counts, part, part_emit,     \
+  const unsigned threads = static_cast<unsigned>(64 * pass2_waves(H / KVH));
+  const int dpl = D <= 64 ? 1 : (D <= 128 ? 2 : (D <= 256 ? 4 : (D <= 512 ? 8 : 16)));
+#define SANTA_GP2(BF, PG, DP)                                                                                       \
+  hipLaunchKernelGGL((pass2_kernel<BF, PG, DP>), dim3(static_cast<unsigned>(grid)), dim3(threads), 0, stream, Vh,    \
+                     u_stash, H, KVH, D, BN, L, L_storage, T_c, cs, cpg, invdelta, a0, counts, part, part_emit,      \
                      want_emit, seq_lens, B, pt)
+#define SANTA_GP2_D(BF, PG)      \
+  do {                           \
+    if (dpl == 1)                \
+      SANTA_GP2(BF, PG, 1);      \
+    else if (dpl == 2)           \
+      SANTA_GP2(BF, PG, 2);      \
+    else if (dpl == 4)           \
+      SANTA_GP2(BF, PG, 4);      \
+    else if (dpl == 8)           \
+      SANTA_GP2(BF, PG, 8);      \
+    else                         \
+      SANTA_GP2(BF, PG, 16);     \
+  } while (0)
   if (dtype == SANTA_BF16) {
-    if (pt.table) SANTA_GP2(true, true); else SANTA_GP2(true, false);
+    if (pt.table) SANTA_GP2_D(true, true); else SANTA_GP2_D(true, false);
   } else {
-    if (pt.table) SANTA_GP2(false, true); else SANTA_GP2(false, false);
+    if (pt.table) SANTA_GP2_D(false, true); else SANTA_GP2_D(false, false);
   }
+#undef SANTA_GP2_D
 #undef SANTA_GP2
   return hipGetLastError();
 }
