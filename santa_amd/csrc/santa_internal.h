@@ -94,10 +94,13 @@ namespace propgen {
 bool generic_shape(int GH, int D, int block_n);
 bool shape_supported(int GH, int D, int block_n);
 // Pass 1 (general numerics): m, ell [B, H, T_c] and the stash [B, L_storage,
-// H]; ragged with seq_lens (L the longest) over total_tiles tiles.
+// H], or tile-major [B, stash_ld / 256, H, 256] when stash_ld > 0 (only for
+// fast_pass1_shape); ragged with seq_lens (L the longest) over total_tiles
+// tiles.
+bool fast_pass1_shape(int GH, int D, int block_n);
 hipError_t launch_pass1(const void* q, const void* K, int dtype, int B, int H, int KVH, int D, int L, int L_storage,
                         int BN, float* m_tiles, float* ell_tiles, uint16_t* u_stash, const int* seq_lens,
-                        long long total_tiles, PageTable pt, hipStream_t stream);
+                        long long total_tiles, PageTable pt, hipStream_t stream, int stash_ld = 0);
 // The budgets for any tile count (one workgroup per (b, h), BH of them).
 hipError_t launch_budgets_big(const float* m_tiles, const float* ell_tiles, int BH, int H, int T_c, int S,
                               uint64_t seed, float* m_star, int* S_tiles, float* invdelta, float* a0,
@@ -108,7 +111,7 @@ hipError_t launch_budgets_big(const float* m_tiles, const float* ell_tiles, int 
 hipError_t launch_pass2(const void* V, const uint16_t* u_stash, int dtype, int B, int H, int KVH, int D, int L,
                         int L_storage, int BN, int T_c, int cs, int cpg, int n_wg, const float* invdelta,
                         const float* a0, int16_t* counts, float* part, int* part_emit, int want_emit,
-                        const int* seq_lens, PageTable pt, hipStream_t stream);
+                        const int* seq_lens, PageTable pt, hipStream_t stream, int stash_ld = 0);
 // Waves per generic pass-2 workgroup (one per head, up to four); the chunk
 // plan counts min(GH, 4)-wave workgroups for GH < 4.
 int pass2_waves(int GH);

@@ -920,7 +920,7 @@ static int prop_pass2_launch(const void* V, const uint16_t* u_stash, int dtype, 
   hipError_t e;
   if (propgen::generic_shape(GH, D, block_n)) {
     e = propgen::launch_pass2(V, u_stash, dtype, B, H, KVH, D, L, L_storage, block_n, T_c, w.cs, w.cpg, w.n_wg,
-                              invdelta, a0, counts, part, pe, want_emit, seq_lens, pt, stream);
+                              invdelta, a0, counts, part, pe, want_emit, seq_lens, pt, stream, stash_ld);
     if (e != hipSuccess) return set_error(SANTA_ERR_HIP, "pass-2 launch failed: %s", hipGetErrorString(e));
     e = propgen::launch_finalize(part, pe, dtype, B, H, KVH, D, w.cpg, scale_out, out, vrows, seq_lens, seq_S,
                                  block_n, w.cs, L, w.n_wg, stream);
@@ -1011,10 +1011,12 @@ extern "C" int santa_prop_decode(const void* q, const void* K, const void* V, in
   // a pass 1 on the wave kernel (the vec path, the general path at GH 8)
   // keeps the stash tile-major between the two passes, except for a small
   // pass, which runs four waves per tile with the [L, H] stash
+  // (the generic path keeps it tile-major too wherever its fast pass 1 runs)
   const bool small = flash::small_prop_pass(static_cast<long long>(T_c) * KVH);
-  const int sld = (!gen && flash::prop_wave_pass1(pass1_path, H / KVH, block_n) && !small) ? prop::stash_ld(L) : 0;
+  const int sld = gen ? (propgen::fast_pass1_shape(H / KVH, D, block_n) ? prop::stash_ld(L) : 0)
+                      : ((flash::prop_wave_pass1(pass1_path, H / KVH, block_n) && !small) ? prop::stash_ld(L) : 0);
   hipError_t e = gen ? propgen::launch_pass1(q, K, dtype, 1, H, KVH, D, L, L, block_n, m_tiles, ell_tiles, stash,
-                                             nullptr, -1, PageTable{nullptr, 0, 3, 1}, stream)
+                                             nullptr, -1, PageTable{nullptr, 0, 3, 1}, stream, sld)
                      : flash::launch_prop_pass1(q, K, dtype, 1, H, KVH, L, L, block_n, pass1_path, m_tiles, ell_tiles,
                                                 stash, nullptr, 0, 0, sld, stream);
   if (e != hipSuccess) return set_error(SANTA_ERR_HIP, "pass-1 launch failed: %s", hipGetErrorString(e));
@@ -1066,9 +1068,10 @@ static int prop_decode_batched(const void* q, const void* K, const void* V, int 
   const bool gen = propgen::generic_shape(H / KVH, D, block_n);
   const bool small = !pt.table && flash::small_prop_pass(total_tiles * KVH);  // as in the scalar call
   const int sld =
-      (!gen && flash::prop_wave_pass1(pass1_path, H / KVH, block_n) && !small) ? prop::stash_ld(L_storage) : 0;
+      gen ? (propgen::fast_pass1_shape(H / KVH, D, block_n) ? prop::stash_ld(L_storage) : 0)
+          : ((flash::prop_wave_pass1(pass1_path, H / KVH, block_n) && !small) ? prop::stash_ld(L_storage) : 0);
   hipError_t e = gen ? propgen::launch_pass1(q, K, dtype, B, H, KVH, D, max_len, L_storage, block_n, m_tiles,
-                                             ell_tiles, stash, seq_lens, total_tiles, pt, stream)
+                                             ell_tiles, stash, seq_lens, total_tiles, pt, stream, sld)
                      : flash::launch_prop_pass1(q, K, dtype, B, H, KVH, max_len, L_storage, block_n, pass1_path,
                                                 m_tiles, ell_tiles, stash, seq_lens, w.cs, w.n_wg, sld, stream, pt,
                                                 total_tiles);

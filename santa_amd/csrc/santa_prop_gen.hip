@@ -275,59 +275,95 @@ bool fast_pass1_shape(int GH, int D, int block_n) {
   return block_n == 256 && (D == 64 || D == 128 || D == 256) && GH >= 1 && GH <= kMaxGH;
 }
 
+// Workgroups per CU of pass1_fast_kernel: its LDS staging (64 rows of D
+// 16-bit values per wave) allows two at D <= 128; D = 256, and four head
+// blocks (whose scores, exps and the next tile's rows need more than half the
+// registers), take one.
+template <int D, int NHB>
+constexpr int fast_occupancy() {
+  return (D == 256 || (D == 128 && NHB == 4)) ? 1 : 2;
+}
+// Whether the next tile's rows are held in registers while a tile is scored
+// (D / 2 registers); the wider shapes load each tile straight into the
+// staging instead, and rely on the other resident workgroup to cover the wait.
+template <int D, int NHB>
+constexpr bool fast_prefetch() {
+  return NHB == 1 || (D == 64 && NHB == 2);
+}
+
 template <bool BF16, int D, int NHB, bool PAGED>
-__global__ __launch_bounds__(kThreads, 2) void pass1_fast_kernel(const uint16_t* __restrict__ Q,
-                                                                const uint16_t* __restrict__ K, int H, int KVH,
-                                                                int L_valid, int L_storage, int T_c, float q_scale,
-                                                                float* __restrict__ m_tiles,
-                                                                float* __restrict__ ell_tiles,
-                                                                uint16_t* __restrict__ u_stash,
-                                                                const int* __restrict__ seq_lens, int B, PageTable pt) {
+__global__ __launch_bounds__(kThreads, (fast_occupancy<D, NHB>())) void pass1_fast_kernel(
+    const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K, int H, int KVH, int L_valid, int L_storage,
+    int T_c, int cs, int cpg, float q_scale, float* __restrict__ m_tiles, float* __restrict__ ell_tiles,
+    uint16_t* __restrict__ u_stash, const int* __restrict__ seq_lens, int B, PageTable pt, int stash_ld) {
   constexpr int BN = 256;
   constexpr int NS = D / 8;     // 16-byte slots (8-dim chunks) per K row
   constexpr int RPL = 64 / NS;  // rows per 64-lane load
   constexpr int NQ = D / 16;    // broadcast q registers per head block
   const int GH = H / KVH;
-  const GridPos gp = grid_pos(static_cast<int>(blockIdx.x), seq_lens, B, KVH, BN, L_valid, T_c, 1, T_c);
+  // one (sequence, KV head, chunk of cs tiles) per workgroup
+  const GridPos gp = grid_pos(static_cast<int>(blockIdx.x), seq_lens, B, KVH, BN, L_valid, T_c, cs, cpg);
   if (gp.b < 0) return;
-  const int b = gp.b, kv = gp.kv, t = gp.chunk;
-  const int n0 = t * BN;
-  const int len = min(BN, gp.len - n0);
+  const int b = gp.b, kv = gp.kv;
+  const int t_begin = gp.chunk * cs;
+  const int t_end = min(gp.n_tiles, t_begin + cs);
   const int h0 = kv * GH;
   const int tid = static_cast<int>(threadIdx.x);
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
 
   __shared__ u32x4 s_k[4 * 64 * NS];
-  __shared__ int s_wmax[4][4 * NHB];
-  __shared__ float s_slab[4 * NHB][16];
+  __shared__ int s_wmax[2][4][4 * NHB];      // by tile parity: the next tile's writes
+  __shared__ float s_slab[2][4 * NHB][16];   // never meet this tile's late reads
   u32x4* const wk = s_k + wave * 64 * NS;
 
-  // this wave's rows n0 + 64 wave .. + 63 into the staging: load i fills
-  // slots 64i .. 64i+63 (rows RPL i .. RPL i + RPL - 1), lane l the piece
-  // (l % NS) ^ (row & (NS - 1)) of row RPL i + l / NS
+  // This wave's rows n0 + 64 wave .. + 63 of a tile, register form: load i
+  // holds rows RPL i .. RPL i + RPL - 1, lane l the piece (l % NS) ^ (row &
+  // (NS - 1)) of row RPL i + l / NS, which is the staging slot 64 i + l
+  // (rows past the tile's end read as zero, with no traffic).  The next
+  // tile's loads are in flight while this one is scored.
   const uint32_t row_bytes = static_cast<uint32_t>(KVH) * D * 2u;
   const int wrow0 = 64 * wave;
-  const int nrows = min(max(len - wrow0, 0), 64);
-  const int rl = lane / NS, sl = lane % NS;
+  constexpr bool PF = fast_prefetch<D, NHB>();
+  u32x4 kw[PF ? NS : 1];
+  // one load of this wave's rows of tile t: to registers (PF) or straight
+  // into the staging
+  auto load_rows = [&](int t) {
+    // the lane index through an empty asm, so that the per-load offsets are
+    // recomputed at each tile rather than held in registers across the loop
+    int l = lane;
+    asm volatile("" : "+v"(l));
+    const int rl = l / NS, sl = l % NS;
+    const int n0 = t * BN;
+    const int nrows = min(max(min(BN, gp.len - n0) - wrow0, 0), 64);
 #pragma unroll
-  for (int i = 0; i < NS; ++i) {
-    const int nvalid = __builtin_amdgcn_readfirstlane(min(max(nrows - i * RPL, 0), RPL));
-    const int n = n0 + wrow0 + i * RPL;  // first token of the load (RPL tokens lie in one page)
-    size_t base;
-    if constexpr (PAGED) {
-      const int page = __builtin_amdgcn_readfirstlane(page_of_row(pt, b, n, nvalid > 0));
-      base = ((static_cast<size_t>(page) << pt.shift) + static_cast<size_t>(n & ((1 << pt.shift) - 1))) * KVH * D +
-             static_cast<size_t>(kv) * D;
-    } else {
-      base = (static_cast<size_t>(b) * L_storage + n) * KVH * D + static_cast<size_t>(kv) * D;
+    for (int i = 0; i < NS; ++i) {
+      const int nvalid = __builtin_amdgcn_readfirstlane(min(max(nrows - i * RPL, 0), RPL));
+      const int n = n0 + wrow0 + i * RPL;  // first token of the load (RPL tokens lie in one page)
+      size_t base;
+      if constexpr (PAGED) {
+        const int page = __builtin_amdgcn_readfirstlane(page_of_row(pt, b, n, nvalid > 0));
+        base = ((static_cast<size_t>(page) << pt.shift) + static_cast<size_t>(n & ((1 << pt.shift) - 1))) * KVH * D +
+               static_cast<size_t>(kv) * D;
+      } else {
+        base = (static_cast<size_t>(b) * L_storage + n) * KVH * D + static_cast<size_t>(kv) * D;
+      }
+      const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+          const_cast<uint16_t*>(K + base), static_cast<short>(0), nvalid * static_cast<int>(row_bytes), kBufWord3);
+      const uint32_t voff = static_cast<uint32_t>(rl) * row_bytes +
+                            16u * static_cast<uint32_t>(sl ^ ((i * RPL + rl) & (NS - 1)));
+      if constexpr (PF) {
+        kw[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rs, voff, 0, kBufNontemporal));
+      } else {
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (__attribute__((address_space(3))) void*)(wk + 64 * i), 16, voff,
+                                                 0, 0, kBufNontemporal);
+      }
     }
-    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
-        const_cast<uint16_t*>(K + base), static_cast<short>(0), nvalid * static_cast<int>(row_bytes), kBufWord3);
-    const uint32_t voff = static_cast<uint32_t>(rl) * row_bytes +
-                          16u * static_cast<uint32_t>(sl ^ ((i * RPL + rl) & (NS - 1)));
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (__attribute__((address_space(3))) void*)(wk + 64 * i), 16, voff, 0,
-                                             0, kBufNontemporal);
+  };
+  if constexpr (PF) {
+    load_rows(t_begin);
+  } else {
+    load_rows(t_begin);  // one tile per workgroup: its rows first, then q
   }
 
   // q' = TK(f32(q) * scale) of each head block, broadcast layout (heads past
@@ -346,72 +382,108 @@ __global__ __launch_bounds__(kThreads, 2) void pass1_fast_kernel(const uint16_t*
       qa[hb][m] = v;
     }
   }
-  // the loads to LDS are not ordered before LDS reads by the compiler
-  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-  __builtin_amdgcn_wave_barrier();
 
-  f32x4 sc[NHB];
-#pragma unroll
-  for (int hb = 0; hb < NHB; ++hb) {
-    f32x4 e, o;
-    fast_tree<BF16, NS, 0, 1>(wk, lane, qa[hb], e, o);
-    sc[hb] = e + o;
-    __builtin_amdgcn_sched_barrier(0);
-  }
-
-  // tile max per head (order keys: exact in any order)
-  const bool valid = wrow0 + lane < len;
-#pragma unroll
-  for (int hb = 0; hb < NHB; ++hb)
-#pragma unroll
-    for (int k = 0; k < 4; ++k) {
-      int key = valid ? order_key(sc[hb][k]) : (-2147483647 - 1);
-      key = wave_max_key_lane63(key);
-      const int wm = __builtin_amdgcn_readlane(key, 63);
-      if (lane == 0) s_wmax[wave][4 * hb + k] = wm;
-    }
-  __syncthreads();
-
-  uint32_t bits[NHB][4];
   const int slab = 4 * wave + (lane >> 4);
+  auto tile = [&](int t) {
+    const int par = (t - t_begin) & 1;
+    const int n0 = t * BN;
+    const int len = min(BN, gp.len - n0);
+    if constexpr (PF) {
+      // the tile's rows into this wave's staging (its previous reads are
+      // done: LDS accesses of one wave complete in order), then the next
+      // tile's loads
 #pragma unroll
-  for (int hb = 0; hb < NHB; ++hb)
-#pragma unroll
-    for (int k = 0; k < 4; ++k) {
-      const int g = 4 * hb + k;
-      const float mg = from_order_key(max(max(s_wmax[0][g], s_wmax[1][g]), max(s_wmax[2][g], s_wmax[3][g])));
-      const float u = valid ? santa_expf_nonpos(sc[hb][k] - mg) : 0.0f;
-      bits[hb][k] = BF16 ? (__float_as_uint(round16_nonneg<true>(u)) >> 16)
-                         : static_cast<uint32_t>(f32_to_h16<false>(u));
-      // the slab's sum in row order at its last lane: ((u0 + u1) + u2) + ...
-      float a = u;
-#pragma unroll
-      for (int j = 1; j < 16; ++j) a = dpp_shr_zero<1>(a) + u;
-      if ((lane & 15) == 15) s_slab[g][slab] = a;
+      for (int i = 0; i < NS; ++i) wk[64 * i + lane] = kw[i];
+      if (t + 1 < t_end) load_rows(t + 1);
+    } else {
+      // (the loads to LDS are not ordered before LDS reads by the compiler)
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     }
-  if (valid) {
-    uint16_t* dst = u_stash + (static_cast<size_t>(b) * L_storage + n0 + wrow0 + lane) * H + h0;
+    __builtin_amdgcn_wave_barrier();
+
+    // (the row through an empty asm: the staging addresses are recomputed at
+    // each tile rather than held in registers across the loop)
+    int row = lane;
+    asm volatile("" : "+v"(row));
+    f32x4 sc[NHB];
+#pragma unroll
+    for (int hb = 0; hb < NHB; ++hb) {
+      f32x4 e, o;
+      fast_tree<BF16, NS, 0, 1>(wk, row, qa[hb], e, o);
+      sc[hb] = e + o;
+      __builtin_amdgcn_sched_barrier(0);
+    }
+
+    // tile max per head (order keys: exact in any order)
+    const bool valid = wrow0 + lane < len;
 #pragma unroll
     for (int hb = 0; hb < NHB; ++hb)
 #pragma unroll
-      for (int k = 0; k < 4; k += 2) {
-        const int g = 4 * hb + k;
-        if (GH % 2 == 0) {
-          if (g < GH) *reinterpret_cast<uint32_t*>(dst + g) = bits[hb][k] | (bits[hb][k + 1] << 16);
-        } else {
-          if (g < GH) dst[g] = static_cast<uint16_t>(bits[hb][k]);
-          if (g + 1 < GH) dst[g + 1] = static_cast<uint16_t>(bits[hb][k + 1]);
-        }
+      for (int k = 0; k < 4; ++k) {
+        int key = valid ? order_key(sc[hb][k]) : (-2147483647 - 1);
+        key = wave_max_key_lane63(key);
+        const int wm = __builtin_amdgcn_readlane(key, 63);
+        if (lane == 0) s_wmax[par][wave][4 * hb + k] = wm;
       }
-  }
-  __syncthreads();
-  if (tid < GH) {
-    float ell = 0.0f;
+    __syncthreads();
+
+    uint32_t bits[NHB][4];
 #pragma unroll
-    for (int w = 0; w < 16; ++w) ell += s_slab[tid][w];
-    const size_t mt = (static_cast<size_t>(b) * H + h0 + tid) * T_c + t;
-    m_tiles[mt] = from_order_key(max(max(s_wmax[0][tid], s_wmax[1][tid]), max(s_wmax[2][tid], s_wmax[3][tid])));
-    ell_tiles[mt] = ell;
+    for (int hb = 0; hb < NHB; ++hb)
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const int g = 4 * hb + k;
+        const float mg = from_order_key(max(max(s_wmax[par][0][g], s_wmax[par][1][g]),
+                                            max(s_wmax[par][2][g], s_wmax[par][3][g])));
+        const float u = valid ? santa_expf_nonpos(sc[hb][k] - mg) : 0.0f;
+        bits[hb][k] = BF16 ? (__float_as_uint(round16_nonneg<true>(u)) >> 16)
+                           : static_cast<uint32_t>(f32_to_h16<false>(u));
+        // the slab's sum in row order at its last lane: ((u0 + u1) + u2) + ...
+        float a = u;
+#pragma unroll
+        for (int j = 1; j < 16; ++j) a = dpp_shr_zero<1>(a) + u;
+        if ((lane & 15) == 15) s_slab[par][g][slab] = a;
+      }
+    if (stash_ld > 0) {
+      // tile-major [B, T, H, 256]: per head the wave's 64 rows as one 128-B
+      // run (0 past len), where [L, H] would scatter 2-B pieces H * 2 B apart
+      uint16_t* dst = u_stash + static_cast<size_t>(b) * H * stash_ld + (static_cast<size_t>(t) * H + h0) * BN +
+                      wrow0 + lane;
+#pragma unroll
+      for (int hb = 0; hb < NHB; ++hb)
+#pragma unroll
+        for (int k = 0; k < 4; ++k)
+          if (4 * hb + k < GH) dst[(4 * hb + k) * BN] = static_cast<uint16_t>(bits[hb][k]);
+    } else if (valid) {
+      uint16_t* dst = u_stash + (static_cast<size_t>(b) * L_storage + n0 + wrow0 + lane) * H + h0;
+#pragma unroll
+      for (int hb = 0; hb < NHB; ++hb)
+#pragma unroll
+        for (int k = 0; k < 4; k += 2) {
+          const int g = 4 * hb + k;
+          if (GH % 2 == 0) {
+            if (g < GH) *reinterpret_cast<uint32_t*>(dst + g) = bits[hb][k] | (bits[hb][k + 1] << 16);
+          } else {
+            if (g < GH) dst[g] = static_cast<uint16_t>(bits[hb][k]);
+            if (g + 1 < GH) dst[g + 1] = static_cast<uint16_t>(bits[hb][k + 1]);
+          }
+        }
+    }
+    __syncthreads();
+    if (tid < GH) {
+      float ell = 0.0f;
+#pragma unroll
+      for (int w = 0; w < 16; ++w) ell += s_slab[par][tid][w];
+      const size_t mt = (static_cast<size_t>(b) * H + h0 + tid) * T_c + t;
+      m_tiles[mt] = from_order_key(max(max(s_wmax[par][0][tid], s_wmax[par][1][tid]),
+                                       max(s_wmax[par][2][tid], s_wmax[par][3][tid])));
+      ell_tiles[mt] = ell;
+    }
+  };
+  if constexpr (PF) {
+    for (int t = t_begin; t < t_end; ++t) tile(t);
+  } else {
+    tile(t_begin);
   }
 }
 
@@ -585,7 +657,8 @@ __global__ __launch_bounds__(kThreads) void pass2_kernel(const uint16_t* __restr
                                                          const float* __restrict__ a0_tile,
                                                          int16_t* __restrict__ dbg_counts, float* __restrict__ part,
                                                          int* __restrict__ part_emit, int want_emit,
-                                                         const int* __restrict__ seq_lens, int B, PageTable pt) {
+                                                         const int* __restrict__ seq_lens, int B, PageTable pt,
+                                                         int stash_ld) {
   const int GH = H / KVH;
   const int wg = static_cast<int>(blockIdx.x);
   const GridPos gp = grid_pos(wg, seq_lens, B, KVH, BN, L, T_c, cs, cpg);
@@ -642,11 +715,23 @@ __global__ __launch_bounds__(kThreads) void pass2_kernel(const uint16_t* __restr
       if (BN == 256) {
         // two rows per lane: rows 32 (4p + j) + 2q (x0) and + 1 (x1) at lane 16j + q
         float x0[2], x1[2];
+        if (stash_ld > 0) {
+          // tile-major stash (whole tiles): the lane's two rows as one 4-B load
+          const uint16_t* ut = u_stash + static_cast<size_t>(b) * H * stash_ld + (static_cast<size_t>(t) * H + h) * BN;
 #pragma unroll
-        for (int p = 0; p < 2; ++p) {
-          const int row = 32 * (4 * p + jrow) + 2 * qq;
-          x0[p] = (row < len) ? h16_to_f32<BF16>(ub[static_cast<size_t>(n0 + row) * H + h]) * inv : 0.0f;
-          x1[p] = (row + 1 < len) ? h16_to_f32<BF16>(ub[static_cast<size_t>(n0 + row + 1) * H + h]) * inv : 0.0f;
+          for (int p = 0; p < 2; ++p) {
+            const int row = 32 * (4 * p + jrow) + 2 * qq;
+            const uint32_t w2 = *reinterpret_cast<const uint32_t*>(ut + row);
+            x0[p] = (row < len) ? h16_to_f32<BF16>(static_cast<uint16_t>(w2 & 0xffffu)) * inv : 0.0f;
+            x1[p] = (row + 1 < len) ? h16_to_f32<BF16>(static_cast<uint16_t>(w2 >> 16)) * inv : 0.0f;
+          }
+        } else {
+#pragma unroll
+          for (int p = 0; p < 2; ++p) {
+            const int row = 32 * (4 * p + jrow) + 2 * qq;
+            x0[p] = (row < len) ? h16_to_f32<BF16>(ub[static_cast<size_t>(n0 + row) * H + h]) * inv : 0.0f;
+            x1[p] = (row + 1 < len) ? h16_to_f32<BF16>(ub[static_cast<size_t>(n0 + row + 1) * H + h]) * inv : 0.0f;
+          }
         }
         int c0[2], c1[2];
         systematic_counts<8>(x0, x1, len, a0, lane, c0, c1);
@@ -799,9 +884,9 @@ __global__ __launch_bounds__(kMaxD) void finalize_kernel(const float* __restrict
 // ---------------------------------------------------------------- launchers
 hipError_t launch_pass1(const void* q, const void* K, int dtype, int B, int H, int KVH, int D, int L, int L_storage,
                         int BN, float* m_tiles, float* ell_tiles, uint16_t* u_stash, const int* seq_lens,
-                        long long total_tiles, PageTable pt, hipStream_t stream) {
+                        long long total_tiles, PageTable pt, hipStream_t stream, int stash_ld) {
   const int T_c = (L + BN - 1) / BN;
-  const long long grid = seq_lens ? total_tiles * KVH : static_cast<long long>(B) * KVH * T_c;
+  long long grid = seq_lens ? total_tiles * KVH : static_cast<long long>(B) * KVH * T_c;
   if (grid <= 0) return hipSuccess;
   const float q_scale = 1.0f / sqrtf(static_cast<float>(D));
   const uint16_t* Qh = static_cast<const uint16_t*>(q);
@@ -811,9 +896,26 @@ hipError_t launch_pass1(const void* q, const void* K, int dtype, int B, int H, i
     // head blocks of four: GH 1-4 -> 1, 5-8 -> 2, 9-16 -> 4
     const int nhb = GH <= 4 ? 1 : (GH <= 8 ? 2 : 4);
     const bool bf = dtype == SANTA_BF16, pg = pt.table != nullptr;
+    // chunks of tiles for about one resident round of workgroups (uniform),
+    // or about eight over the sequences' tiles (ragged)
+    const int occ = (D == 256 || (D == 128 && nhb == 4)) ? 1 : 2;
+    const int per_round = flash::rows_per_round() / 8 * occ;
+    const bool stream_tiles = nhb == 1 || (D == 64 && nhb == 2);  // fast_prefetch<D, NHB>()
+    int cs = 1, cpg = T_c, n_wg = 0;
+    if (!stream_tiles) {
+      // one tile per workgroup (grid as computed above)
+    } else if (seq_lens) {
+      flash::plan_ragged(B, KVH, total_tiles, T_c, &cs, &n_wg, per_round, 1);
+      cpg = 0;
+      grid = n_wg;
+    } else {
+      flash::plan_chunks(B, KVH, T_c, &cs, &cpg, per_round);
+      grid = static_cast<long long>(B) * KVH * cpg;
+    }
 #define SANTA_GF1(BF, DD, NB, PG)                                                                                  \
   hipLaunchKernelGGL((pass1_fast_kernel<BF, DD, NB, PG>), dim3(static_cast<unsigned>(grid)), dim3(kThreads), 0,    \
-                     stream, Qh, Kh, H, KVH, L, L_storage, T_c, q_scale, m_tiles, ell_tiles, u_stash, seq_lens, B, pt)
+                     stream, Qh, Kh, H, KVH, L, L_storage, T_c, cs, cpg, q_scale, m_tiles, ell_tiles, u_stash,      \
+                     seq_lens, B, pt, stash_ld)
 #define SANTA_GF1_NB(BF, DD, PG) \
   do {                           \
     if (nhb == 1)                \
@@ -867,7 +969,7 @@ hipError_t launch_budgets_big(const float* m_tiles, const float* ell_tiles, int 
 hipError_t launch_pass2(const void* V, const uint16_t* u_stash, int dtype, int B, int H, int KVH, int D, int L,
                         int L_storage, int BN, int T_c, int cs, int cpg, int n_wg, const float* invdelta,
                         const float* a0, int16_t* counts, float* part, int* part_emit, int want_emit,
-                        const int* seq_lens, PageTable pt, hipStream_t stream) {
+                        const int* seq_lens, PageTable pt, hipStream_t stream, int stash_ld) {
   const long long grid = seq_lens ? n_wg : static_cast<long long>(B) * KVH * cpg;
   if (grid <= 0) return hipSuccess;
   const uint16_t* Vh = static_cast<const uint16_t*>(V);
@@ -876,7 +978,7 @@ hipError_t launch_pass2(const void* V, const uint16_t* u_stash, int dtype, int B
 #define SANTA_GP2(BF, PG, DP)                                                                                       \
   hipLaunchKernelGGL((pass2_kernel<BF, PG, DP>), dim3(static_cast<unsigned>(grid)), dim3(threads), 0, stream, Vh,    \
                      u_stash, H, KVH, D, BN, L, L_storage, T_c, cs, cpg, invdelta, a0, counts, part, part_emit,      \
-                     want_emit, seq_lens, B, pt)
+                     want_emit, seq_lens, B, pt, stash_ld)
 #define SANTA_GP2_D(BF, PG)      \
   do {                           \
     if (dpl == 1)                \
