@@ -187,6 +187,23 @@ def test_prop_fast_generic_pass1(H, KVH, D, L, S, monkeypatch):
     assert exp["pass1_mode"] == 1 and exp["T_c"] == (L + 255) // 256
 
 
+@pytest.mark.parametrize("H,KVH,D,L,S", [
+    (32, 32, 128, 32700, 512),   # MHA: chunks of 8 tiles per workgroup, the next tile's rows in registers
+    (32, 4, 64, 40000, 600),     # GH 8 at D 64 (two head blocks, registers): chunks of 2 tiles
+    (8, 2, 256, 40000, 300),     # GH 4 at D 256 (one workgroup per CU): chunks of 2 tiles
+])
+def test_prop_fast_generic_streaming(H, KVH, D, L, S, monkeypatch):
+    """The generic pass 1 streaming a chunk of tiles per workgroup (one
+    resident round of (KV head, chunk) items, the next tile's rows loaded
+    while the current one is scored) and the tile-major stash of the fused
+    decode: every stage bit-exact to the oracle, the fused decode equal to the
+    stage entry points bit for bit.  The last tile is partial in each."""
+    _announce(f"prop fast generic streaming H={H} KVH={KVH} D={D} L={L} S={S} bn=256")
+    q, K, V = _general_inputs(H, KVH, D, L, SEED + 11 * D + H)
+    exp = _check(q, K, V, S, SEED, block_n=256, monkeypatch=monkeypatch)
+    assert exp["pass1_mode"] == 1 and exp["T_c"] == (L + 255) // 256
+
+
 @pytest.mark.parametrize("H,KVH,D,L,S,block_n", [(8, 4, 512, 1500, 60, 64), (4, 2, 1024, 900, 40, 32),
                                                   (4, 4, 512, 3100, 50, 256)])
 def test_prop_head_dim_above_256(H, KVH, D, L, S, block_n, monkeypatch):
