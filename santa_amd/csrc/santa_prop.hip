@@ -790,7 +790,7 @@ static int pass1_mode(const char* env) {
 }
 
 // D = 128 with GH 4 or 8 runs the tuned kernels at block_n 32 / 64 / 256;
-// every other shape with D a multiple of 16 up to 256, GH up to 16 and
+// every other shape with D a multiple of 16 up to 1024, GH up to 16 and
 // block_n a multiple of 16 up to 512 runs the generic ones
 // (santa_prop_gen.hip).
 static int check_common(int dtype, int H, int KVH, int D) {

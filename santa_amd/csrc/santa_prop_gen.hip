@@ -1,33 +1,41 @@
 // santa_prop_gen.hip -- santa_prop on the shapes the tuned kernels of
 // santa_flash.hip / santa_prop.hip do not take: any query-group size GH up to
-// 16, head_dim D any multiple of 16 up to 256, block_n any multiple of 16 up
+// 16, head_dim D any multiple of 16 up to 1024, block_n any multiple of 16 up
 // to 512 (the reference's general pass 1 takes D % 16 == 0 and
 // block_n % 16 == 0, prop/santa_cuda.cpp:212-259; its pass 2 launches
 // (128, GH) threads, prop/santa_cuda_kernel.cu:917-946), and more than 4096
 // tiles per head in the budgets (the reference sizes that kernel's shared
 // memory at T_c * 8 bytes, prop/santa_cuda_kernel.cu:904-915).
 //
+// Pass 1 rounds q after scaling, q' = TK(f32(q) * scale)
+// (prop/santa_cuda_kernel.cu:121-140), and sums ell as the reference's WMMA
+// kernel does: per 16-row slab in row order, then the slabs in order
+// (:225-262).  The scores take one fixed association for what the reference
+// leaves to its 16x16x16 MMA, the same for every D: virtual lanes of 4 dims
+// chained with fma, then the shfl_down tree over the D / 4 lanes (for D = 128
+// the vec path's association).
+//
 // Kernels (one decode step, as in santa_prop.hip):
-//  * pass1_kernel: one workgroup per (sequence, KV head, tile).  q' =
-//    TK(f32(q) * scale) (prop/santa_cuda_kernel.cu:121-140); scores in a
-//    fixed association for what the reference leaves to its 16x16x16 MMA:
-//    for D = 128 the vec path's (4-element fma chains per virtual lane, then
-//    the 32-lane shfl_down tree), otherwise one fma chain over d ascending;
-//    m_t, u = exp(s - m_t) and the 16-bit u stash [B, L_storage, H]; ell as
-//    the reference's WMMA kernel sums it: per 16-row slab in row order, then
-//    the slabs in order (:225-262).
+//  * pass1_fast_kernel (block_n 256, D 64 / 128 / 256): four waves per tile,
+//    a row per lane, K staged in swizzled LDS by 16-byte loads and scored on
+//    the matrix pipe (broadcast 4x4x1 MFMA chains); for one head block a
+//    workgroup streams a chunk of tiles, the next tile's rows in registers.
+//    m_t, ell_t and the 16-bit u stash ([B, L_storage, H], or tile-major
+//    [B, T, H, 256] inside the fused decode).
+//  * pass1_kernel (every other D and block_n): one workgroup per (sequence,
+//    KV head, tile), scalar fma chains read from LDS.
 //  * budgets_big_kernel: the largest-remainder budgets of santa_prop.hip's
 //    budgets_kernel (same m*, Z association, bases, jitter and bitonic
 //    network, :577-726) with the network's keys in global memory (the
 //    head's invdelta and a0 rows until their final values), for any number
 //    of tiles.
-//  * pass2_kernel: per (sequence, KV head, chunk of tiles): each head's
-//    systematic counts from the stash (32-row chunks, the reference's
-//    Hillis-Steele scan with a sequential carry, :771-807), its sampled rows
-//    ascending, and their count-weighted V rows summed with fma (:843-857).
+//  * pass2_kernel: per (sequence, KV head, chunk of tiles), one wave per head
+//    (up to four heads a wave): each head's systematic counts from the stash
+//    (at block_n 256 the two-rows-per-lane DPP scan, otherwise 32-row chunks
+//    with the reference's Hillis-Steele scan and sequential carry, :771-807),
+//    its sampled rows ascending, and their count-weighted V rows summed with
+//    fma (:843-857).
 //  * finalize_kernel: out = dtype(sum over chunks * (1/S)) and vrows.
-// These are plain, correct kernels for shapes outside the tuned paths; the
-// shapes of the benchmarks run the tuned kernels.
 #include "santa_device.h"
 #include "santa_amd.h"
 #include "santa_internal.h"
