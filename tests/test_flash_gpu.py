@@ -174,6 +174,8 @@ def test_device_expf_matches_oracle():
         (1, 32, 8, 2048, 100000, -1, torch.bfloat16),  # lists overflow inside a tile
         (2, 32, 8, 32768, 256, -1, torch.bfloat16),    # several tiles per wave, cfg2 rows
         (2, 32, 8, 6000, 300, -1, torch.float16),
+        (2, 32, 8, 50000, 256, -1, torch.float16),     # f16 above the small pass: the production call on the rows kernel
+        (1, 64, 8, 100000, 512, -1, torch.float16),    # f16 GH 8 above the small pass
         (2, 16, 4, 9000, 256, -1, torch.bfloat16),     # KVH 4: the four-wave layout
         (1, 8, 2, 5000, 64, 4500, torch.bfloat16),     # KVH 2, valid_len < storage
     ],

@@ -222,6 +222,16 @@ def test_prop_fast_generic_f16(monkeypatch):
     _check(q, K, V, 90, SEED, block_n=256, is_bf16=False, monkeypatch=monkeypatch)
 
 
+@pytest.mark.parametrize("H,KVH,L,S", [(32, 8, 20000, 300), (64, 8, 20000, 300)])
+def test_prop_wave_pass1_f16(H, KVH, L, S, monkeypatch):
+    """f16 through the wave-kernel pass 1 (GH 4 vec path, GH 8 general path)
+    above the small pass, with the tile-major stash of the fused decode: every
+    stage bit-exact to the oracle, the fused decode equal to the stages."""
+    _announce(f"prop wave pass 1 f16 H={H} KVH={KVH} L={L} S={S} bn=256")
+    q, K, V = _general_inputs(H, KVH, 128, L, SEED + 13 + H, dtype=torch.float16)
+    _check(q, K, V, S, SEED, block_n=256, is_bf16=False, monkeypatch=monkeypatch)
+
+
 def test_prop_general_f16(monkeypatch):
     _announce("prop general shape f16 H=16 KVH=8 D=96 L=1500 S=70 bn=32")
     q, K, V = _general_inputs(16, 8, 96, 1500, SEED + 5, dtype=torch.float16)
