@@ -81,6 +81,10 @@ def parse_args():
     ap.add_argument("--copy-calibration-mib", type=int, default=0,
                     help="first run a plain device copy of this many MiB 5 times (a known-size kernel "
                          "that calibrates rocprofv3 FETCH_SIZE / WRITE_SIZE)")
+    ap.add_argument("--extra-workloads", default="cfg3,cfg5,cfg5p,propgen",
+                    help="with the headline workload (cfg2, contiguous): after its own timing, also time these "
+                         "workloads (20 steps each, 2 step windows) and report them under `extra_workloads` in the "
+                         "same JSON line; '' for none")
     return ap.parse_args()
 
 
@@ -628,6 +632,39 @@ def run_cfg4(args, dev):
     }
 
 
+def extra_workloads(args, dev):
+    """The other BASELINE workloads (and the generic-shape one) timed after the
+    headline in the same process, 20 steps each: a summary of each line."""
+    import copy
+    import torch
+
+    runners = {"cfg3": run_cfg3, "cfg5": run_cfg5, "cfg5p": run_cfg5p, "propgen": run_propgen}
+    out = []
+    for name in [w.strip() for w in args.extra_workloads.split(",") if w.strip()]:
+        sub = copy.copy(args)
+        sub.steps, sub.warmup, sub.warmup_ms, sub.windows = 20, 2, 200.0, 2
+        sub.no_cpu_baseline, sub.page_size, sub.copy_calibration_mib = True, 0, 0
+        sub.batch, sub.ctx, sub.heads, sub.kv_heads, sub.head_dim = 8, 32768, 32, 32, 128
+        print(f"[bench] extra workload {name}", file=sys.stderr, flush=True)
+        try:
+            if name not in runners:
+                raise ValueError(f"unknown workload {name!r}")
+            r = runners[name](sub, dev)
+            rf = r["roofline"]
+            e = {"name": name, "workload": r["config"]["workload"], "steps": sub.steps,
+                 "us_per_step": r["us_per_step"], "us_per_step_median": r["us_per_step_median"],
+                 "bytes_alg_per_launch": rf["bytes_alg_per_launch"], "step_frac": rf["step_frac"],
+                 "emitted_v_rows": rf["emitted_v_rows"]}
+            if rf.get("kernel_us") is not None and not rf["kernel"].startswith("whole"):
+                e["kernel"], e["kernel_us"], e["kernel_frac"] = rf["kernel"], rf["kernel_us"], rf["frac"]
+        except Exception as exc:  # report it, keep the headline line
+            e = {"name": name, "error": f"{type(exc).__name__}: {exc}"}
+        out.append(e)
+        torch.cuda.synchronize()
+        torch.cuda.empty_cache()
+    return out
+
+
 def main():
     args = parse_args()
     if args.gpus != 1:
@@ -639,6 +676,8 @@ def main():
     dev = torch.device("cuda:0")
     if args.workload == "cfg2":
         line = run_cfg2_paged(args, dev) if args.page_size else run_cfg2(args, dev)
+        if not args.page_size and args.extra_workloads.strip():
+            line["extra_workloads"] = extra_workloads(args, dev)
     else:
         line = {"cfg3": run_cfg3, "cfg4": run_cfg4, "cfg5": run_cfg5, "cfg5p": run_cfg5p,
                 "single": run_single, "propgen": run_propgen}[args.workload](args, dev)
