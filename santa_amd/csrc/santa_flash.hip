@@ -855,7 +855,7 @@ __global__ __launch_bounds__(ROWS ? 512 : kThreads, ROWS ? 1 : 2) void wave_kern
     int L_valid, int L_storage, int T_c, int cs, int cpg, float q_scale, int S_pt, uint64_t seed,
     float* __restrict__ part, int* __restrict__ part_emit, const int* __restrict__ seq_lens, int B, long long S_total,
     float* __restrict__ dbg_m, float* __restrict__ dbg_ell, int16_t* __restrict__ dbg_counts,
-    uint16_t* __restrict__ u_stash, int stash_ld, PageTable pt) {
+    uint16_t* __restrict__ u_stash, int stash_ld, PageTable pt, int stash_nt) {
   constexpr int BN = 256;
   constexpr int NHB = GH / 4;
   constexpr int LCAP = kWaveListCap;
@@ -1304,13 +1304,28 @@ __global__ __launch_bounds__(ROWS ? 512 : kThreads, ROWS ? 1 : 2) void wave_kern
       // past len).  The KV heads of a tile write one contiguous block (GH 8:
       // the cfg5-shaped prop step 2058 -> 1983 us against the head-major
       // [B, H, stash_ld], whose per-head rows lie stash_ld * 2 bytes apart)
+      if (stash_nt) {
+        // non-temporal: buffer stores with the nt bit through one descriptor
+        // over this sequence's stash (a separate instruction form, so the two
+        // branches cannot be merged into one store that drops the hint)
+        const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+            u_stash + static_cast<size_t>(b) * H * stash_ld, static_cast<short>(0), H * stash_ld * 2, kBufferWord3);
 #pragma unroll
-      for (int g = 0; g < GH; ++g)
+        for (int g = 0; g < GH; ++g)
 #pragma unroll
-        for (int hh = 0; hh < 2; ++hh)
-          *reinterpret_cast<uint32_t*>(u_stash + static_cast<size_t>(b) * H * stash_ld +
-                                       (static_cast<size_t>(t) * H + h0 + g) * BN + 128 * hh + 32 * jrow + 2 * qq) =
-              ubits[g][hh][0] | (ubits[g][hh][1] << 16);
+          for (int hh = 0; hh < 2; ++hh)
+            __builtin_amdgcn_raw_buffer_store_b32(
+                ubits[g][hh][0] | (ubits[g][hh][1] << 16), rs,
+                2 * (((t * H + h0 + g) * BN) + 128 * hh + 32 * jrow + 2 * qq), 0, kBufferNontemporal);
+      } else {
+#pragma unroll
+        for (int g = 0; g < GH; ++g)
+#pragma unroll
+          for (int hh = 0; hh < 2; ++hh)
+            *reinterpret_cast<uint32_t*>(u_stash + static_cast<size_t>(b) * H * stash_ld +
+                                         (static_cast<size_t>(t) * H + h0 + g) * BN + 128 * hh + 32 * jrow + 2 * qq) =
+                ubits[g][hh][0] | (ubits[g][hh][1] << 16);
+      }
     } else if constexpr (P1) {
       // the stash row [n, h0 .. h0+GH) of each valid row: one 8-B (GH 4) or
       // 16-B (GH 8) store
@@ -1906,14 +1921,14 @@ static hipError_t launch_wave_t(const Args& a, float* dbg_m, float* dbg_ell, int
                          dim3(static_cast<unsigned>(64 * a.KVH)), 0, stream, static_cast<const uint16_t*>(a.q),
                          static_cast<const uint16_t*>(a.K), static_cast<const uint16_t*>(a.V), a.H, a.KVH, a.L_valid,
                          a.L_storage, a.T_c, a.cs, a.cpg, q_scale, a.S_pt, a.seed, a.part, a.part_emit, a.seq_lens,
-                         a.B, a.S_total, dbg_m, dbg_ell, dbg_counts, nullptr, 0, a.pt);
+                         a.B, a.S_total, dbg_m, dbg_ell, dbg_counts, nullptr, 0, a.pt, 0);
       return hipGetLastError();
     }
     hipLaunchKernelGGL((wave_kernel<BF16, GH, true>), dim3(grid), dim3(kThreads), 0, stream,
                        static_cast<const uint16_t*>(a.q), static_cast<const uint16_t*>(a.K),
                        static_cast<const uint16_t*>(a.V), a.H, a.KVH, a.L_valid, a.L_storage, a.T_c, a.cs, a.cpg,
                        q_scale, a.S_pt, a.seed, a.part, a.part_emit, a.seq_lens, a.B, a.S_total, dbg_m, dbg_ell,
-                       dbg_counts, nullptr, 0, a.pt);
+                       dbg_counts, nullptr, 0, a.pt, 0);
   } else if (rows_layout(a.KVH)) {
     // one workgroup of KVH waves per (sequence, chunk) item
     const unsigned rgrid = grid / static_cast<unsigned>(a.KVH);
@@ -1923,25 +1938,25 @@ static hipError_t launch_wave_t(const Args& a, float* dbg_m, float* dbg_ell, int
                          static_cast<const uint16_t*>(a.q), static_cast<const uint16_t*>(a.K),
                          static_cast<const uint16_t*>(a.V), a.H, a.KVH, a.L_valid, a.L_storage, a.T_c, a.cs, a.cpg,
                          q_scale, a.S_pt, a.seed, a.part, a.part_emit, a.seq_lens, a.B, a.S_total, nullptr,
-                         nullptr, nullptr, nullptr, 0, a.pt);
+                         nullptr, nullptr, nullptr, 0, a.pt, 0);
     else
       hipLaunchKernelGGL((wave_kernel<BF16, GH, false, false, false, true>), dim3(rgrid), block, 0, stream,
                          static_cast<const uint16_t*>(a.q), static_cast<const uint16_t*>(a.K),
                          static_cast<const uint16_t*>(a.V), a.H, a.KVH, a.L_valid, a.L_storage, a.T_c, a.cs, a.cpg,
                          q_scale, a.S_pt, a.seed, a.part, a.part_emit, a.seq_lens, a.B, a.S_total, nullptr,
-                         nullptr, nullptr, nullptr, 0, a.pt);
+                         nullptr, nullptr, nullptr, 0, a.pt, 0);
   } else if (a.pt.table) {
     hipLaunchKernelGGL((wave_kernel<BF16, GH, false, false, true>), dim3(grid), dim3(kThreads), 0, stream,
                        static_cast<const uint16_t*>(a.q), static_cast<const uint16_t*>(a.K),
                        static_cast<const uint16_t*>(a.V), a.H, a.KVH, a.L_valid, a.L_storage, a.T_c, a.cs, a.cpg,
                        q_scale, a.S_pt, a.seed, a.part, a.part_emit, a.seq_lens, a.B, a.S_total, nullptr,
-                       nullptr, nullptr, nullptr, 0, a.pt);
+                       nullptr, nullptr, nullptr, 0, a.pt, 0);
   } else {
     hipLaunchKernelGGL((wave_kernel<BF16, GH, false>), dim3(grid), dim3(kThreads), 0, stream,
                        static_cast<const uint16_t*>(a.q), static_cast<const uint16_t*>(a.K),
                        static_cast<const uint16_t*>(a.V), a.H, a.KVH, a.L_valid, a.L_storage, a.T_c, a.cs, a.cpg,
                        q_scale, a.S_pt, a.seed, a.part, a.part_emit, a.seq_lens, a.B, a.S_total, nullptr,
-                       nullptr, nullptr, nullptr, 0, a.pt);
+                       nullptr, nullptr, nullptr, 0, a.pt, 0);
   }
   return hipGetLastError();
 }
@@ -2149,13 +2164,25 @@ hipError_t launch_prop_pass1(const void* q, const void* K, int dtype, int B, int
     unsigned grid = a.seq_lens ? static_cast<unsigned>(a.n_wg)
                                : static_cast<unsigned>(a.B) * static_cast<unsigned>(a.KVH) * static_cast<unsigned>(a.cpg);
     if (rows) grid /= static_cast<unsigned>(a.KVH);
+    // A tile-major stash larger than half the 256 MiB last-level cache is
+    // written with non-temporal stores: cached, it would only evict itself
+    // before pass 2 reads it (cfg5-shaped prop step, a 1 GiB stash: 1961 ->
+    // 1896 us), while a smaller one is read back from the cache (B = 32 at 32k
+    // tokens, 64 MiB: 507 us cached against 525 us non-temporal)
+    // (the non-temporal stores address one sequence's stash through a
+    // buffer descriptor, whose range and offsets are 32-bit)
+    const size_t seq_stash_bytes = static_cast<size_t>(stash_ld) * a.H * sizeof(uint16_t);
+    const int stash_nt = (stash_ld > 0 && a.B * seq_stash_bytes > (static_cast<size_t>(128) << 20) &&
+                          seq_stash_bytes < (static_cast<size_t>(1) << 31))
+                             ? 1
+                             : 0;
     if (grid == 0) return hipSuccess;
     const dim3 block(rows ? static_cast<unsigned>(64 * a.KVH) : static_cast<unsigned>(kThreads));
 #define SANTA_P1_LAUNCH(BF, G, PG, RW)                                                                            \
   hipLaunchKernelGGL((wave_kernel<BF, G, false, true, PG, RW>), dim3(grid), block, 0, stream,                     \
                      static_cast<const uint16_t*>(a.q), static_cast<const uint16_t*>(a.K), nullptr, a.H, a.KVH,     \
                      a.L_valid, a.L_storage, a.T_c, a.cs, a.cpg, q_scale, 0, 0ULL, nullptr, nullptr, a.seq_lens,   \
-                     a.B, 0LL, m_tiles, ell_tiles, nullptr, u_stash, stash_ld, a.pt)
+                     a.B, 0LL, m_tiles, ell_tiles, nullptr, u_stash, stash_ld, a.pt, stash_nt)
 #define SANTA_P1_GH(BF, PG, RW)    \
   do {                             \
     if (GH == 4)                   \
