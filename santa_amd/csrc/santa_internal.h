@@ -115,6 +115,9 @@ hipError_t launch_pass2(const void* V, const uint16_t* u_stash, int dtype, int B
 // Waves per generic pass-2 workgroup (one per head, up to four); the chunk
 // plan counts min(GH, 4)-wave workgroups for GH < 4.
 int pass2_waves(int GH);
+// Generic pass-2 workgroups resident on the current device at once (its
+// registers and LDS allow), for the chunk plan; 0 if the runtime cannot say.
+int pass2_resident(int GH, int D);
 hipError_t launch_finalize(const float* part, const int* part_emit, int dtype, int B, int H, int KVH, int D, int cpg,
                            float scale_out, void* out, int* vrows, const int* seq_lens, const int* seq_S, int BN,
                            int cs, int max_rows, int n_wg, hipStream_t stream);

@@ -741,10 +741,20 @@ struct PropWs {
 static PropWs prop_ws_layout(int B, int H, int KVH, int D, int L_storage, int T_c, long long total_tiles = -1) {
   PropWs w{};
   size_t chunks;
-  // GH < 4 (generic pass 2 with GH-wave workgroups): chunks for as many
-  // resident workgroups as four-wave ones leave room for
-  const int nw = propgen::pass2_waves(H / KVH);
-  const int per_round = nw < 4 ? flash::rows_per_round() / nw : 0;
+  // Shapes that only the generic pass 2 takes: chunks for one round of as many
+  // of its workgroups as the device holds at once (five waves per SIMD at
+  // D = 128, seven at D = 64), since each wave walks its tiles one dependent
+  // round trip after another; with no device to ask, for as many GH-wave
+  // workgroups as four-wave ones leave room for.  D = 128 at GH 4 or 8 keeps
+  // the tuned kernels' plan (one round of 4-wave workgroups, two per CU).
+  const int GH = H / KVH;
+  const int nw = propgen::pass2_waves(GH);
+  const bool tuned = D == 128 && (GH == 4 || GH == 8);
+  int per_round = (!tuned && nw < 4) ? flash::rows_per_round() / nw : 0;
+  if (!tuned) {
+    const int r = propgen::pass2_resident(GH, D);
+    if (r > 0) per_round = r;
+  }
   if (total_tiles >= 0) {
     flash::plan_ragged(B, KVH, total_tiles, T_c, &w.cs, &w.n_wg, per_round);
     w.cpg = 0;

@@ -41,6 +41,8 @@
 #include "santa_internal.h"
 
 #include <algorithm>
+#include <atomic>
+#include <type_traits>
 #include <cfloat>
 
 namespace santa {
@@ -632,8 +634,8 @@ __global__ __launch_bounds__(kBudgetThreads) void budgets_big_kernel(
 // santa_device.h, else 32-row pieces with the lane scan; both the
 // reference's 32-lane Hillis-Steele scan with a sequential carry,
 // :771-807), the sampled rows ascending, and their count-weighted V rows
-// added with one fma per element in row order (:843-857), 16 rows' loads in
-// flight at a time.  Lane l holds dims DPL l .. DPL l + DPL - 1.
+// added with one fma per element in row order (:843-857), up to 16 rows'
+// loads in flight at a time.  Lane l holds dims DPL l .. DPL l + DPL - 1.
 constexpr int kGatherRows = 16;
 constexpr int kMaxHeadsPerWave = kMaxGH / 4;
 
@@ -657,16 +659,21 @@ __device__ __forceinline__ void load_dims(const uint16_t* p, uint16_t (&v)[DPL])
   }
 }
 
-template <bool BF16, bool PAGED, int DPL>
+// T256: block_n is 256 (the two-rows-per-lane path only; compiled apart so
+// that the other path's per-piece bounds are not computed for it).  NK: the
+// most heads a wave takes (1 for GH <= 4, else kMaxHeadsPerWave), which
+// sizes the unrolled per-head state.
+template <bool BF16, bool PAGED, int DPL, bool T256, int NK>
 __global__ __launch_bounds__(kThreads) void pass2_kernel(const uint16_t* __restrict__ V,
                                                          const uint16_t* __restrict__ u_stash, int H, int KVH, int D,
-                                                         int BN, int L, int L_storage, int T_c, int cs, int cpg,
+                                                         int BN_arg, int L, int L_storage, int T_c, int cs, int cpg,
                                                          const float* __restrict__ invdelta,
                                                          const float* __restrict__ a0_tile,
                                                          int16_t* __restrict__ dbg_counts, float* __restrict__ part,
                                                          int* __restrict__ part_emit, int want_emit,
                                                          const int* __restrict__ seq_lens, int B, PageTable pt,
                                                          int stash_ld) {
+  const int BN = T256 ? 256 : BN_arg;
   const int GH = H / KVH;
   const int wg = static_cast<int>(blockIdx.x);
   const GridPos gp = grid_pos(wg, seq_lens, B, KVH, BN, L, T_c, cs, cpg);
@@ -684,14 +691,18 @@ __global__ __launch_bounds__(kThreads) void pass2_kernel(const uint16_t* __restr
   const int jrow = lane >> 4;
   const int qq = lane & 15;
 
-  __shared__ int s_lrow[4][kMaxBN];
-  __shared__ float s_lc[4][kMaxBN];
-  __shared__ int s_flag[kMaxBN];
-  __shared__ int s_nemit;
+  // LDS sized by the launch (pass2_lds_bytes): per wave BN listed rows and
+  // their counts, then BN emitted-row flags and the tile's emitted total
+  extern __shared__ int s_p2[];
+  int* const s_lrow = s_p2 + wave * BN;
+  float* const s_lc = reinterpret_cast<float*>(s_p2 + nwv * BN) + wave * BN;
+  int* const s_flag = s_p2 + 2 * nwv * BN;
+  int* const s_nemit = s_flag + BN;
 
-  float acc[kMaxHeadsPerWave][DPL];
+  static_assert(NK == 1 || NK == kMaxHeadsPerWave, "heads per wave");
+  float acc[NK][DPL];
 #pragma unroll
-  for (int k = 0; k < kMaxHeadsPerWave; ++k)
+  for (int k = 0; k < NK; ++k)
 #pragma unroll
     for (int j = 0; j < DPL; ++j) acc[k][j] = 0.0f;
   int emit_total = 0;
@@ -706,7 +717,7 @@ __global__ __launch_bounds__(kThreads) void pass2_kernel(const uint16_t* __restr
       __syncthreads();
     }
 #pragma unroll
-    for (int k = 0; k < kMaxHeadsPerWave; ++k) {
+    for (int k = 0; k < NK; ++k) {
       const int g = wave + nwv * k;
       if (g >= GH) break;
       const int h = h0 + g;
@@ -720,7 +731,7 @@ __global__ __launch_bounds__(kThreads) void pass2_kernel(const uint16_t* __restr
         continue;
       }
       int lc = 0;
-      if (BN == 256) {
+      if constexpr (T256) {
         // two rows per lane: rows 32 (4p + j) + 2q (x0) and + 1 (x1) at lane 16j + q
         float x0[2], x1[2];
         if (stash_ld > 0) {
@@ -755,13 +766,13 @@ __global__ __launch_bounds__(kThreads) void pass2_kernel(const uint16_t* __restr
           const int pos0 = lc + __popcll(nz0 & below) + __popcll(nz1 & below);
           const int pos1 = pos0 + (c0[p] != 0 ? 1 : 0);
           if (c0[p] != 0) {
-            s_lrow[wave][pos0] = n0 + row;
-            s_lc[wave][pos0] = static_cast<float>(c0[p]);
+            s_lrow[pos0] = n0 + row;
+            s_lc[pos0] = static_cast<float>(c0[p]);
             if (want_emit) s_flag[row] = 1;
           }
           if (c1[p] != 0) {
-            s_lrow[wave][pos1] = n0 + row + 1;
-            s_lc[wave][pos1] = static_cast<float>(c1[p]);
+            s_lrow[pos1] = n0 + row + 1;
+            s_lc[pos1] = static_cast<float>(c1[p]);
             if (want_emit) s_flag[row + 1] = 1;
           }
           lc += __popcll(nz0) + __popcll(nz1);
@@ -791,8 +802,8 @@ __global__ __launch_bounds__(kThreads) void pass2_kernel(const uint16_t* __restr
           const uint64_t nz = __ballot(c != 0);
           if (c != 0) {
             const int pos = lc + __popcll(nz & ((1ull << lane) - 1ull));
-            s_lrow[wave][pos] = n0 + r;
-            s_lc[wave][pos] = static_cast<float>(c);
+            s_lrow[pos] = n0 + r;
+            s_lc[pos] = static_cast<float>(c);
             if (want_emit) s_flag[r] = 1;
           }
           lc += __popcll(nz);
@@ -801,16 +812,19 @@ __global__ __launch_bounds__(kThreads) void pass2_kernel(const uint16_t* __restr
           for (int r = ((len + 31) / 32) * 32 + lane; r < BN; r += 64) dbg_counts[ht * BN + r] = 0;
       }
       __builtin_amdgcn_wave_barrier();
-      // count-weighted V rows, rows ascending, one fma per element; the loads
-      // of up to 16 rows go out before the first is used
-      for (int i0 = 0; i0 < lc; i0 += kGatherRows) {
-        uint16_t vv[kGatherRows][DPL];
-        float cf[kGatherRows];
+      // count-weighted V rows, rows ascending, one fma per element: batches
+      // of 16 rows whose loads go out before the first is used, then what is
+      // left in batches of 4 (a tile lists about S / T_c rows per head, often
+      // fewer than 16)
+      auto gather = [&](auto nb, int i0) {
+        constexpr int NB = decltype(nb)::value;
+        uint16_t vv[NB][DPL];
+        float cf[NB];
 #pragma unroll
-        for (int q = 0; q < kGatherRows; ++q) {
+        for (int q = 0; q < NB; ++q) {
           const int i = min(i0 + q, lc - 1);
-          const int row = __builtin_amdgcn_readfirstlane(s_lrow[wave][i]);
-          cf[q] = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(s_lc[wave][i])));
+          const int row = __builtin_amdgcn_readfirstlane(s_lrow[i]);
+          cf[q] = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(s_lc[i])));
           if (d0 < D) {
             load_dims<DPL>(V + row_offset<PAGED>(pt, b, row, kv, KVH, D, L_storage) + d0, vv[q]);
           } else {
@@ -819,13 +833,16 @@ __global__ __launch_bounds__(kThreads) void pass2_kernel(const uint16_t* __restr
           }
         }
 #pragma unroll
-        for (int q = 0; q < kGatherRows; ++q) {
+        for (int q = 0; q < NB; ++q) {
           if (i0 + q < lc) {
 #pragma unroll
             for (int j = 0; j < DPL; ++j) acc[k][j] = fmaf(cf[q], h16_to_f32<BF16>(vv[q][j]), acc[k][j]);
           }
         }
-      }
+      };
+      int i0 = 0;
+      for (; i0 + kGatherRows <= lc; i0 += kGatherRows) gather(std::integral_constant<int, kGatherRows>{}, i0);
+      for (; i0 < lc; i0 += 4) gather(std::integral_constant<int, 4>{}, i0);
       __builtin_amdgcn_wave_barrier();
     }
     if (want_emit) {
@@ -834,14 +851,14 @@ __global__ __launch_bounds__(kThreads) void pass2_kernel(const uint16_t* __restr
         int e = 0;
         for (int r = lane; r < BN; r += 64) e += s_flag[r];
         for (int s = 32; s > 0; s >>= 1) e += __shfl_xor(e, s, 64);
-        if (lane == 0) s_nemit = e;
+        if (lane == 0) *s_nemit = e;
       }
       __syncthreads();
-      emit_total += s_nemit;
+      emit_total += *s_nemit;
     }
   }
 #pragma unroll
-  for (int k = 0; k < kMaxHeadsPerWave; ++k) {
+  for (int k = 0; k < NK; ++k) {
     const int g = wave + nwv * k;
     if (g >= GH) break;
     if (d0 < D) {
@@ -854,6 +871,86 @@ __global__ __launch_bounds__(kThreads) void pass2_kernel(const uint16_t* __restr
 
 // Waves per pass-2 workgroup: one per head up to four.
 int pass2_waves(int GH) { return GH < 4 ? GH : 4; }
+
+// Pass 2's dynamic LDS: per wave BN row indices and BN counts, then BN flags
+// and one total.
+static size_t pass2_lds_bytes(int nw, int BN) {
+  return (static_cast<size_t>(2 * nw + 1) * BN + 1) * sizeof(int);
+}
+
+static int pass2_dpl(int D) { return D <= 64 ? 1 : (D <= 128 ? 2 : (D <= 256 ? 4 : (D <= 512 ? 8 : 16))); }
+
+// The fewest workgroups per CU over the instantiations of one DPL and head
+// bound NK (bf16 / f16, contiguous / paged, block_n 256 or not): their
+// registers differ (f16 takes more).
+template <int DPL, int NK>
+static int pass2_blocks_per_cu(int threads, size_t lds) {
+  const void* fns[8] = {reinterpret_cast<const void*>(&pass2_kernel<true, false, DPL, true, NK>),
+                        reinterpret_cast<const void*>(&pass2_kernel<true, true, DPL, true, NK>),
+                        reinterpret_cast<const void*>(&pass2_kernel<false, false, DPL, true, NK>),
+                        reinterpret_cast<const void*>(&pass2_kernel<false, true, DPL, true, NK>),
+                        reinterpret_cast<const void*>(&pass2_kernel<true, false, DPL, false, NK>),
+                        reinterpret_cast<const void*>(&pass2_kernel<true, true, DPL, false, NK>),
+                        reinterpret_cast<const void*>(&pass2_kernel<false, false, DPL, false, NK>),
+                        reinterpret_cast<const void*>(&pass2_kernel<false, true, DPL, false, NK>)};
+  int best = 0;
+  for (int i = 0; i < 8; ++i) {
+    int n = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, fns[i], threads, lds) != hipSuccess) {
+      (void)hipGetLastError();
+      return 0;
+    }
+    best = (i == 0 || n < best) ? n : best;
+  }
+  return best;
+}
+
+template <int NK>
+static int pass2_blocks_per_cu_dpl(int dpl, int threads, size_t lds) {
+  switch (dpl) {
+    case 1: return pass2_blocks_per_cu<1, NK>(threads, lds);
+    case 2: return pass2_blocks_per_cu<2, NK>(threads, lds);
+    case 4: return pass2_blocks_per_cu<4, NK>(threads, lds);
+    case 8: return pass2_blocks_per_cu<8, NK>(threads, lds);
+    default: return pass2_blocks_per_cu<16, NK>(threads, lds);
+  }
+}
+
+// Pass-2 workgroups resident on the current device at once for this shape,
+// from the compiled kernel's registers and the LDS of a block_n = 512 launch
+// (the most any block_n takes); 0 where the runtime cannot say (no device).
+// Cached per (device, D class, waves per workgroup and heads per wave).
+int pass2_resident(int GH, int D) {
+  constexpr int kMaxDev = 64;
+  static std::atomic<int> cached[kMaxDev][5][5];  // [dev][DPL class][waves - 1, or 4 for GH > 4]
+  const int nw = pass2_waves(GH);
+  const int wi = GH > 4 ? 4 : nw - 1;
+  const int dpl = pass2_dpl(D);
+  const int di = dpl == 1 ? 0 : (dpl == 2 ? 1 : (dpl == 4 ? 2 : (dpl == 8 ? 3 : 4)));
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) {
+    (void)hipGetLastError();
+    return 0;
+  }
+  const bool slot = dev >= 0 && dev < kMaxDev;
+  if (slot) {
+    const int c = cached[dev][di][wi].load(std::memory_order_relaxed);
+    if (c > 0) return c;
+  }
+  int cus = 0;
+  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) {
+    (void)hipGetLastError();
+    return 0;
+  }
+  const int threads = 64 * nw;
+  const size_t lds = pass2_lds_bytes(nw, kMaxBN);
+  const int per_cu = GH <= 4 ? pass2_blocks_per_cu_dpl<1>(dpl, threads, lds)
+                             : pass2_blocks_per_cu_dpl<kMaxHeadsPerWave>(dpl, threads, lds);
+  if (per_cu <= 0) return 0;
+  const int r = per_cu * cus;
+  if (slot) cached[dev][di][wi].store(r, std::memory_order_relaxed);
+  return r;
+}
 
 // ---------------------------------------------------------------- finalize
 template <bool BF16>
@@ -878,12 +975,28 @@ __global__ __launch_bounds__(kMaxD) void finalize_kernel(const float* __restrict
     nch = max(0, min(nch, (n_wg - base - kv + KVH - 1) / KVH));
   }
   if (seq_S) scale_out = (seq_S[b] > 0) ? (1.0f / static_cast<float>(seq_S[b])) : 0.0f;
+  // the chunks' partials summed in chunk order, the loads of eight chunks
+  // issued before the first is added
+  constexpr int kBatch = 8;
+  const bool lead = vrows && g == 0 && d == 0;
   float s = 0.0f;
   int e = 0;
-  for (int c = 0; c < nch; ++c) {
-    const size_t slot = static_cast<size_t>(base) + static_cast<size_t>(c) * KVH + kv;
-    if (d < D) s += part[(slot * GH + g) * D + d];
-    if (vrows && g == 0 && d == 0) e += part_emit[slot];
+  for (int c0 = 0; c0 < nch; c0 += kBatch) {
+    float v[kBatch];
+    int ev[kBatch];
+#pragma unroll
+    for (int j = 0; j < kBatch; ++j) {
+      const size_t slot = static_cast<size_t>(base) + static_cast<size_t>(min(c0 + j, nch - 1)) * KVH + kv;
+      v[j] = (d < D) ? part[(slot * GH + g) * D + d] : 0.0f;
+      ev[j] = lead ? part_emit[slot] : 0;
+    }
+#pragma unroll
+    for (int j = 0; j < kBatch; ++j) {
+      if (c0 + j < nch) {
+        s += v[j];
+        e += ev[j];
+      }
+    }
   }
   if (d < D) out[static_cast<size_t>(bh) * D + d] = f32_to_h16<BF16>(s * scale_out);
   if (vrows && g == 0 && d == 0) vrows[static_cast<size_t>(b) * KVH + kv] = e;
@@ -981,12 +1094,28 @@ hipError_t launch_pass2(const void* V, const uint16_t* u_stash, int dtype, int B
   const long long grid = seq_lens ? n_wg : static_cast<long long>(B) * KVH * cpg;
   if (grid <= 0) return hipSuccess;
   const uint16_t* Vh = static_cast<const uint16_t*>(V);
-  const unsigned threads = static_cast<unsigned>(64 * pass2_waves(H / KVH));
-  const int dpl = D <= 64 ? 1 : (D <= 128 ? 2 : (D <= 256 ? 4 : (D <= 512 ? 8 : 16)));
-#define SANTA_GP2(BF, PG, DP)                                                                                       \
-  hipLaunchKernelGGL((pass2_kernel<BF, PG, DP>), dim3(static_cast<unsigned>(grid)), dim3(threads), 0, stream, Vh,    \
-                     u_stash, H, KVH, D, BN, L, L_storage, T_c, cs, cpg, invdelta, a0, counts, part, part_emit,      \
-                     want_emit, seq_lens, B, pt, stash_ld)
+  const int nw = pass2_waves(H / KVH);
+  const unsigned threads = static_cast<unsigned>(64 * nw);
+  const int dpl = pass2_dpl(D);
+  const size_t lds = pass2_lds_bytes(nw, BN);
+#define SANTA_GP2_K(BF, PG, DP, T2, NK)                                                                              \
+  hipLaunchKernelGGL((pass2_kernel<BF, PG, DP, T2, NK>), dim3(static_cast<unsigned>(grid)), dim3(threads), lds,      \
+                     stream, Vh, u_stash, H, KVH, D, BN, L, L_storage, T_c, cs, cpg, invdelta, a0, counts, part,     \
+                     part_emit, want_emit, seq_lens, B, pt, stash_ld)
+#define SANTA_GP2(BF, PG, DP)                                 \
+  do {                                                        \
+    if (H / KVH <= 4) {                                       \
+      if (BN == 256)                                          \
+        SANTA_GP2_K(BF, PG, DP, true, 1);                     \
+      else                                                    \
+        SANTA_GP2_K(BF, PG, DP, false, 1);                    \
+    } else {                                                  \
+      if (BN == 256)                                          \
+        SANTA_GP2_K(BF, PG, DP, true, kMaxHeadsPerWave);      \
+      else                                                    \
+        SANTA_GP2_K(BF, PG, DP, false, kMaxHeadsPerWave);     \
+    }                                                         \
+  } while (0)
 #define SANTA_GP2_D(BF, PG)      \
   do {                           \
     if (dpl == 1)                \
@@ -1007,6 +1136,7 @@ hipError_t launch_pass2(const void* V, const uint16_t* u_stash, int dtype, int B
   }
 #undef SANTA_GP2_D
 #undef SANTA_GP2
+#undef SANTA_GP2_K
   return hipGetLastError();
 }
 
