@@ -975,9 +975,10 @@ __global__ __launch_bounds__(kMaxD) void finalize_kernel(const float* __restrict
     nch = max(0, min(nch, (n_wg - base - kv + KVH - 1) / KVH));
   }
   if (seq_S) scale_out = (seq_S[b] > 0) ? (1.0f / static_cast<float>(seq_S[b])) : 0.0f;
-  // the chunks' partials summed in chunk order, the loads of eight chunks
-  // issued before the first is added
-  constexpr int kBatch = 8;
+  // the chunks' partials summed in chunk order, the loads of 32 chunks
+  // issued before the first is added (one memory round trip for the usual
+  // one-round plan of up to 32 chunks per (b, kv))
+  constexpr int kBatch = 32;
   const bool lead = vrows && g == 0 && d == 0;
   float s = 0.0f;
   int e = 0;
