@@ -1,7 +1,8 @@
 """Seeded random shapes: santa_flash and santa_prop against the CPU oracle.
 
-Twenty-four flash and sixteen prop configurations drawn once from a fixed
-seed (the draw is part of the test, so every run checks the same cases):
+Twenty-four flash, sixteen prop and fourteen generic-shape prop
+configurations drawn once from fixed seeds (the draw is part of the test, so
+every run checks the same cases):
 group sizes 4 and 8 with 1-8 KV heads, 1-3 sequences, lengths from one token to
 20k (so every block size, partial tiles and one-tile sequences occur),
 budgets from 0 to several per row, explicit and automatic block_n, and a
@@ -10,7 +11,11 @@ flash production kernel's tile statistics and counts (block_n 256) or the
 tile kernel's (block_n 32/64), m* and vrows, and the output to the bf16
 tolerance; for prop, m*, vrows and the output per sequence.  These are the
 plans and grids (chunk sizes, the rows and four-wave layouts, ragged last
-chunks) that hand-picked cases leave out.
+chunks) that hand-picked cases leave out.  The generic-shape prop cases
+(`santa_prop_gen.hip`: group sizes other than 4 and 8, head dims 16-256,
+block_n 16-512, bf16 and f16) run the batched, ragged call and check each
+sequence against the oracle's per-sequence call: m* and vrows exact, the
+output to the bf16 tolerance.
 
 Every case prints its name, shape and seed before touching the GPU.
 """
@@ -53,6 +58,23 @@ def _prop_cases():
         S = rng.choice([0, 1, 50, 1000, 5000])
         block_n = rng.choice([0, 32, 64, 256])
         cases.append((i, H, KVH, L, S, block_n))
+    return cases
+
+
+def _prop_generic_cases():
+    rng = random.Random(20261203)
+    cases = []
+    for i in range(14):
+        GH = rng.choice([1, 2, 3, 5, 6, 12, 16])
+        KVH = rng.choice([1, 2, 4]) if GH > 4 else rng.choice([1, 2, 4, 8])
+        D = rng.choice([16, 32, 64, 64, 96, 128, 128, 256, 256])
+        B = rng.choice([1, 2, 3])
+        L = rng.choice([200, 1000, 4097, 9000])
+        lens = [L] + [rng.randint(1, L) for _ in range(B - 1)]
+        Ss = [rng.choice([0, 1, 40, 40, 700, 700]) for _ in range(B)]
+        block_n = rng.choice([16, 48, 256, 256, 512])
+        f16 = rng.random() < 0.25
+        cases.append((i, GH * KVH, KVH, D, lens, Ss, block_n, f16))
     return cases
 
 
@@ -105,3 +127,29 @@ def test_prop_random_shape(case, monkeypatch):
     np.testing.assert_array_equal(vr.cpu().numpy(), exp["vrows"], err_msg="vrows")
     ok, mabs, mrel = tol_check(h16_to_f32(bits16(out)), h16_to_f32(exp["out16"]))
     assert ok, ("vs oracle", mabs, mrel)
+
+
+@pytest.mark.parametrize("case", _prop_generic_cases(), ids=lambda c: f"propgen{c[0]}")
+def test_prop_generic_random_shape(case, monkeypatch):
+    import santa_prop_batch_cuda as m
+
+    monkeypatch.delenv("SANTA_PASS1", raising=False)
+    i, H, KVH, D, lens, Ss, block_n, f16 = case
+    seed = 9000 + i
+    dtype = torch.float16 if f16 else torch.bfloat16
+    print(f"\n[case] prop generic random #{i} H={H} KVH={KVH} D={D} lens={lens} S={Ss} block_n={block_n} "
+          f"dtype={'f16' if f16 else 'bf16'} seed={seed}", flush=True)
+    q, K, V = gen_qkv(len(lens), H, KVH, max(lens), D=D, seed=seed, dtype=dtype, lowrank=0.5)
+    dev = torch.device("cuda:0")
+    out, ms, vr = m.decode_systematic_batched(q.to(dev), K.to(dev), V.to(dev), Ss, seed=seed, block_n=block_n,
+                                              want_vrows=True, valid_len=lens)
+    torch.cuda.synchronize()
+    for b, (Lb, Sb) in enumerate(zip(lens, Ss)):
+        exp = oracle.prop_decode(q[b], K[b, :Lb], V[b, :Lb], Sb, seed=seed, block_n=block_n, is_bf16=not f16,
+                                 debug=True)
+        assert exp["pass1_mode"] == 1
+        np.testing.assert_array_equal(ms[b].cpu().numpy().view(np.uint32), exp["m_star"].view(np.uint32),
+                                      err_msg=f"m_star b={b}")
+        np.testing.assert_array_equal(vr[b].cpu().numpy(), exp["vrows"], err_msg=f"vrows b={b}")
+        ok, mabs, mrel = tol_check(h16_to_f32(bits16(out[b]), f16), h16_to_f32(exp["out16"], f16))
+        assert ok, (f"b={b} vs oracle", mabs, mrel)
