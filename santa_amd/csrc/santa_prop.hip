@@ -653,9 +653,9 @@ __global__ __launch_bounds__(kD) void finalize_kernel(const float* __restrict__ 
   if (seq_S) scale_out = (seq_S[b] > 0) ? (1.0f / static_cast<float>(seq_S[b])) : 0.0f;
   const float* pb = part + ((static_cast<size_t>(base) + kv) * GH + g) * kD + d;
   const size_t cstride = static_cast<size_t>(KVH) * GH * kD;
-  // chunks in ascending order; the loads of a batch of 16 are issued before
+  // chunks in ascending order; the loads of a batch of 32 are issued before
   // the first add (one memory round trip per batch, not one per chunk)
-  constexpr int kBatch = 16;
+  constexpr int kBatch = 32;
   const bool emit = vrows && g == 0 && d == 0;
   float s = 0.0f;
   int e = 0;
@@ -742,15 +742,24 @@ static PropWs prop_ws_layout(int B, int H, int KVH, int D, int L_storage, int T_
   PropWs w{};
   size_t chunks;
   // Shapes that only the generic pass 2 takes: chunks for one round of as many
-  // of its workgroups as the device holds at once (five waves per SIMD at
-  // D = 128, seven at D = 64), since each wave walks its tiles one dependent
-  // round trip after another; with no device to ask, for as many GH-wave
-  // workgroups as four-wave ones leave room for.  D = 128 at GH 4 or 8 keeps
-  // the tuned kernels' plan (one round of 4-wave workgroups, two per CU).
+  // of its workgroups as the device holds at once (the runtime's occupancy
+  // for the compiled kernels), since each wave walks its tiles one dependent
+  // round trip after another; with no device to ask, for as many GH-wave workgroups as
+  // four-wave ones leave room for.  D = 128 at GH 4 or 8 (the tuned kernels):
+  // uniform lengths over at least 32 (sequence, KV head) groups plan one round
+  // of four 4-wave workgroups per CU, the four waves per SIMD every tuned pass
+  // 2 holds (six at GH 4, block_n 256), where two per CU left two thirds of
+  // them idle (B = 32, 32k tokens, GH 4: step 510.2 -> 476.7 us; cfg5p 1897
+  // -> 1871 us; same bits).  Fewer groups keep two per CU: their chunks are
+  // already short, and more of them only lengthen the finalize (B = 1, 32k:
+  // 43.7 against 47.2 us).  Ragged lengths keep about eight rounds of two per
+  // CU (four per CU measured 531.9 against 515.8 us on cfg3).
   const int GH = H / KVH;
   const int nw = propgen::pass2_waves(GH);
   const bool tuned = D == 128 && (GH == 4 || GH == 8);
+  const bool uniform = total_tiles < 0 || total_tiles == static_cast<long long>(B) * T_c;
   int per_round = (!tuned && nw < 4) ? flash::rows_per_round() / nw : 0;
+  if (tuned && uniform && static_cast<long long>(B) * KVH >= 32) per_round = flash::rows_per_round() / 4 * 2;
   if (!tuned) {
     const int r = propgen::pass2_resident(GH, D);
     if (r > 0) per_round = r;
