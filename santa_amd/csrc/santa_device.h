@@ -486,4 +486,41 @@ __device__ __forceinline__ int lane_xor(int v, int lane) {
   }
 }
 
+// Chunk sums of the finalize kernels: s += fv(c) and e += fe(c) (fe only
+// where with_e) over chunks c = 0 .. n - 1 in ascending order, the loads of up
+// to 32 chunks issued before the first add: full batches of 32, then one batch
+// of 8, 16 or 32 for what is left (loads past n repeat chunk n - 1 and are
+// not added).
+template <int NB, class FV, class FE>
+__device__ __forceinline__ void chunk_batch(int c0, int n, FV fv, FE fe, bool with_e, float& s, int& e) {
+  float v[NB];
+  int ev[NB];
+#pragma unroll
+  for (int i = 0; i < NB; ++i) {
+    const int c = min(c0 + i, n - 1);
+    v[i] = fv(c);
+    ev[i] = with_e ? fe(c) : 0;
+  }
+#pragma unroll
+  for (int i = 0; i < NB; ++i) {
+    if (c0 + i < n) {
+      s += v[i];
+      e += ev[i];
+    }
+  }
+}
+template <class FV, class FE>
+__device__ __forceinline__ void sum_chunks(int n, FV fv, FE fe, bool with_e, float& s, int& e) {
+  int c0 = 0;
+  for (; c0 + 32 <= n; c0 += 32) chunk_batch<32>(c0, n, fv, fe, with_e, s, e);
+  const int r = n - c0;
+  if (r > 16) {
+    chunk_batch<32>(c0, n, fv, fe, with_e, s, e);
+  } else if (r > 8) {
+    chunk_batch<16>(c0, n, fv, fe, with_e, s, e);
+  } else if (r > 0) {
+    chunk_batch<8>(c0, n, fv, fe, with_e, s, e);
+  }
+}
+
 }  // namespace santa

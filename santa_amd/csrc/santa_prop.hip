@@ -653,29 +653,13 @@ __global__ __launch_bounds__(kD) void finalize_kernel(const float* __restrict__ 
   if (seq_S) scale_out = (seq_S[b] > 0) ? (1.0f / static_cast<float>(seq_S[b])) : 0.0f;
   const float* pb = part + ((static_cast<size_t>(base) + kv) * GH + g) * kD + d;
   const size_t cstride = static_cast<size_t>(KVH) * GH * kD;
-  // chunks in ascending order; the loads of a batch of 32 are issued before
-  // the first add (one memory round trip per batch, not one per chunk)
-  constexpr int kBatch = 32;
+  // chunks in ascending order, up to 32 chunks' loads per memory round trip
   const bool emit = vrows && g == 0 && d == 0;
   float s = 0.0f;
   int e = 0;
-  for (int c0 = 0; c0 < nch; c0 += kBatch) {
-    float v[kBatch];
-    int ev[kBatch];
-#pragma unroll
-    for (int i = 0; i < kBatch; ++i) {
-      const int c = min(c0 + i, nch - 1);
-      v[i] = pb[static_cast<size_t>(c) * cstride];
-      ev[i] = emit ? part_emit[static_cast<size_t>(base) + c * KVH + kv] : 0;
-    }
-#pragma unroll
-    for (int i = 0; i < kBatch; ++i) {
-      if (c0 + i < nch) {
-        s += v[i];
-        e += ev[i];
-      }
-    }
-  }
+  sum_chunks(
+      nch, [&](int c) { return pb[static_cast<size_t>(c) * cstride]; },
+      [&](int c) { return part_emit[static_cast<size_t>(base) + c * KVH + kv]; }, emit, s, e);
   out[static_cast<size_t>(bh) * kD + d] = f32_to_h16<BF16>(s * scale_out);
   if (emit) vrows[bk] = e;
 }

@@ -979,30 +979,18 @@ __global__ __launch_bounds__(kMaxD) void finalize_kernel(const float* __restrict
     nch = max(0, min(nch, (n_wg - base - kv + KVH - 1) / KVH));
   }
   if (seq_S) scale_out = (seq_S[b] > 0) ? (1.0f / static_cast<float>(seq_S[b])) : 0.0f;
-  // the chunks' partials summed in chunk order, the loads of 32 chunks
-  // issued before the first is added (one memory round trip for the usual
-  // one-round plan of up to 32 chunks per (b, kv))
-  constexpr int kBatch = 32;
+  // the chunks' partials summed in chunk order, up to 32 chunks' loads per
+  // memory round trip
   const bool lead = vrows && g == 0 && d == 0;
   float s = 0.0f;
   int e = 0;
-  for (int c0 = 0; c0 < nch; c0 += kBatch) {
-    float v[kBatch];
-    int ev[kBatch];
-#pragma unroll
-    for (int j = 0; j < kBatch; ++j) {
-      const size_t slot = static_cast<size_t>(base) + static_cast<size_t>(min(c0 + j, nch - 1)) * KVH + kv;
-      v[j] = (d < D) ? part[(slot * GH + g) * D + d] : 0.0f;
-      ev[j] = lead ? part_emit[slot] : 0;
-    }
-#pragma unroll
-    for (int j = 0; j < kBatch; ++j) {
-      if (c0 + j < nch) {
-        s += v[j];
-        e += ev[j];
-      }
-    }
-  }
+  sum_chunks(
+      nch,
+      [&](int c) {
+        const size_t slot = static_cast<size_t>(base) + static_cast<size_t>(c) * KVH + kv;
+        return (d < D) ? part[(slot * GH + g) * D + d] : 0.0f;
+      },
+      [&](int c) { return part_emit[static_cast<size_t>(base) + static_cast<size_t>(c) * KVH + kv]; }, lead, s, e);
   if (d < D) out[static_cast<size_t>(bh) * D + d] = f32_to_h16<BF16>(s * scale_out);
   if (vrows && g == 0 && d == 0) vrows[static_cast<size_t>(b) * KVH + kv] = e;
 }
