@@ -442,7 +442,7 @@ std::string tile_pass_kernel(int64_t B, int64_t H, int64_t KVH, int64_t T_c, int
   TORCH_CHECK(B > 0 && H > 0 && KVH > 0 && H % KVH == 0 && T_c > 0, "bad shape");
   const std::string gh = "GH " + std::to_string(H / KVH);
   if (block_n == 256 && !santa::flash::uniform_small_pass(static_cast<int>(B), static_cast<int>(KVH),
-                                                         static_cast<int>(T_c)))
+                                                         static_cast<int>(T_c), static_cast<int>(H / KVH)))
     return "santa::flash::wave_kernel (block_n 256, " + gh +
            (santa::flash::rows_layout(static_cast<int>(KVH)) ? ", rows layout)" : ", four-wave layout)");
   return "santa::flash::tile_kernel (block_n " + std::to_string(block_n) + ", " + gh + ", online)";

@@ -1981,9 +1981,11 @@ static hipError_t launch_merge(const float* part, const int* pe, int dtype, int 
   const unsigned grid = static_cast<unsigned>(B) * static_cast<unsigned>(H);
   uint16_t* o = static_cast<uint16_t*>(out);
   const int max_chunks = seq_lens ? ((max_len + bn - 1) / bn + cs - 1) / cs : cpg;
-  if (max_chunks <= 64) {
-    // one wave per (b, h) up to 32 chunks, else four waves of 16 chunks
-    // each (B = 1 at 32k, 64 chunks: step 24.7 -> 23.6 us)
+  if (max_chunks <= 256) {
+    // one wave per (b, h) up to 32 chunks, else 4, 8 or 16 waves of 16
+    // chunks each, every load in one round trip (B = 1 at 32k, 64 chunks:
+    // step 24.7 -> 23.6 us; beyond 64 chunks the thread-group merge below
+    // took 20-26 us per call at B = 1, GH 8, 64k-96k tokens)
 #define SANTA_MERGE_WAVE(BF, G, NBC)                                                                          \
   hipLaunchKernelGGL((merge_wave_kernel<BF, G, NBC>), dim3(grid), dim3(64), 0, stream, part, pe, H, KVH, cpg, \
                      S_pt, o, m_star, vrows, seq_lens, bn, cs, max_len, n_wg, S_total)
@@ -1995,8 +1997,12 @@ static hipError_t launch_merge(const float* part, const int* pe, int dtype, int 
     SANTA_MERGE_WAVE(BF, G, 16);        \
   else if (max_chunks <= 32)            \
     SANTA_MERGE_WAVE(BF, G, 32);        \
+  else if (max_chunks <= 64)            \
+    SANTA_MERGE_SPLIT(BF, G, 4);        \
+  else if (max_chunks <= 128)           \
+    SANTA_MERGE_SPLIT(BF, G, 8);        \
   else                                  \
-    SANTA_MERGE_SPLIT(BF, G, 4)
+    SANTA_MERGE_SPLIT(BF, G, 16)
     if (dtype == SANTA_BF16) {
       if (GH == 4) { SANTA_MERGE_NB(true, 4); } else { SANTA_MERGE_NB(true, 8); }
     } else {
@@ -2004,6 +2010,7 @@ static hipError_t launch_merge(const float* part, const int* pe, int dtype, int 
     }
 #undef SANTA_MERGE_NB
 #undef SANTA_MERGE_WAVE
+#undef SANTA_MERGE_SPLIT
     return hipGetLastError();
   }
   // thread groups of 128: enough that each merges at most 16 chunks (up to 8)
@@ -2231,8 +2238,14 @@ int rows_per_round() { return 4 * resident_workgroups(); }
 // tile kernel, four waves per tile, whose per-tile latency chain is a
 // quarter of a wave's (B = 1, 4k tokens: 13.0 against 31.2 us per step; B =
 // 1, 32k: 26.5 against 36.2 us).  Above it the wave kernel is faster (B = 4,
-// 32k: 60.9 against 63.9 us).
-bool small_pass(long long kv_tiles) { return kv_tiles <= rows_per_round(); }
+// 32k: 60.9 against 63.9 us).  At GH 8 the tile kernel holds one workgroup
+// per CU (its registers), one wave per SIMD, and keeps the tile pass only up
+// to 1 / kGh8SmallDiv of a round of (kv, tile) items, uniform or ragged.
+constexpr int kGh8SmallDiv = 4;
+static long long gh8_small_items() { return rows_per_round() / kGh8SmallDiv; }
+bool small_pass(long long kv_tiles, int GH) {
+  return kv_tiles <= (GH == 8 ? gh8_small_items() : static_cast<long long>(rows_per_round()));
+}
 // santa_prop's vec pass 1 takes the tile kernel below a quarter of that: the
 // [L, H] stash it writes costs pass 2 four 2-byte loads per lane and row pair
 // where the tile-major one costs one, which outweighs the shorter pass 1 from
@@ -2249,8 +2262,9 @@ bool prop_wave_pass1(int path, int GH, int block_n) {
 // against 50.8 us for the rows layout, and the two meet near 4,096 items
 // (B = 4: 66.4 against 67.2 us at T_c = 129; B = 8 is 10 % faster on the rows
 // layout).  Ragged grids keep the one-round threshold.
-bool uniform_small_pass(int B, int KVH, int T_c) {
-  return static_cast<long long>(B) * KVH * T_c <= static_cast<long long>(rows_per_round()) * 3 / 2;
+bool uniform_small_pass(int B, int KVH, int T_c, int GH) {
+  const long long items = static_cast<long long>(B) * KVH * T_c;
+  return items <= (GH == 8 ? gh8_small_items() : static_cast<long long>(rows_per_round()) * 3 / 2);
 }
 
 // Ragged batches: chunks small enough for about eight resident rounds over
@@ -2379,7 +2393,7 @@ struct FlashWs {
 };
 FlashWs flash_ws_layout(int B, int H, int KVH, int T_c) {
   FlashWs w{};
-  const bool rows = flash::rows_layout(KVH) && !flash::uniform_small_pass(B, KVH, T_c);
+  const bool rows = flash::rows_layout(KVH) && !flash::uniform_small_pass(B, KVH, T_c, H / KVH);
   flash::chunk_plan(B, KVH, T_c, &w.cs, &w.cpg, rows ? flash::rows_per_round() : 0);
   const size_t chunks = static_cast<size_t>(B) * KVH * w.cpg;
   const int GH = H / KVH;
@@ -2435,7 +2449,7 @@ extern "C" int santa_flash_decode_tiles(const void* q, const void* K, const void
   flash::Args a{q, K, V, B, H, KVH, L_valid, L_storage, T_c, S_per_tile, seed, nullptr, nullptr, nullptr, nullptr,
                 nullptr, reinterpret_cast<float*>(base + w.part), reinterpret_cast<int*>(base + w.emit), w.cs, w.cpg,
                 nullptr};
-  const bool wave = block_n == 256 && !flash::uniform_small_pass(B, KVH, T_c);
+  const bool wave = block_n == 256 && !flash::uniform_small_pass(B, KVH, T_c, H / KVH);
   const hipError_t e = wave ? flash::launch_wave(dtype, H / KVH, a, nullptr, nullptr, nullptr, stream)
                             : flash::launch_tiles<flash::kOnline>(dtype, H / KVH, block_n, a, stream);
   if (e != hipSuccess) return set_error(SANTA_ERR_HIP, "tile launch failed: %s", hipGetErrorString(e));
@@ -2567,7 +2581,7 @@ extern "C" size_t santa_flash_ragged_workspace_size(int B, int H, int KVH, int D
   // both plans a call may take (the small one only at block_n 256, which
   // this size does not know about)
   size_t bytes = ragged_ws_layout(B, H, KVH, total_tiles, max_tiles).total;
-  if (flash::small_pass(total_tiles * KVH))
+  if (flash::small_pass(total_tiles * KVH, H / KVH))
     bytes = std::max(bytes, ragged_ws_layout(B, H, KVH, total_tiles, max_tiles, true).total);
   return bytes;
 }
@@ -2586,7 +2600,7 @@ static int flash_decode_ragged(const void* q, const void* K, const void* V, int 
     return set_error(SANTA_ERR_INVALID, "total_tiles out of range");
   // little K: the tile kernel, for contiguous and paged caches alike (so that
   // the two stay bit-identical)
-  const bool small = block_n == 256 && flash::small_pass(total_tiles * KVH);
+  const bool small = block_n == 256 && flash::small_pass(total_tiles * KVH, H / KVH);
   const RaggedWs w = ragged_ws_layout(B, H, KVH, total_tiles, T_c, small);
   if (!workspace || workspace_bytes < w.total)
     return set_error(SANTA_ERR_WORKSPACE, "workspace too small: need %zu bytes, got %zu", w.total, workspace_bytes);

@@ -54,14 +54,14 @@ void plan_ragged(int B, int KVH, long long total_tiles, int max_tiles, int* cs, 
 // The flash tile pass's layout: one wave per KV head (ROWS) for KVH = 8, its
 // chunks planned for rows_per_round() items per round.
 bool rows_layout(int KVH);
-// A tile pass with at most one resident round of (kv, tile) items runs four
-// waves per tile (tile_kernel) rather than one (wave_kernel); for santa_prop's
-// vec pass 1 that also means the [L, H] stash layout.
-bool small_pass(long long kv_tiles);
+// A tile pass with at most one resident round of (kv, tile) items (a quarter of
+// one at GH 8) runs four waves per tile (tile_kernel) rather than one
+// (wave_kernel).
+bool small_pass(long long kv_tiles, int GH);
 // Uniform (one length) flash calls keep the tile kernel up to one and a half
-// resident rounds; the launch, the workspace plan and the bench label all
-// decide with this one function.
-bool uniform_small_pass(int B, int KVH, int T_c);
+// resident rounds (a quarter of one at GH 8); the launch, the workspace plan and
+// the bench label all decide with this one function.
+bool uniform_small_pass(int B, int KVH, int T_c, int GH);
 bool small_prop_pass(long long kv_tiles);
 // santa_prop's pass 1 on the wave kernel (block_n 256: the vec path at GH 4,
 // the general path at GH 8); it writes the tile-major stash when given a

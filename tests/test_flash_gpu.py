@@ -177,6 +177,8 @@ def test_device_expf_matches_oracle():
         (2, 32, 8, 50000, 256, -1, torch.float16),     # f16 above the small pass: the production call on the rows kernel
         (1, 64, 8, 100000, 512, -1, torch.float16),    # f16 GH 8 above the small pass
         (1, 32, 8, 300000, 2048, -1, torch.bfloat16),  # 1,172 tiles: 235 chunks per (b, h), the many-chunk merge
+        (1, 64, 8, 24000, 512, -1, torch.bfloat16),    # GH 8, 752 items: the wave kernel above its 512-item small pass, 94 chunks (eight-wave merge)
+        (2, 64, 8, 20000, 300, -1, torch.bfloat16),    # GH 8, B = 2: 79 chunks per (b, h)
         (2, 16, 4, 9000, 256, -1, torch.bfloat16),     # KVH 4: the four-wave layout
         (1, 8, 2, 5000, 64, 4500, torch.bfloat16),     # KVH 2, valid_len < storage
     ],
