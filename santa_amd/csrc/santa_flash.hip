@@ -873,7 +873,11 @@ __global__ __launch_bounds__(ROWS ? 512 : kThreads, ROWS ? 1 : 2) void wave_kern
   const GridPos gp = grid_pos(wg, seq_lens, B, ROWS ? 1 : KVH, BN, L_valid, T_c, cs, cpg);
   const int kv = ROWS ? wave : gp.kv;
   const int b = gp.b < 0 ? 0 : gp.b;
-  const int h0 = kv * GH;
+  // heads per KV head: GH, except that santa_prop's pass 1 at GH 8 also takes
+  // groups of 5-7 heads (santa_prop's generic shapes at D = 128), the second
+  // head block's last heads then zero and never written (tile-major stash only)
+  const int gsz = (P1 && GH == 8) ? H / KVH : GH;
+  const int h0 = kv * gsz;
   L_valid = gp.len;
   const int t_begin = gp.chunk * cs;
   const int t_end = (gp.b < 0) ? t_begin : min(gp.n_tiles, t_begin + cs);
@@ -897,10 +901,11 @@ __global__ __launch_bounds__(ROWS ? 512 : kThreads, ROWS ? 1 : 2) void wave_kern
   float qa[NHB][8];
 #pragma unroll
   for (int hb = 0; hb < NHB; ++hb) {
-    const uint16_t* qh = Q + (static_cast<size_t>(b) * H + h0 + 4 * hb + (lane & 3)) * kD + (lane >> 2);
+    const int gq = 4 * hb + (lane & 3);
+    const uint16_t* qh = Q + (static_cast<size_t>(b) * H + h0 + min(gq, gsz - 1)) * kD + (lane >> 2);
 #pragma unroll
     for (int m = 0; m < 8; ++m) {
-      qa[hb][m] = h16_to_f32<BF16>(qh[16 * m]) * q_scale;
+      qa[hb][m] = (gq < gsz) ? h16_to_f32<BF16>(qh[16 * m]) * q_scale : 0.0f;
       // pass 1 of GH 8 is santa_prop's general path: q rounded to the 16-bit
       // type after scaling (prop/santa_cuda_kernel.cu:121-140)
       if constexpr (P1 && GH == 8) qa[hb][m] = h16_to_f32<BF16>(f32_to_h16<BF16>(qa[hb][m]));
@@ -1195,7 +1200,7 @@ __global__ __launch_bounds__(ROWS ? 512 : kThreads, ROWS ? 1 : 2) void wave_kern
 #pragma unroll
         for (int k = 0; k < 4; ++k) {
           const size_t mt = (static_cast<size_t>(b) * H + h0 + 4 * hb + k) * T_c + t;
-          if (lane == 0) {
+          if (lane == 0 && 4 * hb + k < gsz) {
             dbg_m[mt] = mg[4 * hb + k];
             dbg_ell[mt] = ell[k];
           }
@@ -1314,21 +1319,24 @@ __global__ __launch_bounds__(ROWS ? 512 : kThreads, ROWS ? 1 : 2) void wave_kern
         for (int g = 0; g < GH; ++g)
 #pragma unroll
           for (int hh = 0; hh < 2; ++hh)
-            __builtin_amdgcn_raw_buffer_store_b32(
-                ubits[g][hh][0] | (ubits[g][hh][1] << 16), rs,
-                2 * (((t * H + h0 + g) * BN) + 128 * hh + 32 * jrow + 2 * qq), 0, kBufferNontemporal);
+            if (g < gsz)
+              __builtin_amdgcn_raw_buffer_store_b32(
+                  ubits[g][hh][0] | (ubits[g][hh][1] << 16), rs,
+                  2 * (((t * H + h0 + g) * BN) + 128 * hh + 32 * jrow + 2 * qq), 0, kBufferNontemporal);
       } else {
 #pragma unroll
         for (int g = 0; g < GH; ++g)
 #pragma unroll
           for (int hh = 0; hh < 2; ++hh)
-            *reinterpret_cast<uint32_t*>(u_stash + static_cast<size_t>(b) * H * stash_ld +
-                                         (static_cast<size_t>(t) * H + h0 + g) * BN + 128 * hh + 32 * jrow + 2 * qq) =
-                ubits[g][hh][0] | (ubits[g][hh][1] << 16);
+            if (g < gsz)
+              *reinterpret_cast<uint32_t*>(u_stash + static_cast<size_t>(b) * H * stash_ld +
+                                           (static_cast<size_t>(t) * H + h0 + g) * BN + 128 * hh + 32 * jrow +
+                                           2 * qq) = ubits[g][hh][0] | (ubits[g][hh][1] << 16);
       }
     } else if constexpr (P1) {
       // the stash row [n, h0 .. h0+GH) of each valid row: one 8-B (GH 4) or
-      // 16-B (GH 8) store
+      // 16-B (GH 8) store (whole groups only: the launcher takes groups of 5-7
+      // heads with the tile-major stash alone)
 #pragma unroll
       for (int hh = 0; hh < 2; ++hh)
 #pragma unroll
@@ -2145,7 +2153,10 @@ hipError_t launch_prop_pass1(const void* q, const void* K, int dtype, int B, int
     chunk_plan(B, KVH, a.T_c, &a.cs, &a.cpg);
   }
   const int GH = H / KVH;
-  if (prop_wave_pass1(path, GH, block_n)) {
+  // groups of 5-7 heads with the tile-major stash: the GH 8 kernel, the last
+  // heads of each group zero (santa_prop's generic shapes at D = 128)
+  const bool pad8 = path == 1 && block_n == 256 && GH >= 5 && GH <= 7 && stash_ld > 0;
+  if (prop_wave_pass1(path, GH, block_n) || pad8) {
     // block_n 256 on the wave kernel -- GH 4 with the vec path's numerics,
     // GH 8 with the general path's; for KVH = 8 in its rows form, with a
     // plan of its own (pass 1 writes no chunk partials, so it need not share

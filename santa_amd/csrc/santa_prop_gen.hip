@@ -996,6 +996,10 @@ __global__ __launch_bounds__(kMaxD) void finalize_kernel(const float* __restrict
 }
 
 // ---------------------------------------------------------------- launchers
+// (kv, tile) items from which GH 5-7 at D = 128 take santa_flash's GH 8 pass 1
+// (one resident round of single-wave items; at 1,024 the two measured level)
+constexpr long long kPad8Items = 2048;
+
 hipError_t launch_pass1(const void* q, const void* K, int dtype, int B, int H, int KVH, int D, int L, int L_storage,
                         int BN, float* m_tiles, float* ell_tiles, uint16_t* u_stash, const int* seq_lens,
                         long long total_tiles, PageTable pt, hipStream_t stream, int stash_ld) {
@@ -1006,6 +1010,19 @@ hipError_t launch_pass1(const void* q, const void* K, int dtype, int B, int H, i
   const uint16_t* Qh = static_cast<const uint16_t*>(q);
   const uint16_t* Kh = static_cast<const uint16_t*>(K);
   const int GH = H / KVH;
+  const long long items = (seq_lens ? total_tiles : static_cast<long long>(B) * T_c) * KVH;
+  if (D == 128 && BN == 256 && GH >= 5 && GH <= 7 && stash_ld > 0 && items >= kPad8Items) {
+    // two head blocks at D = 128 with the tile-major stash and at least one
+    // resident round of items: santa_flash's GH 8 pass-1 wave kernel, the last
+    // heads of each group zero (the same general numerics, so the same bits;
+    // 28q/4kv at 32k tokens: B = 8 step 140.6 -> 99.3 us, B = 4 82.9 -> 64.2;
+    // 40q/8kv, B = 8: 245.1 -> 152.5 us).  With fewer items the generic kernel
+    // stays (B = 1: 43.3 against 49.0 us on the wave kernel)
+    int cs = 0, n_wg = 0;
+    if (seq_lens) flash::plan_ragged(B, KVH, total_tiles, T_c, &cs, &n_wg);
+    return flash::launch_prop_pass1(q, K, dtype, B, H, KVH, L, L_storage, BN, 1, m_tiles, ell_tiles, u_stash,
+                                    seq_lens, cs, n_wg, stash_ld, stream, pt, total_tiles);
+  }
   if (fast_pass1_shape(GH, D, BN)) {
     // head blocks of four: GH 1-4 -> 1, 5-8 -> 2, 9-16 -> 4
     const int nhb = GH <= 4 ? 1 : (GH <= 8 ? 2 : 4);

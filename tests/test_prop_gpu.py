@@ -191,6 +191,9 @@ def test_prop_fast_generic_pass1(H, KVH, D, L, S, monkeypatch):
     (32, 32, 128, 32700, 512),   # MHA: chunks of 8 tiles per workgroup, the next tile's rows in registers
     (32, 4, 64, 40000, 600),     # GH 8 at D 64 (two head blocks, registers): chunks of 2 tiles
     (8, 2, 256, 40000, 300),     # GH 4 at D 256 (one workgroup per CU): chunks of 2 tiles
+    (28, 4, 128, 140000, 512),   # GH 7 at D 128, 2,188 items: santa_flash's GH 8 pass-1 wave kernel, four-wave layout
+    (40, 8, 128, 70000, 300),    # GH 5, 2,192 items: the GH 8 wave kernel in its rows layout
+    (28, 4, 128, 32700, 512),    # GH 7 below 2,048 items: the generic kernel
 ])
 def test_prop_fast_generic_streaming(H, KVH, D, L, S, monkeypatch):
     """The generic pass 1 streaming a chunk of tiles per workgroup (one
