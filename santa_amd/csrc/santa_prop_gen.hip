@@ -665,8 +665,8 @@ __device__ __forceinline__ void load_dims(const uint16_t* p, uint16_t (&v)[DPL])
 
 // T256: block_n is 256 (the two-rows-per-lane path only; compiled apart so
 // that the other path's per-piece bounds are not computed for it).  NK: the
-// most heads a wave takes (1 for GH <= 4, else kMaxHeadsPerWave), which
-// sizes the unrolled per-head state.
+// most heads a wave takes (1 for GH <= 4, 2 for GH <= 8, else
+// kMaxHeadsPerWave), which sizes the unrolled per-head state.
 template <bool BF16, bool PAGED, int DPL, bool T256, int NK>
 __global__ __launch_bounds__(kThreads) void pass2_kernel(const uint16_t* __restrict__ V,
                                                          const uint16_t* __restrict__ u_stash, int H, int KVH, int D,
@@ -703,7 +703,7 @@ __global__ __launch_bounds__(kThreads) void pass2_kernel(const uint16_t* __restr
   int* const s_flag = s_p2 + 2 * nwv * BN;
   int* const s_nemit = s_flag + BN;
 
-  static_assert(NK == 1 || NK == kMaxHeadsPerWave, "heads per wave");
+  static_assert(NK == 1 || NK == 2 || NK == kMaxHeadsPerWave, "heads per wave");
   float acc[NK][DPL];
 #pragma unroll
   for (int k = 0; k < NK; ++k)
@@ -926,9 +926,9 @@ static int pass2_blocks_per_cu_dpl(int dpl, int threads, size_t lds) {
 // Cached per (device, D class, waves per workgroup and heads per wave).
 int pass2_resident(int GH, int D) {
   constexpr int kMaxDev = 64;
-  static std::atomic<int> cached[kMaxDev][5][5];  // [dev][DPL class][waves - 1, or 4 for GH > 4]
+  static std::atomic<int> cached[kMaxDev][5][6];  // [dev][DPL class][waves - 1; 4 for GH 5-8, 5 above]
   const int nw = pass2_waves(GH);
-  const int wi = GH > 4 ? 4 : nw - 1;
+  const int wi = GH > 8 ? 5 : (GH > 4 ? 4 : nw - 1);
   const int dpl = pass2_dpl(D);
   const int di = dpl == 1 ? 0 : (dpl == 2 ? 1 : (dpl == 4 ? 2 : (dpl == 8 ? 3 : 4)));
   int dev = 0;
@@ -949,7 +949,8 @@ int pass2_resident(int GH, int D) {
   const int threads = 64 * nw;
   const size_t lds = pass2_lds_bytes(nw, kMaxBN);
   const int per_cu = GH <= 4 ? pass2_blocks_per_cu_dpl<1>(dpl, threads, lds)
-                             : pass2_blocks_per_cu_dpl<kMaxHeadsPerWave>(dpl, threads, lds);
+                             : (GH <= 8 ? pass2_blocks_per_cu_dpl<2>(dpl, threads, lds)
+                                        : pass2_blocks_per_cu_dpl<kMaxHeadsPerWave>(dpl, threads, lds));
   if (per_cu <= 0) return 0;
   const int r = per_cu * cus;
   if (slot) cached[dev][di][wi].store(r, std::memory_order_relaxed);
@@ -1119,6 +1120,11 @@ hipError_t launch_pass2(const void* V, const uint16_t* u_stash, int dtype, int B
         SANTA_GP2_K(BF, PG, DP, true, 1);                     \
       else                                                    \
         SANTA_GP2_K(BF, PG, DP, false, 1);                    \
+    } else if (H / KVH <= 8) {                                \
+      if (BN == 256)                                          \
+        SANTA_GP2_K(BF, PG, DP, true, 2);                     \
+      else                                                    \
+        SANTA_GP2_K(BF, PG, DP, false, 2);                    \
     } else {                                                  \
       if (BN == 256)                                          \
         SANTA_GP2_K(BF, PG, DP, true, kMaxHeadsPerWave);      \
