@@ -88,7 +88,7 @@ void plan_chunks(int B, int KVH, int T_c, int* cs, int* cpg, int per_round = 0);
 
 namespace propgen {
 // santa_prop's shapes outside the tuned kernels (santa_prop_gen.hip): any
-// GH <= 16, D a multiple of 16 up to 256, block_n a multiple of 16 up to 512.
+// GH <= 16, D a multiple of 16 up to 1024, block_n a multiple of 16 up to 512.
 // generic_shape: the shape is not one the tuned kernels take (D = 128, GH 4
 // or 8, block_n 32 / 64 / 256); shape_supported: the generic kernels take it.
 bool generic_shape(int GH, int D, int block_n);
