@@ -855,7 +855,7 @@ __global__ __launch_bounds__(ROWS ? 512 : kThreads, ROWS ? 1 : 2) void wave_kern
     int L_valid, int L_storage, int T_c, int cs, int cpg, float q_scale, int S_pt, uint64_t seed,
     float* __restrict__ part, int* __restrict__ part_emit, const int* __restrict__ seq_lens, int B, long long S_total,
     float* __restrict__ dbg_m, float* __restrict__ dbg_ell, int16_t* __restrict__ dbg_counts,
-    uint16_t* __restrict__ u_stash, int stash_ld, PageTable pt, int stash_nt) {
+    uint16_t* __restrict__ u_stash, int stash_ld, PageTable pt, int stash_nt, int kv_div) {
   constexpr int BN = 256;
   constexpr int NHB = GH / 4;
   constexpr int LCAP = kWaveListCap;
@@ -891,11 +891,15 @@ __global__ __launch_bounds__(ROWS ? 512 : kThreads, ROWS ? 1 : 2) void wave_kern
   int2* const list = s_list + wave * GH * LCAP;
 
   // Paged: the base is the pool's (plus this KV head), rows go through pt.
-  const size_t row_stride = static_cast<size_t>(KVH) * kD;
-  const uint32_t row_bytes = static_cast<uint32_t>(KVH) * kD * 2u;
+  // kv_div > 1 (santa_prop's pass 1 at GH 10-16): KVH counts virtual KV heads,
+  // kv_div of them per cache KV head, each taking 8 of its query heads; wave
+  // kv reads the rows of cache KV head kv / kv_div (1 everywhere else).
+  const int kvc = kv / kv_div;
+  const size_t row_stride = static_cast<size_t>(KVH / kv_div) * kD;
+  const uint32_t row_bytes = static_cast<uint32_t>(KVH / kv_div) * kD * 2u;
   const size_t seq_off = PAGED ? 0 : static_cast<size_t>(b) * L_storage * row_stride;
-  const char* Kg = reinterpret_cast<const char*>(K + seq_off + static_cast<size_t>(kv) * kD);
-  const char* Vg = reinterpret_cast<const char*>(V + seq_off + static_cast<size_t>(kv) * kD);
+  const char* Kg = reinterpret_cast<const char*>(K + seq_off + static_cast<size_t>(kvc) * kD);
+  const char* Vg = reinterpret_cast<const char*>(V + seq_off + static_cast<size_t>(kvc) * kD);
   const uint32_t v_lane_off = 4u * static_cast<uint32_t>(lane);
 
   float qa[NHB][8];
@@ -1929,14 +1933,14 @@ static hipError_t launch_wave_t(const Args& a, float* dbg_m, float* dbg_ell, int
                          dim3(static_cast<unsigned>(64 * a.KVH)), 0, stream, static_cast<const uint16_t*>(a.q),
                          static_cast<const uint16_t*>(a.K), static_cast<const uint16_t*>(a.V), a.H, a.KVH, a.L_valid,
                          a.L_storage, a.T_c, a.cs, a.cpg, q_scale, a.S_pt, a.seed, a.part, a.part_emit, a.seq_lens,
-                         a.B, a.S_total, dbg_m, dbg_ell, dbg_counts, nullptr, 0, a.pt, 0);
+                         a.B, a.S_total, dbg_m, dbg_ell, dbg_counts, nullptr, 0, a.pt, 0, 1);
       return hipGetLastError();
     }
     hipLaunchKernelGGL((wave_kernel<BF16, GH, true>), dim3(grid), dim3(kThreads), 0, stream,
                        static_cast<const uint16_t*>(a.q), static_cast<const uint16_t*>(a.K),
                        static_cast<const uint16_t*>(a.V), a.H, a.KVH, a.L_valid, a.L_storage, a.T_c, a.cs, a.cpg,
                        q_scale, a.S_pt, a.seed, a.part, a.part_emit, a.seq_lens, a.B, a.S_total, dbg_m, dbg_ell,
-                       dbg_counts, nullptr, 0, a.pt, 0);
+                       dbg_counts, nullptr, 0, a.pt, 0, 1);
   } else if (rows_layout(a.KVH)) {
     // one workgroup of KVH waves per (sequence, chunk) item
     const unsigned rgrid = grid / static_cast<unsigned>(a.KVH);
@@ -1946,25 +1950,25 @@ static hipError_t launch_wave_t(const Args& a, float* dbg_m, float* dbg_ell, int
                          static_cast<const uint16_t*>(a.q), static_cast<const uint16_t*>(a.K),
                          static_cast<const uint16_t*>(a.V), a.H, a.KVH, a.L_valid, a.L_storage, a.T_c, a.cs, a.cpg,
                          q_scale, a.S_pt, a.seed, a.part, a.part_emit, a.seq_lens, a.B, a.S_total, nullptr,
-                         nullptr, nullptr, nullptr, 0, a.pt, 0);
+                         nullptr, nullptr, nullptr, 0, a.pt, 0, 1);
     else
       hipLaunchKernelGGL((wave_kernel<BF16, GH, false, false, false, true>), dim3(rgrid), block, 0, stream,
                          static_cast<const uint16_t*>(a.q), static_cast<const uint16_t*>(a.K),
                          static_cast<const uint16_t*>(a.V), a.H, a.KVH, a.L_valid, a.L_storage, a.T_c, a.cs, a.cpg,
                          q_scale, a.S_pt, a.seed, a.part, a.part_emit, a.seq_lens, a.B, a.S_total, nullptr,
-                         nullptr, nullptr, nullptr, 0, a.pt, 0);
+                         nullptr, nullptr, nullptr, 0, a.pt, 0, 1);
   } else if (a.pt.table) {
     hipLaunchKernelGGL((wave_kernel<BF16, GH, false, false, true>), dim3(grid), dim3(kThreads), 0, stream,
                        static_cast<const uint16_t*>(a.q), static_cast<const uint16_t*>(a.K),
                        static_cast<const uint16_t*>(a.V), a.H, a.KVH, a.L_valid, a.L_storage, a.T_c, a.cs, a.cpg,
                        q_scale, a.S_pt, a.seed, a.part, a.part_emit, a.seq_lens, a.B, a.S_total, nullptr,
-                       nullptr, nullptr, nullptr, 0, a.pt, 0);
+                       nullptr, nullptr, nullptr, 0, a.pt, 0, 1);
   } else {
     hipLaunchKernelGGL((wave_kernel<BF16, GH, false>), dim3(grid), dim3(kThreads), 0, stream,
                        static_cast<const uint16_t*>(a.q), static_cast<const uint16_t*>(a.K),
                        static_cast<const uint16_t*>(a.V), a.H, a.KVH, a.L_valid, a.L_storage, a.T_c, a.cs, a.cpg,
                        q_scale, a.S_pt, a.seed, a.part, a.part_emit, a.seq_lens, a.B, a.S_total, nullptr,
-                       nullptr, nullptr, nullptr, 0, a.pt, 0);
+                       nullptr, nullptr, nullptr, 0, a.pt, 0, 1);
   }
   return hipGetLastError();
 }
@@ -2140,7 +2144,7 @@ hipError_t launch_mfma_check(const float* a, const float* b, const float* c, flo
 hipError_t launch_prop_pass1(const void* q, const void* K, int dtype, int B, int H, int KVH, int L, int L_storage,
                              int block_n, int path, float* m_tiles, float* ell_tiles, uint16_t* u_stash,
                              const int* seq_lens, int cs, int n_wg, int stash_ld, hipStream_t stream,
-                             PageTable pt, long long total_tiles) {
+                             PageTable pt, long long total_tiles, int kv_div) {
   Args a{q, K, nullptr, B, H, KVH, L, L_storage, (L + block_n - 1) / block_n, 0, 0, m_tiles, ell_tiles, nullptr,
          nullptr, nullptr, nullptr, nullptr, 0, 0, u_stash, seq_lens};
   a.pt = pt;
@@ -2156,6 +2160,8 @@ hipError_t launch_prop_pass1(const void* q, const void* K, int dtype, int B, int
   // groups of 5-7 heads with the tile-major stash: the GH 8 kernel, the last
   // heads of each group zero (santa_prop's generic shapes at D = 128)
   const bool pad8 = path == 1 && block_n == 256 && GH >= 5 && GH <= 7 && stash_ld > 0;
+  if (kv_div != 1 && !(path == 1 && block_n == 256 && GH >= 5 && GH <= 8 && stash_ld > 0 && KVH % kv_div == 0))
+    return hipErrorInvalidValue;  // virtual KV heads: the GH 8 wave kernel with the tile-major stash only
   if (prop_wave_pass1(path, GH, block_n) || pad8) {
     // block_n 256 on the wave kernel -- GH 4 with the vec path's numerics,
     // GH 8 with the general path's; for KVH = 8 in its rows form, with a
@@ -2200,7 +2206,7 @@ hipError_t launch_prop_pass1(const void* q, const void* K, int dtype, int B, int
   hipLaunchKernelGGL((wave_kernel<BF, G, false, true, PG, RW>), dim3(grid), block, 0, stream,                     \
                      static_cast<const uint16_t*>(a.q), static_cast<const uint16_t*>(a.K), nullptr, a.H, a.KVH,     \
                      a.L_valid, a.L_storage, a.T_c, a.cs, a.cpg, q_scale, 0, 0ULL, nullptr, nullptr, a.seq_lens,   \
-                     a.B, 0LL, m_tiles, ell_tiles, nullptr, u_stash, stash_ld, a.pt, stash_nt)
+                     a.B, 0LL, m_tiles, ell_tiles, nullptr, u_stash, stash_ld, a.pt, stash_nt, kv_div)
 #define SANTA_P1_GH(BF, PG, RW)    \
   do {                             \
     if (GH == 4)                   \

@@ -40,10 +40,14 @@ namespace flash {
 // workgroups (any workgroup past the last sequence exits at once).
 // stash_ld > 0 (vec path only): the stash is tile-major [B, stash_ld / 256, H, 256],
 // whole 256-row tiles, 0 past each sequence's length.
+// kv_div > 1: KVH counts virtual KV heads, kv_div per KV head of the cache,
+// each with H / KVH (5-8) query heads (the general path at block_n 256 with
+// the tile-major stash only).
 hipError_t launch_prop_pass1(const void* q, const void* K, int dtype, int B, int H, int KVH, int L, int L_storage,
                              int block_n, int path, float* m_tiles, float* ell_tiles, uint16_t* u_stash,
                              const int* seq_lens, int cs, int n_wg, int stash_ld, hipStream_t stream,
-                             PageTable pt = PageTable{nullptr, 0, 3, 1}, long long total_tiles = -1);
+                             PageTable pt = PageTable{nullptr, 0, 3, 1}, long long total_tiles = -1,
+                             int kv_div = 1);
 // Chunking of a ragged batch with total_tiles tiles, the longest sequence
 // having max_tiles: cs tiles per chunk and an upper bound n_wg on the
 // workgroups of the ragged grid.

@@ -1011,18 +1011,24 @@ hipError_t launch_pass1(const void* q, const void* K, int dtype, int B, int H, i
   const uint16_t* Qh = static_cast<const uint16_t*>(q);
   const uint16_t* Kh = static_cast<const uint16_t*>(K);
   const int GH = H / KVH;
-  const long long items = (seq_lens ? total_tiles : static_cast<long long>(B) * T_c) * KVH;
-  if (D == 128 && BN == 256 && GH >= 5 && GH <= 7 && stash_ld > 0 && items >= kPad8Items) {
-    // two head blocks at D = 128 with the tile-major stash and at least one
-    // resident round of items: santa_flash's GH 8 pass-1 wave kernel, the last
-    // heads of each group zero (the same general numerics, so the same bits;
-    // 28q/4kv at 32k tokens: B = 8 step 140.6 -> 99.3 us, B = 4 82.9 -> 64.2;
-    // 40q/8kv, B = 8: 245.1 -> 152.5 us).  With fewer items the generic kernel
-    // stays (B = 1: 43.3 against 49.0 us on the wave kernel)
+  // GH 10, 12, 14, 16: two virtual KV heads per cache KV head, each with half
+  // its query heads (5-8), on the same kernel; each cache row is read by the
+  // two virtual heads' waves at about the same time
+  const int kvd = (GH >= 10 && GH <= 16 && GH % 2 == 0) ? 2 : 1;
+  const int ghv = GH / kvd;
+  const long long items = (seq_lens ? total_tiles : static_cast<long long>(B) * T_c) * KVH * kvd;
+  if (D == 128 && BN == 256 && ghv >= 5 && ghv <= (kvd == 2 ? 8 : 7) && stash_ld > 0 && items >= kPad8Items) {
+    // two or more head blocks at D = 128 with the tile-major stash and at
+    // least one resident round of items: santa_flash's GH 8 pass-1 wave
+    // kernel, the last heads of each (virtual) group zero (the same general
+    // numerics, so the same bits; 28q/4kv at 32k tokens: B = 8 step 140.6 ->
+    // 99.3 us, B = 4 82.9 -> 64.2; 40q/8kv, B = 8: 245.1 -> 152.5 us; 64q/4kv
+    // 353.6 -> 156.0 us; 128q/8kv 658.5 -> 305.2 us).  With fewer items the
+    // generic kernel stays (28q/4kv, B = 1: 43.3 against 49.0 us)
     int cs = 0, n_wg = 0;
-    if (seq_lens) flash::plan_ragged(B, KVH, total_tiles, T_c, &cs, &n_wg);
-    return flash::launch_prop_pass1(q, K, dtype, B, H, KVH, L, L_storage, BN, 1, m_tiles, ell_tiles, u_stash,
-                                    seq_lens, cs, n_wg, stash_ld, stream, pt, total_tiles);
+    if (seq_lens) flash::plan_ragged(B, KVH * kvd, total_tiles, T_c, &cs, &n_wg);
+    return flash::launch_prop_pass1(q, K, dtype, B, H, KVH * kvd, L, L_storage, BN, 1, m_tiles, ell_tiles, u_stash,
+                                    seq_lens, cs, n_wg, stash_ld, stream, pt, total_tiles, kvd);
   }
   if (fast_pass1_shape(GH, D, BN)) {
     // head blocks of four: GH 1-4 -> 1, 5-8 -> 2, 9-16 -> 4

@@ -208,6 +208,7 @@ def test_cfg5_prop_leg_parity():
     (24, 8, 256, [4100, 2600], [70, 33], 256, 64),             # GH 3, D 256, fast generic pass 1
     (28, 4, 128, [70000, 50000, 30000], [800, 600, 100], 256, 64),  # GH 7, 2,352 items: the GH 8 wave kernel's pass 1
     (48, 8, 128, [40000, 40000], [300, 500], 256, 256),        # GH 6, 2,504 items, equal lengths: the uniform plan
+    (64, 4, 128, [50000, 30000, 20000], [600, 300, 90], 256, 64),  # GH 16 on virtual KV heads, ragged and paged
 ])
 def test_prop_general_batched_and_paged(H, KVH, D, lens, Ss, block_n, page_size, monkeypatch):
     """The generic kernels in the batched, ragged call (one launch sequence over

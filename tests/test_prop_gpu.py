@@ -194,6 +194,9 @@ def test_prop_fast_generic_pass1(H, KVH, D, L, S, monkeypatch):
     (28, 4, 128, 140000, 512),   # GH 7 at D 128, 2,188 items: santa_flash's GH 8 pass-1 wave kernel, four-wave layout
     (40, 8, 128, 70000, 300),    # GH 5, 2,192 items: the GH 8 wave kernel in its rows layout
     (28, 4, 128, 32700, 512),    # GH 7 below 2,048 items: the generic kernel
+    (64, 4, 128, 70000, 512),    # GH 16: two virtual KV heads of 8 per cache KV head, rows layout
+    (128, 8, 128, 40000, 512),   # GH 16 at 128q/8kv (Llama-3.1-405B's heads): 16 virtual KV heads, four-wave layout
+    (48, 4, 128, 70000, 300),    # GH 12: virtual groups of 6
 ])
 def test_prop_fast_generic_streaming(H, KVH, D, L, S, monkeypatch):
     """The generic pass 1 streaming a chunk of tiles per workgroup (one
