@@ -695,23 +695,70 @@ __global__ __launch_bounds__(kThreads) void pass2_kernel(const uint16_t* __restr
   const int jrow = lane >> 4;
   const int qq = lane & 15;
 
-  // LDS sized by the launch (pass2_lds_bytes): per wave BN listed rows and
-  // their counts, then BN emitted-row flags and the tile's emitted total
+  // LDS sized by the launch (pass2_lds_bytes): per wave and head k (block_n
+  // 256; one list otherwise) BN listed rows and their counts, then BN
+  // emitted-row flags and the tile's emitted total
+  constexpr int NL = T256 ? NK : 1;  // lists per wave
   extern __shared__ int s_p2[];
-  int* const s_lrow = s_p2 + wave * BN;
-  float* const s_lc = reinterpret_cast<float*>(s_p2 + nwv * BN) + wave * BN;
-  int* const s_flag = s_p2 + 2 * nwv * BN;
+  int* const s_lrow = s_p2 + wave * NL * BN;
+  float* const s_lc = reinterpret_cast<float*>(s_p2 + nwv * NL * BN) + wave * NL * BN;
+  int* const s_flag = s_p2 + 2 * nwv * NL * BN;
   int* const s_nemit = s_flag + BN;
 
   static_assert(NK == 1 || NK == 2 || NK == kMaxHeadsPerWave, "heads per wave");
   float acc[NK][DPL];
+  int lcnt[NK];
 #pragma unroll
-  for (int k = 0; k < NK; ++k)
+  for (int k = 0; k < NK; ++k) {
+    lcnt[k] = 0;
 #pragma unroll
     for (int j = 0; j < DPL; ++j) acc[k][j] = 0.0f;
+  }
   int emit_total = 0;
   const uint16_t* ub = u_stash + static_cast<size_t>(b) * L_storage * H;
   const int d0 = DPL * lane;  // this lane's first dim
+
+  // Head k's listed rows, in list order, into its numerator: count-weighted
+  // V rows, one fma per element, in batches of 16 rows whose loads go out
+  // before the first is used, then what is left in batches of 4.  At block_n
+  // 256 a head's list collects the rows of consecutive tiles and is gathered
+  // when the next tile's rows would not fit and at the end of the chunk (the
+  // same ascending (tile, row) fma order as a gather per tile, so the same
+  // bits, with fewer memory round trips); otherwise after every tile.
+  auto flush = [&](int k) {
+    const int n = lcnt[k];
+    int* const lrow = s_lrow + (T256 ? k : 0) * BN;
+    float* const lcw = s_lc + (T256 ? k : 0) * BN;
+    auto gather = [&](auto nb, int i0) {
+      constexpr int NB = decltype(nb)::value;
+      uint16_t vv[NB][DPL];
+      float cf[NB];
+#pragma unroll
+      for (int q = 0; q < NB; ++q) {
+        const int i = min(i0 + q, n - 1);
+        const int row = __builtin_amdgcn_readfirstlane(lrow[i]);
+        cf[q] = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(lcw[i])));
+        if (d0 < D) {
+          load_dims<DPL>(V + row_offset<PAGED>(pt, b, row, kv, KVH, D, L_storage) + d0, vv[q]);
+        } else {
+#pragma unroll
+          for (int j = 0; j < DPL; ++j) vv[q][j] = 0;
+        }
+      }
+#pragma unroll
+      for (int q = 0; q < NB; ++q) {
+        if (i0 + q < n) {
+#pragma unroll
+          for (int j = 0; j < DPL; ++j) acc[k][j] = fmaf(cf[q], h16_to_f32<BF16>(vv[q][j]), acc[k][j]);
+        }
+      }
+    };
+    int i0 = 0;
+    for (; i0 + kGatherRows <= n; i0 += kGatherRows) gather(std::integral_constant<int, kGatherRows>{}, i0);
+    for (; i0 < n; i0 += 4) gather(std::integral_constant<int, 4>{}, i0);
+    lcnt[k] = 0;
+    __builtin_amdgcn_wave_barrier();
+  };
 
   for (int t = t_begin; t < t_end; ++t) {
     const int n0 = t * BN;
@@ -734,7 +781,6 @@ __global__ __launch_bounds__(kThreads) void pass2_kernel(const uint16_t* __restr
           for (int r = lane; r < BN; r += 64) dbg_counts[ht * BN + r] = 0;
         continue;
       }
-      int lc = 0;
       if constexpr (T256) {
         // two rows per lane: rows 32 (4p + j) + 2q (x0) and + 1 (x1) at lane 16j + q
         float x0[2], x1[2];
@@ -759,6 +805,18 @@ __global__ __launch_bounds__(kThreads) void pass2_kernel(const uint16_t* __restr
         int c0[2], c1[2];
         systematic_counts<8>(x0, x1, len, a0, lane, c0, c1);
         const uint64_t below = (1ull << lane) - 1ull;
+        uint64_t nz0[2], nz1[2];
+        int cnt = 0;
+#pragma unroll
+        for (int p = 0; p < 2; ++p) {
+          nz0[p] = __ballot(c0[p] != 0);
+          nz1[p] = __ballot(c1[p] != 0);
+          cnt += __popcll(nz0[p]) + __popcll(nz1[p]);
+        }
+        if (lcnt[k] + cnt > BN) flush(k);
+        int* const lrow = s_lrow + k * BN;
+        float* const lcw = s_lc + k * BN;
+        int lc = lcnt[k];
 #pragma unroll
         for (int p = 0; p < 2; ++p) {
           const int row = 32 * (4 * p + jrow) + 2 * qq;
@@ -766,22 +824,24 @@ __global__ __launch_bounds__(kThreads) void pass2_kernel(const uint16_t* __restr
             dbg_counts[ht * BN + row] = static_cast<int16_t>(c0[p]);
             dbg_counts[ht * BN + row + 1] = static_cast<int16_t>(c1[p]);
           }
-          const uint64_t nz0 = __ballot(c0[p] != 0), nz1 = __ballot(c1[p] != 0);
-          const int pos0 = lc + __popcll(nz0 & below) + __popcll(nz1 & below);
+          const int pos0 = lc + __popcll(nz0[p] & below) + __popcll(nz1[p] & below);
           const int pos1 = pos0 + (c0[p] != 0 ? 1 : 0);
           if (c0[p] != 0) {
-            s_lrow[pos0] = n0 + row;
-            s_lc[pos0] = static_cast<float>(c0[p]);
+            lrow[pos0] = n0 + row;
+            lcw[pos0] = static_cast<float>(c0[p]);
             if (want_emit) s_flag[row] = 1;
           }
           if (c1[p] != 0) {
-            s_lrow[pos1] = n0 + row + 1;
-            s_lc[pos1] = static_cast<float>(c1[p]);
+            lrow[pos1] = n0 + row + 1;
+            lcw[pos1] = static_cast<float>(c1[p]);
             if (want_emit) s_flag[row + 1] = 1;
           }
-          lc += __popcll(nz0) + __popcll(nz1);
+          lc += __popcll(nz0[p]) + __popcll(nz1[p]);
         }
+        lcnt[k] = lc;
+        __builtin_amdgcn_wave_barrier();
       } else {
+        int lc = 0;
         float carry = 0.0f;
         for (int base = 0; base < len; base += 32) {
           const int r = base + lane;
@@ -814,40 +874,10 @@ __global__ __launch_bounds__(kThreads) void pass2_kernel(const uint16_t* __restr
         }
         if (dbg_counts)
           for (int r = ((len + 31) / 32) * 32 + lane; r < BN; r += 64) dbg_counts[ht * BN + r] = 0;
+        __builtin_amdgcn_wave_barrier();
+        lcnt[k] = lc;
+        flush(k);
       }
-      __builtin_amdgcn_wave_barrier();
-      // count-weighted V rows, rows ascending, one fma per element: batches
-      // of 16 rows whose loads go out before the first is used, then what is
-      // left in batches of 4 (a tile lists about S / T_c rows per head, often
-      // fewer than 16)
-      auto gather = [&](auto nb, int i0) {
-        constexpr int NB = decltype(nb)::value;
-        uint16_t vv[NB][DPL];
-        float cf[NB];
-#pragma unroll
-        for (int q = 0; q < NB; ++q) {
-          const int i = min(i0 + q, lc - 1);
-          const int row = __builtin_amdgcn_readfirstlane(s_lrow[i]);
-          cf[q] = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(s_lc[i])));
-          if (d0 < D) {
-            load_dims<DPL>(V + row_offset<PAGED>(pt, b, row, kv, KVH, D, L_storage) + d0, vv[q]);
-          } else {
-#pragma unroll
-            for (int j = 0; j < DPL; ++j) vv[q][j] = 0;
-          }
-        }
-#pragma unroll
-        for (int q = 0; q < NB; ++q) {
-          if (i0 + q < lc) {
-#pragma unroll
-            for (int j = 0; j < DPL; ++j) acc[k][j] = fmaf(cf[q], h16_to_f32<BF16>(vv[q][j]), acc[k][j]);
-          }
-        }
-      };
-      int i0 = 0;
-      for (; i0 + kGatherRows <= lc; i0 += kGatherRows) gather(std::integral_constant<int, kGatherRows>{}, i0);
-      for (; i0 < lc; i0 += 4) gather(std::integral_constant<int, 4>{}, i0);
-      __builtin_amdgcn_wave_barrier();
     }
     if (want_emit) {
       __syncthreads();
@@ -859,6 +889,13 @@ __global__ __launch_bounds__(kThreads) void pass2_kernel(const uint16_t* __restr
       }
       __syncthreads();
       emit_total += *s_nemit;
+    }
+  }
+  if constexpr (T256) {
+#pragma unroll
+    for (int k = 0; k < NK; ++k) {
+      if (wave + nwv * k >= GH) break;
+      flush(k);
     }
   }
 #pragma unroll
@@ -876,11 +913,13 @@ __global__ __launch_bounds__(kThreads) void pass2_kernel(const uint16_t* __restr
 // Waves per pass-2 workgroup: one per head up to four.
 int pass2_waves(int GH) { return GH < 4 ? GH : 4; }
 
-// Pass 2's dynamic LDS: per wave BN row indices and BN counts, then BN flags
-// and one total.
-static size_t pass2_lds_bytes(int nw, int BN) {
-  return (static_cast<size_t>(2 * nw + 1) * BN + 1) * sizeof(int);
+// Pass 2's dynamic LDS: per wave and list (one per head it holds at block_n
+// 256, one otherwise) BN row indices and BN counts, then BN flags and one
+// total.
+static size_t pass2_lds_bytes(int nw, int BN, int lists) {
+  return (static_cast<size_t>(2 * nw * lists + 1) * BN + 1) * sizeof(int);
 }
+static int pass2_heads_per_wave(int GH) { return GH <= 4 ? 1 : (GH <= 8 ? 2 : kMaxHeadsPerWave); }
 
 static int pass2_dpl(int D) { return D <= 64 ? 1 : (D <= 128 ? 2 : (D <= 256 ? 4 : (D <= 512 ? 8 : 16))); }
 
@@ -921,8 +960,9 @@ static int pass2_blocks_per_cu_dpl(int dpl, int threads, size_t lds) {
 }
 
 // Pass-2 workgroups resident on the current device at once for this shape,
-// from the compiled kernel's registers and the LDS of a block_n = 512 launch
-// (the most any block_n takes); 0 where the runtime cannot say (no device).
+// from the compiled kernel's registers and the most LDS a launch takes (one
+// list at block_n 512, or a list per head at block_n 256); 0 where the runtime
+// cannot say (no device).
 // Cached per (device, D class, waves per workgroup and heads per wave).
 int pass2_resident(int GH, int D) {
   constexpr int kMaxDev = 64;
@@ -947,7 +987,7 @@ int pass2_resident(int GH, int D) {
     return 0;
   }
   const int threads = 64 * nw;
-  const size_t lds = pass2_lds_bytes(nw, kMaxBN);
+  const size_t lds = std::max(pass2_lds_bytes(nw, kMaxBN, 1), pass2_lds_bytes(nw, 256, pass2_heads_per_wave(GH)));
   const int per_cu = GH <= 4 ? pass2_blocks_per_cu_dpl<1>(dpl, threads, lds)
                              : (GH <= 8 ? pass2_blocks_per_cu_dpl<2>(dpl, threads, lds)
                                         : pass2_blocks_per_cu_dpl<kMaxHeadsPerWave>(dpl, threads, lds));
@@ -1114,7 +1154,7 @@ hipError_t launch_pass2(const void* V, const uint16_t* u_stash, int dtype, int B
   const int nw = pass2_waves(H / KVH);
   const unsigned threads = static_cast<unsigned>(64 * nw);
   const int dpl = pass2_dpl(D);
-  const size_t lds = pass2_lds_bytes(nw, BN);
+  const size_t lds = pass2_lds_bytes(nw, BN, BN == 256 ? pass2_heads_per_wave(H / KVH) : 1);
 #define SANTA_GP2_K(BF, PG, DP, T2, NK)                                                                              \
   hipLaunchKernelGGL((pass2_kernel<BF, PG, DP, T2, NK>), dim3(static_cast<unsigned>(grid)), dim3(threads), lds,      \
                      stream, Vh, u_stash, H, KVH, D, BN, L, L_storage, T_c, cs, cpg, invdelta, a0, counts, part,     \
