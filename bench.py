@@ -81,7 +81,7 @@ def parse_args():
     ap.add_argument("--copy-calibration-mib", type=int, default=0,
                     help="first run a plain device copy of this many MiB 5 times (a known-size kernel "
                          "that calibrates rocprofv3 FETCH_SIZE / WRITE_SIZE)")
-    ap.add_argument("--extra-workloads", default="cfg3,cfg5,cfg5p,propgen",
+    ap.add_argument("--extra-workloads", default="cfg3,cfg5,cfg5p,propgen,propgen_gqa7,propgen_gqa16",
                     help="with the headline workload (cfg2, contiguous): after its own timing, also time these "
                          "workloads (20 steps each, 2 step windows) and report them under `extra_workloads` in the "
                          "same JSON line; '' for none")
@@ -638,13 +638,18 @@ def extra_workloads(args, dev):
     import copy
     import torch
 
-    runners = {"cfg3": run_cfg3, "cfg5": run_cfg5, "cfg5p": run_cfg5p, "propgen": run_propgen}
+    runners = {"cfg3": run_cfg3, "cfg5": run_cfg5, "cfg5p": run_cfg5p, "propgen": run_propgen,
+               "propgen_gqa7": run_propgen, "propgen_gqa16": run_propgen}
+    # santa_prop shapes outside the tuned kernels: MHA, Qwen2.5-7B's 28q/4kv
+    # and Llama-3.1-405B's 128q/8kv (d = 128, B = 8, 32k tokens)
+    heads = {"propgen_gqa7": (28, 4), "propgen_gqa16": (128, 8)}
     out = []
     for name in [w.strip() for w in args.extra_workloads.split(",") if w.strip()]:
         sub = copy.copy(args)
         sub.steps, sub.warmup, sub.warmup_ms, sub.windows = 20, 2, 200.0, 2
         sub.no_cpu_baseline, sub.page_size, sub.copy_calibration_mib = True, 0, 0
         sub.batch, sub.ctx, sub.heads, sub.kv_heads, sub.head_dim = 8, 32768, 32, 32, 128
+        sub.heads, sub.kv_heads = heads.get(name, (sub.heads, sub.kv_heads))
         print(f"[bench] extra workload {name}", file=sys.stderr, flush=True)
         try:
             if name not in runners:
