@@ -222,6 +222,18 @@ def test_prop_head_dim_above_256(H, KVH, D, L, S, block_n, monkeypatch):
     assert exp["pass1_mode"] == 1
 
 
+@pytest.mark.parametrize("H,KVH,L,S", [(28, 4, 140000, 512), (64, 4, 70000, 300)])
+def test_prop_gh8_route_f16(H, KVH, L, S, monkeypatch):
+    """f16 through santa_flash's GH 8 pass-1 wave kernel on santa_prop's
+    generic shapes (GH 7 with each group's eighth head zero; GH 16 over two
+    virtual KV heads per cache KV head), above the 2,048-item threshold: every
+    stage bit-exact to the oracle, the fused decode equal to the stages."""
+    _announce(f"prop GH 8 route f16 H={H} KVH={KVH} L={L} S={S} bn=256")
+    q, K, V = _general_inputs(H, KVH, 128, L, SEED + 17 + H, dtype=torch.float16)
+    exp = _check(q, K, V, S, SEED, block_n=256, is_bf16=False, monkeypatch=monkeypatch)
+    assert exp["pass1_mode"] == 1
+
+
 def test_prop_fast_generic_f16(monkeypatch):
     _announce("prop fast generic pass 1 f16 H=16 KVH=8 D=64 L=3300 S=90 bn=256")
     q, K, V = _general_inputs(16, 8, 64, 3300, SEED + 9, dtype=torch.float16)
