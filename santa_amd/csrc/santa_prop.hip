@@ -879,18 +879,19 @@ static int prop_budgets_launch(const float* m_tiles, const float* ell_tiles, int
   }
   // waves per (b, h) and registers per thread for every tile of the longest
   // sequence (T_c <= kMaxTiles): two registers a thread, up to 16 waves
-  // (up to 128 tiles one per thread: B = 1 at 32k tokens 42.4 -> 40.7 us per
-  // step, MHA at B = 8 419.4 -> 417.8 us; at 512 tiles two per thread stay
-  // ahead on cfg5p)
+  // (up to 256 tiles one per thread: B = 1 at 32k tokens 42.4 -> 40.7 us per
+  // step, at 64k 51.6 -> 49.9 us; MHA at B = 8 419.4 -> 417.8 us; at 512
+  // tiles two per thread stay ahead on cfg5p)
   int N = 1;
   while (N < T_c) N <<= 1;
-  const int NW = N <= 128 ? std::max(1, N / 64) : std::min(16, N / 128);
+  const int NW = N <= 256 ? std::max(1, N / 64) : std::min(16, N / 128);
   const int R = std::max(1, N / (64 * NW));
 #define SANTA_BUDGETS(W, RR)                                                                                      \
   hipLaunchKernelGGL((prop::budgets_kernel<W, RR>), dim3(BH), dim3(64 * W), 0, stream, m_tiles, ell_tiles, H, T_c, \
                      S, seed, m_star, S_tiles, invdelta, a0, seq_lens, seq_S, block_n)
   if (NW == 1 && R == 1) SANTA_BUDGETS(1, 1);
   else if (NW == 2 && R == 1) SANTA_BUDGETS(2, 1);
+  else if (NW == 4 && R == 1) SANTA_BUDGETS(4, 1);
   else if (NW == 1 && R == 2) SANTA_BUDGETS(1, 2);
   else if (NW == 2 && R == 2) SANTA_BUDGETS(2, 2);
   else if (NW == 4 && R == 2) SANTA_BUDGETS(4, 2);
