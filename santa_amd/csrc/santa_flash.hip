@@ -2074,13 +2074,29 @@ static int resident_workgroups() {
 
 // Chunking of each group's T_c tiles so that B*KVH*cpg is about one resident
 // round of per_round items (0: resident_workgroups(), one 4-wave workgroup
-// per item): cpg chunks of cs tiles (the last may be shorter).
+// per item): cpg chunks of cs tiles (the last may be shorter).  The chunk
+// count per group is rounded to the nearest, unless that puts more than one
+// round of items in the grid; then it is the count that fits one round.  The
+// few items of a second round would each walk a whole chunk after the rest:
+// in the flash rows layout (one workgroup per CU) B = 6, 10, 20, 24, ... at
+// 32k tokens had planned 258-264 workgroups, and one round took B = 6 from
+// 116.7 to 85.6 us per step, B = 10 194.1 -> 123.4, B = 20 341.1 -> 224.7,
+// B = 24 380.7 -> 262.1 (GH 8: B = 6 191.7 -> 129.2, B = 10 295.1 -> 187.2).
+// Chunks whose lengths differ by one tile, so that every CU holds one,
+// measured slower (B = 6 at 32k 92.7 us; B = 4 at T_c = 129, 43 chunks of
+// three tiles, 71.8 against 66.8 us): the pass is bandwidth-bound there, and
+// the longer chunks run on alone after the others.
 static void chunk_plan(int B, int KVH, int T_c, int* cs, int* cpg, int per_round = 0) {
   const long long groups = static_cast<long long>(B) * KVH;
-  long long want = ((per_round > 0 ? per_round : resident_workgroups()) + groups / 2) / groups;
+  const long long round = per_round > 0 ? per_round : resident_workgroups();
+  long long want = (round + groups / 2) / groups;
   if (want < 1) want = 1;
   if (want > T_c) want = T_c;
-  const int c = static_cast<int>((T_c + want - 1) / want);
+  int c = static_cast<int>((T_c + want - 1) / want);
+  if (groups * ((T_c + c - 1) / c) > round && round / groups >= 1) {
+    want = round / groups;  // one round
+    c = static_cast<int>((T_c + want - 1) / want);
+  }
   *cs = c;
   *cpg = (T_c + c - 1) / c;
 }

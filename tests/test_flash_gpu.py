@@ -368,6 +368,39 @@ def test_cfg4_attention_shape_parity(valid_len):
     assert ok, ("vs oracle", mabs, mrel)
 
 
+@pytest.mark.parametrize("B,H,L,dtype", [(6, 32, 32768, torch.bfloat16), (6, 64, 33000, torch.bfloat16),
+                                          (10, 32, 32768, torch.float16)])
+def test_rows_plan_one_round_parity(B, H, L, dtype):
+    """Uniform batches whose chunks rounded to the nearest count would spill
+    past one round of workgroups run the rows layout's one-round plan (on 256
+    CUs: B=6 at 128 tiles in 32 chunks of 4 tiles, B=6 at 129 in 33, B=10 at
+    128 in 22 chunks of 6).
+    The production wave kernel's tile max, tile mass and counts bit-exact to
+    the oracle, m* and vrows exact, the output within the 16-bit tolerance."""
+    KVH, S = 8, 512
+    m = _mod()
+    T_c = (L + 255) // 256
+    assert "wave_kernel" in m._tile_pass_kernel(B, H, KVH, T_c, 256)
+    _announce(f"rows plan, one round B={B} H={H} KVH={KVH} L={L} S={S} dtype={dtype}")
+    q, K, V = gen_qkv(B, H, KVH, L, seed=SEED + 7 * B, lowrank=0.5, dtype=dtype)
+    dev = torch.device("cuda:0")
+    qd, Kd, Vd = q.to(dev), K.to(dev), V.to(dev)
+    mt, lt, cnt = m._debug_wave(qd, Kd, Vd, S, seed=SEED)
+    out, ms, vr = m.decode_systematic_batched(qd, Kd, Vd, S, seed=SEED, want_vrows=True)
+    torch.cuda.synchronize()
+    is_bf16 = dtype == torch.bfloat16
+    exp = oracle.flash_decode(q, K, V, S, seed=SEED, is_bf16=is_bf16, debug=True)
+    np.testing.assert_array_equal(mt.cpu().numpy().view(np.uint32), exp["m_tiles"].view(np.uint32), err_msg="m_tiles")
+    np.testing.assert_array_equal(lt.cpu().numpy().view(np.uint32), exp["ell_tiles"].view(np.uint32),
+                                  err_msg="ell_tiles")
+    c_gpu = cnt.cpu().numpy()
+    assert np.array_equal(c_gpu, exp["counts"]), f"counts differ at {np.argwhere(c_gpu != exp['counts'])[:8]}"
+    np.testing.assert_array_equal(ms.cpu().numpy().view(np.uint32), exp["m_star"].view(np.uint32), err_msg="m_star")
+    np.testing.assert_array_equal(vr.cpu().numpy(), exp["vrows"], err_msg="vrows")
+    ok, mabs, mrel = tol_check(h16_to_f32(bits16(out), is_bf16), h16_to_f32(exp["out16"], is_bf16))
+    assert ok, ("vs oracle", mabs, mrel)
+
+
 @pytest.mark.parametrize("B,L", [(3, 32768), (2, 32800)])
 def test_uniform_small_pass_range_parity(B, L):
     """Uniform calls of 2,049 to 3,072 (kv, tile) items run their block_n =
