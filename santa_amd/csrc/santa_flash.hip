@@ -2300,14 +2300,14 @@ bool uniform_small_pass(int B, int KVH, int T_c, int GH) {
   return items <= (GH == 8 ? gh8_small_items() : static_cast<long long>(rows_per_round()) * 3 / 2);
 }
 
-// Ragged batches: chunks small enough for about eight resident rounds over
+// Ragged batches: chunks small enough for about `rounds` resident rounds over
 // all (kv, tile) items, so the hardware's workgroup dispatch evens out the
 // uneven chunks (each sequence adds at most one partial chunk per KV head;
 // B * KVH slots of each round are counted for those).  Eight rounds measured
 // best for santa_prop on 16 sequences of 8k-128k tokens (one round: 824 us,
 // four: 795, eight: 745, sixteen: 750).
 void plan_ragged(int B, int KVH, long long total_tiles, int max_tiles, int* cs, int* n_wg, int per_round,
-                 int granule) {
+                 int granule, int rounds) {
   if (max_tiles > 0 && total_tiles == static_cast<long long>(B) * max_tiles) {
     // every sequence has the same tile count: the uniform plan (one resident
     // round), whose workgroups the ragged grid enumerates in the same order
@@ -2322,7 +2322,7 @@ void plan_ragged(int B, int KVH, long long total_tiles, int max_tiles, int* cs, 
   const long long items = total_tiles * KVH;
   const long long resident = per_round > 0 ? per_round : resident_workgroups();
   const long long slack = static_cast<long long>(B) * KVH;
-  const long long want = 8 * ((resident > 2 * slack) ? resident - slack : (resident + 1) / 2);
+  const long long want = rounds * ((resident > 2 * slack) ? resident - slack : (resident + 1) / 2);
   long long c = (items + want - 1) / want;
   c = (c + granule - 1) / granule * granule;
   *cs = static_cast<int>(c);
@@ -2594,8 +2594,19 @@ struct RaggedWs {
 RaggedWs ragged_ws_layout(int B, int H, int KVH, long long total_tiles, int max_tiles, bool small = false) {
   RaggedWs w{};
   const bool rows = flash::rows_layout(KVH) && !small;
+  // The rows layout takes one round where the sequences' partial chunks
+  // (B * KVH items at most) hold no more than an eighth of it (B <= 32 at KVH
+  // 8), eight otherwise.  Each chunk costs its workgroup a start and an end
+  // (first K after about 8 us, the V gathers and partial write after the
+  // loop), which eight rounds of two- or three-tile chunks pay several times
+  // per CU.  One round, against eight: cfg3's 16 lengths (8k-128k) 441.6 ->
+  // 384.5 us per step, B = 8 at 16k-64k 172.3 -> 116.2, B = 4 at 32k-128k
+  // 240.4 -> 131.8, B = 2 at 64k-128k 173.7 -> 89.4, B = 32 at 8k-32k 285.3
+  // -> 247.4; but B = 12 at 1k-128k 325.2 -> 353.6, and at B = 40, 48 and 64
+  // (a quarter of the round and more in partial chunks) 3-10 % slower.
+  const int rounds = (rows && 8LL * B * KVH <= flash::rows_per_round()) ? 1 : 8;
   flash::plan_ragged(B, KVH, total_tiles, max_tiles, &w.cs, &w.n_wg, rows ? flash::rows_per_round() : 0,
-                     rows ? 1 : 4);
+                     rows ? 1 : 4, rounds);
   const size_t chunks = static_cast<size_t>(w.n_wg);
   size_t off = 0;
   w.part = off;

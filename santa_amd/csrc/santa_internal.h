@@ -52,9 +52,10 @@ hipError_t launch_prop_pass1(const void* q, const void* K, int dtype, int B, int
 // having max_tiles: cs tiles per chunk and an upper bound n_wg on the
 // workgroups of the ragged grid.
 // per_round: work items per resident round (0: one per 4-wave workgroup
-// slot); granule: cs is a multiple of it for uneven lengths.
+// slot); granule: cs is a multiple of it for uneven lengths; rounds: about
+// how many resident rounds the chunks of uneven lengths make.
 void plan_ragged(int B, int KVH, long long total_tiles, int max_tiles, int* cs, int* n_wg, int per_round = 0,
-                 int granule = 4);
+                 int granule = 4, int rounds = 8);
 // The flash tile pass's layout: one wave per KV head (ROWS) for KVH = 8, its
 // chunks planned for rows_per_round() items per round.
 bool rows_layout(int KVH);
