@@ -2603,7 +2603,13 @@ RaggedWs ragged_ws_layout(int B, int H, int KVH, long long total_tiles, int max_
   // 384.5 us per step, B = 8 at 16k-64k 172.3 -> 116.2, B = 4 at 32k-128k
   // 240.4 -> 131.8, B = 2 at 64k-128k 173.7 -> 89.4, B = 32 at 8k-32k 285.3
   // -> 247.4; but B = 12 at 1k-128k 325.2 -> 353.6, and at B = 40, 48 and 64
-  // (a quarter of the round and more in partial chunks) 3-10 % slower.
+  // (a quarter of the round and more in partial chunks) 3-10 % slower.  The
+  // loss at B = 12 (GH 8: 450.1 -> 589.6 us) is a sequence shorter than one
+  // chunk (4 tiles against 12): it is one chunk, and S_per_tile = S / 4 puts
+  // all its S samples per head, S * GH row gathers per wave in dependent
+  // batches of 16, on one CU, where eight rounds split it in two.  The host
+  // does not know the shortest length (the call carries total_tiles and
+  // max_len), so the rule stands on the batches measured above.
   const int rounds = (rows && 8LL * B * KVH <= flash::rows_per_round()) ? 1 : 8;
   flash::plan_ragged(B, KVH, total_tiles, max_tiles, &w.cs, &w.n_wg, rows ? flash::rows_per_round() : 0,
                      rows ? 1 : 4, rounds);
