@@ -57,7 +57,8 @@ def parse_args():
     ap.add_argument("--S", type=int, default=256)
     ap.add_argument("--seed", type=int, default=1690)
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--workload", choices=("cfg2", "cfg3", "cfg4", "cfg5", "cfg5p", "single", "propgen"),
+    ap.add_argument("--workload", choices=("cfg2", "cfg3", "cfg4", "cfg5", "cfg5p", "single", "propgen",
+                                           "flashragged"),
                     default="cfg2",
                     help="cfg2: the headline (flash, B=8, 32k); cfg3: batched ragged santa_prop (B=16, "
                          "L_b in [8192, 131072], S_b = L_b // 64); cfg4: model-level decode, random-init "
@@ -66,7 +67,8 @@ def parse_args():
                          "S=512 per sequence; single: one sequence of --ctx tokens through santa_flash (S=256) "
                          "and santa_prop (S=L/64); propgen: santa_prop on a shape outside the tuned kernels "
                          "(--heads/--kv-heads/--head-dim, default MHA 32q/32kv d=128), B=--batch, --ctx tokens, "
-                         "S = L // 64 per sequence")
+                         "S = L // 64 per sequence; flashragged: santa_flash on cfg3's lengths (B=16, "
+                         "--heads query heads over 8 KV heads, one S = --S for the batch)")
     ap.add_argument("--heads", type=int, default=32, help="propgen: query heads")
     ap.add_argument("--kv-heads", type=int, default=32, help="propgen: KV heads")
     ap.add_argument("--head-dim", type=int, default=128, help="propgen: head_dim")
@@ -441,6 +443,37 @@ def run_cfg3(args, dev):
     return line
 
 
+def run_flashragged(args, dev):
+    """Ragged santa_flash on cfg3's seeded lengths: B=16 sequences, L_b ~
+    U[8192, 131072], one S for the batch (--S; S_per_tile from
+    each sequence's tile count), --heads query heads over 8 KV heads, one
+    decode_systematic_batched call per step."""
+    import torch
+    import santa_flash_batch_cuda as flash
+
+    B, H, KVH, D, S, seed = 16, args.heads, 8, 128, args.S, args.seed
+    gl = torch.Generator().manual_seed(seed)
+    lens = torch.randint(8192, 131072 + 1, (B,), generator=gl).tolist()
+    L = max(lens)
+    q, K, V = device_inputs(B, L, H, KVH, D, seed, dev)
+    torch.cuda.synchronize()
+
+    def step(want_vrows=False):
+        return flash.decode_systematic_batched(q, K, V, S, seed=seed, want_vrows=want_vrows, valid_len=lens)
+    _, _, vrows = step(True)
+    v_rows = int(vrows.sum().item())
+    tm = Timing(args).run(step)
+    line = base_line("sampled-attn decode µs/step + achieved HBM TB/s; tokens/s (ragged santa_flash on cfg3's "
+                     "lengths)", B, tm, args)
+    line["config"] = {"workload": f"santa_flash batched ragged decode, {H}q/{KVH}kv, d=128, B={B}, L_b seeded "
+                                  f"U[8192, 131072] (sum {sum(lens)}), S={S}, seed {seed}, K/V ~ N(0,1) + rank-4 key "
+                                  "bias 0.5", "global_batch": B, "seq_len": lens, "S": S, "parallelism": "single GPU"}
+    line["roofline"] = roofline(flash_bytes(lens, KVH, H, B, v_rows), tm, "whole flash step (tile pass + merge)",
+                                None, v_rows)
+    line.update(timing_keys(tm))
+    return line
+
+
 def run_cfg5(args, dev):
     """Flash stress: B=32, 64q/8kv (GH 8), L=131072, S=512, Student-t(3) keys with
     planted needles."""
@@ -685,7 +718,7 @@ def main():
             line["extra_workloads"] = extra_workloads(args, dev)
     else:
         line = {"cfg3": run_cfg3, "cfg4": run_cfg4, "cfg5": run_cfg5, "cfg5p": run_cfg5p,
-                "single": run_single, "propgen": run_propgen}[args.workload](args, dev)
+                "single": run_single, "propgen": run_propgen, "flashragged": run_flashragged}[args.workload](args, dev)
     print(json.dumps(line))
     return 0
 
