@@ -2196,7 +2196,14 @@ hipError_t launch_prop_pass1(const void* q, const void* K, int dtype, int B, int
     const bool rows = rows_layout(a.KVH) && (!a.seq_lens || total_tiles >= 0);
     if (rows) {
       if (a.seq_lens) {
-        plan_ragged(a.B, a.KVH, total_tiles, a.T_c, &a.cs, &a.n_wg, rows_per_round(), 1);
+        // one round of chunks up to 32 sequences (B * KVH at most an eighth
+        // of the round), as flash's ragged plan: B = 8 at 16k-64k 172.4 ->
+        // 149.7 us per step, B = 4 at 32k-128k 206.6 -> 182.7, B = 12 at
+        // 1k-128k 362.8 -> 351.3, cfg3 516.8 -> 514.4 (the same bits); pass 1
+        // gathers nothing, so a short sequence's chunk is no heavier than
+        // its tiles
+        plan_ragged(a.B, a.KVH, total_tiles, a.T_c, &a.cs, &a.n_wg, rows_per_round(), 1,
+                    (8LL * a.B * a.KVH <= rows_per_round()) ? 1 : 8);
       } else {
         chunk_plan(a.B, a.KVH, a.T_c, &a.cs, &a.cpg, rows_per_round());
       }
