@@ -83,7 +83,7 @@ def parse_args():
     ap.add_argument("--copy-calibration-mib", type=int, default=0,
                     help="first run a plain device copy of this many MiB 5 times (a known-size kernel "
                          "that calibrates rocprofv3 FETCH_SIZE / WRITE_SIZE)")
-    ap.add_argument("--extra-workloads", default="cfg3,cfg5,cfg5p,propgen,propgen_gqa7,propgen_gqa16",
+    ap.add_argument("--extra-workloads", default="cfg3,cfg5,cfg5p,propgen,propgen_gqa7,propgen_gqa16,flashragged",
                     help="with the headline workload (cfg2, contiguous): after its own timing, also time these "
                          "workloads (20 steps each, 2 step windows) and report them under `extra_workloads` in the "
                          "same JSON line; '' for none")
@@ -672,10 +672,11 @@ def extra_workloads(args, dev):
     import torch
 
     runners = {"cfg3": run_cfg3, "cfg5": run_cfg5, "cfg5p": run_cfg5p, "propgen": run_propgen,
-               "propgen_gqa7": run_propgen, "propgen_gqa16": run_propgen}
+               "propgen_gqa7": run_propgen, "propgen_gqa16": run_propgen, "flashragged": run_flashragged}
     # santa_prop shapes outside the tuned kernels: MHA, Qwen2.5-7B's 28q/4kv
-    # and Llama-3.1-405B's 128q/8kv (d = 128, B = 8, 32k tokens)
-    heads = {"propgen_gqa7": (28, 4), "propgen_gqa16": (128, 8)}
+    # and Llama-3.1-405B's 128q/8kv (d = 128, B = 8, 32k tokens); santa_flash
+    # on cfg3's ragged lengths at 32q/8kv with S = 512
+    heads = {"propgen_gqa7": (28, 4), "propgen_gqa16": (128, 8), "flashragged": (32, 8)}
     out = []
     for name in [w.strip() for w in args.extra_workloads.split(",") if w.strip()]:
         sub = copy.copy(args)
@@ -683,6 +684,8 @@ def extra_workloads(args, dev):
         sub.no_cpu_baseline, sub.page_size, sub.copy_calibration_mib = True, 0, 0
         sub.batch, sub.ctx, sub.heads, sub.kv_heads, sub.head_dim = 8, 32768, 32, 32, 128
         sub.heads, sub.kv_heads = heads.get(name, (sub.heads, sub.kv_heads))
+        if name == "flashragged":
+            sub.S = 512
         print(f"[bench] extra workload {name}", file=sys.stderr, flush=True)
         try:
             if name not in runners:
